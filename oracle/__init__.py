@@ -1,0 +1,133 @@
+"""TEST INFRASTRUCTURE ONLY: the float64 CPU oracle of the G1 control step (``g1_oracle.cpp``).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import this package, and only
+as the checker. The product path (``nablaengine_amd``) never imports it.
+
+Parity status of each function (how it is pinned; the tests that pin it are named):
+- ``step``: pinned end to end against MuJoCo C float64 truth (``benchmarks/data/truth/mf_s*.npz`` ``check_out``, 64
+  states per corpus, 4 corpora: committed as ``tests/golden/truth_check_*.npz``) in ``tests/test_oracle.py``.
+- ``smooth``: M against closed forms (symmetry, positive definiteness, kinetic energy ``0.5 v' M v`` against the sum of
+  the bodies' kinetic energies, gravity torque against the finite difference of potential energy) in
+  ``tests/test_oracle.py``.
+- ``contacts``: pinned by the step truth and by closed forms (sphere-plane depth, segment distance).
+- ``integrate_pos``, ``qpos_tangent``: closed forms (quaternion norm, round trip) in ``tests/test_oracle.py``.
+"""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle_g1.so")
+NQ, NV, NU, NB = 36, 35, 29, 31
+
+_lib = None
+
+
+def build():
+    """Compile the oracle (g++ on g1_oracle.cpp; the Makefile next to this file)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = ctypes.CDLL(LIB)
+        dp = ctypes.POINTER(ctypes.c_double)
+        ip = ctypes.POINTER(ctypes.c_int)
+        L.g1o_step.argtypes = [ctypes.c_int, dp, dp, dp, dp, dp, dp, ctypes.c_int, ctypes.c_double, ctypes.c_int,
+                               ctypes.c_double, ctypes.c_int, dp, dp, dp, ip]
+        L.g1o_smooth.argtypes = [dp] * 9
+        L.g1o_contacts.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
+
+
+def _c(a, shape):
+    return np.ascontiguousarray(np.asarray(a, np.float64).reshape(shape))
+
+
+# the engine's settings (iterations 10, the model's tolerance 1e-8, line search 40 / 1e-7) and MuJoCo C's truth
+# settings (benchmarks/data/truth/README.md: 2000 iterations, tolerance 1e-13, 100 line-search steps)
+ENGINE = dict(iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7)
+TRUTH = dict(iterations=2000, tol=1e-13, ls_max=100, ls_tol=1e-12)
+
+
+def step(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4):
+    """One control step of B worlds in float64: (qpos' (B, 36), qvel' (B, 35), warm' (B, 35), info (B, 4) int32)."""
+    qpos = _c(qpos, (-1, NQ))
+    B = qpos.shape[0]
+    qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
+    friction, com = _c(friction, (B,)), _c(com, (B, 3))
+    oq, ov, ow = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NV))
+    info = np.empty((B, 4), np.int32)
+    lib().g1o_step(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
+                   int(ls_max), float(ls_tol), int(nsub), _p(oq), _p(ov), _p(ow),
+                   info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    return oq, ov, ow, info
+
+
+def smooth(qpos, qvel, ctrl, com):
+    """Smooth dynamics of one state: M (35, 35), qfrc_smooth, qacc_smooth, xpos (31, 3), xquat (31, 4)."""
+    M, qsm, qa = np.empty((NV, NV)), np.empty(NV), np.empty(NV)
+    xp, xq = np.empty((NB, 3)), np.empty((NB, 4))
+    lib().g1o_smooth(_p(_c(qpos, NQ)), _p(_c(qvel, NV)), _p(_c(ctrl, NU)), _p(_c(com, 3)), _p(M), _p(qsm), _p(qa),
+                     _p(xp), _p(xq))
+    return M, qsm, qa, xp, xq
+
+
+def contacts(qpos, qvel, ctrl, com, friction):
+    """Contacts of one state at its input pose: (n, 15) rows (pair, slot, dist, pos[3], frame[9])."""
+    out = np.empty((64, 15))
+    n = lib().g1o_contacts(_p(_c(qpos, NQ)), _p(_c(qvel, NV)), _p(_c(ctrl, NU)), _p(_c(com, 3)), float(friction),
+                           _p(out))
+    return out[:n].copy()
+
+
+def quat_mul(a, b):
+    w1, x1, y1, z1 = np.moveaxis(a, -1, 0)
+    w2, x2, y2, z2 = np.moveaxis(b, -1, 0)
+    return np.stack([w1 * w2 - x1 * x2 - y1 * y2 - z1 * z2, w1 * x2 + x1 * w2 + y1 * z2 - z1 * y2,
+                     w1 * y2 - x1 * z2 + y1 * w2 + z1 * x2, w1 * z2 + x1 * y2 - y1 * x2 + z1 * w2], -1)
+
+
+def integrate_pos(qpos, dq, scale=1.0):
+    """MuJoCo's mj_integratePos for the G1 (free root, then hinges): qpos (.., 36) moved by the tangent dq (.., 35)
+    times scale; the root quaternion is rotated by the local rotation vector dq[3:6] scale (reference/jax64.py:686-698,
+    the convention of fdlib.py's FD columns)."""
+    qpos = np.array(qpos, np.float64, copy=True)
+    dq = np.asarray(dq, np.float64) * scale
+    qpos[..., :3] += dq[..., :3]
+    w = dq[..., 3:6]
+    ang = np.linalg.norm(w, axis=-1, keepdims=True)
+    safe = np.where(ang > 0, ang, 1.0)
+    dqq = np.concatenate([np.cos(0.5 * ang), np.sin(0.5 * ang) * w / safe], -1)
+    q = quat_mul(qpos[..., 3:7], dqq)
+    qpos[..., 3:7] = q / np.linalg.norm(q, axis=-1, keepdims=True)
+    qpos[..., 7:] += dq[..., 6:]
+    return qpos
+
+
+def qpos_tangent(qpos, g_qpos):
+    """A qpos-form cotangent (.., 36) as a tangent-space cotangent (.., 35): the transpose of the map dq -> d qpos of
+    integrate_pos at dq = 0 (reference/adjoint_groups.py:218-226 qpos_tangent): root position as is, the root
+    quaternion's cotangent through d quat / d w = 0.5 quat * (0, w), hinges as is."""
+    qpos, g = np.asarray(qpos, np.float64), np.asarray(g_qpos, np.float64)
+    out = np.zeros(g.shape[:-1] + (NV,))
+    out[..., :3] = g[..., :3]
+    out[..., 6:] = g[..., 7:]
+    q = qpos[..., 3:7]
+    for k in range(3):
+        e = np.zeros(4)
+        e[1 + k] = 1.0
+        dqk = 0.5 * quat_mul(q, np.broadcast_to(e, q.shape))
+        out[..., 3 + k] = np.sum(g[..., 3:7] * dqk, -1)
+    return out
