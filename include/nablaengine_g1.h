@@ -1,0 +1,55 @@
+/* C ABI of the MI355X G1 control-step library (libnablaengine_g1.so): the entry points the reference's FFI binds
+ * (ctypes in src/nablaengine/torch_ffi.py:333-366 _bind, XLA FFI in src/nablaengine/jax_ffi.py:486-797), with
+ * cudaStream_t -> hipStream_t. Plain pointers and sizes: float32 arrays world-major and row-contiguous, int32 info.
+ * Every entry returns 0 on success, else a hipError_t (or -1: the device cannot take the launch); nothing is
+ * allocated per call (the caller owns every output, the tape and the work buffer); launches go on the given stream. */
+#ifndef NABLAENGINE_G1_H
+#define NABLAENGINE_G1_H
+#include <hip/hip_runtime_api.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces <fwd>_forward (jax_ffi.py:266-278, FWD_SHIM): one control step of nsub substeps for nw worlds.
+ * in: qpos (nw, 36), qvel (nw, 35), warm (nw, 35) Newton warm start, ctrl (nw, 29), fric (nw,), com (nw, 3);
+ * out: oq (nw, 36), ov (nw, 35), ow (nw, 35) = the last substep's qacc, info (nw, 4) = (Newton iterations of the last
+ * substep, contacts found, constraint rows, flags: 4 contacts beyond 64 dropped, 16 rows beyond 192 dropped);
+ * ocon (nw, 64, 8) or NULL: the last substep's contacts (pair, dist, pos[3], normal[3]; pair -1 past the count);
+ * tape (nw, nsub * DK_REC_WORDS) or NULL: the adjoint's record; work: dk_fwd_work_bytes(nw) bytes or NULL when 0. */
+int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
+                   const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
+                   int* info, float* ocon, float* tape, void* work);
+/* Replaces <fwd>_work_bytes (jax_ffi.py:265): scratch bytes the forward needs for nw worlds (0: none). */
+long long dk_fwd_work_bytes(int nw);
+/* Replaces <unit>_upload (jax_ffi.py:214-225): the model constants are compiled into this library, so the call only
+ * checks that the current device can run the kernels; consts may be NULL. */
+int dk_fwd_upload(const float* consts, hipStream_t st);
+/* Replaces <unit>_sizes (jax_ffi.py:255-258): o[0..8] = LDS bytes of the forward, of the adjoint, tape words per
+ * world and substep, nq, nv, max contacts, clamp_kv, normal, the tape's flags word offset (o[6], o[7] -1: runtime). */
+void dk_fwd_sizes(long long* o);
+
+/* Replaces <variant>_adjoint (jax_ffi.py:228-241) for every (clamp_kv, normal) variant at once: the VJP of one control
+ * step from its tape. in: tape (nw, nsub * DK_REC_WORDS), fric, com as the forward's, gq_out (nw, 36), gv_out (nw, 35)
+ * the output cotangents, ctrl (nw, 29) (clamp_kv 2 only, else may be NULL), clamp_soft (clamp_kv 2); out: gq_in (nw, 36)
+ * qpos-form, gv_in (nw, 35), gctrl (nw, 29), info (nw,) flags. */
+int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+               const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+               const float* ctrl, float clamp_soft, int clamp_kv, int normal);
+
+/* The reference's per-variant unit names (jax_ffi.py:180,845-846: dk_kv{0,1,2}_n{0..3}), each the entry above with
+ * its (clamp_kv, normal) fixed; _upload and _sizes as dk_fwd_upload / dk_fwd_sizes (o[6], o[7] the variant). */
+#define DK_VARIANT_DECL(KV, N)                                                                                       \
+  int dk_kv##KV##_n##N##_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric,            \
+                                  const float* com, const float* gq_out, const float* gv_out, float* gq_in,          \
+                                  float* gv_in, float* gctrl, int* info, const float* ctrl, float clamp_soft);       \
+  int dk_kv##KV##_n##N##_upload(const float* consts, hipStream_t st);                                                \
+  void dk_kv##KV##_n##N##_sizes(long long* o);
+DK_VARIANT_DECL(0, 0) DK_VARIANT_DECL(0, 1) DK_VARIANT_DECL(0, 2) DK_VARIANT_DECL(0, 3)
+DK_VARIANT_DECL(1, 0) DK_VARIANT_DECL(1, 1) DK_VARIANT_DECL(1, 2) DK_VARIANT_DECL(1, 3)
+DK_VARIANT_DECL(2, 0) DK_VARIANT_DECL(2, 1) DK_VARIANT_DECL(2, 2) DK_VARIANT_DECL(2, 3)
+#undef DK_VARIANT_DECL
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,37 @@
+"""Build the HIP library libnablaengine_g1.so in-tree for gfx950 (hipcc; one shared library, the C ABI of
+include/nablaengine_g1.h). `python -m nablaengine_amd.build`."""
+import os
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libnablaengine_g1.so")
+SOURCES = ["g1_forward.hip", "g1_capi.hip"]
+ARCH = os.environ.get("NABLA_OFFLOAD_ARCH", "gfx950")
+# packed FP32 instructions off (-packed-fp32-ops): the kernels are written for scalar FP32
+FLAGS = ["-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared", "-Xclang", "-target-feature", "-Xclang",
+         "-packed-fp32-ops", "-ffp-contract=fast", "-Wno-unused-command-line-argument"]
+
+
+def build(verbose=False):
+    """Compile every HIP source into the library (a temporary file renamed into place: a running process that
+    has the old library loaded keeps it)."""
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    fd, tmp = tempfile.mkstemp(prefix="libnablaengine_g1.", suffix=".so.tmp", dir=HERE)
+    os.close(fd)
+    cmd = [hipcc] + FLAGS + ["-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES]
+    if verbose:
+        print(" ".join(cmd))
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        os.unlink(tmp)
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"hipcc failed ({r.returncode})")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,78 @@
+// The C ABI (include/nablaengine_g1.h): thin entries over the kernels' launchers.
+#include "../../include/nablaengine_g1.h"
+
+#include <hip/hip_runtime.h>
+
+namespace g1k {
+int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
+                   const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
+                   int* info);
+size_t forward_lds_bytes();
+}  // namespace g1k
+
+namespace {
+constexpr int kNotBuilt = -2;  // an entry whose kernel is not in this build
+int check_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  hipDeviceProp_t p;
+  e = hipGetDeviceProperties(&p, dev);
+  if (e != hipSuccess) return (int)e;
+  return p.sharedMemPerBlock >= g1k::forward_lds_bytes() ? 0 : -1;
+}
+}  // namespace
+
+extern "C" {
+
+int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
+                   const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
+                   int* info, float* ocon, float* tape, void* work) {
+  (void)work;
+  if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0) return (int)hipErrorInvalidValue;
+  if (tape || ocon) return kNotBuilt;
+  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info);
+}
+
+long long dk_fwd_work_bytes(int nw) {
+  (void)nw;
+  return 0;
+}
+
+int dk_fwd_upload(const float* consts, hipStream_t st) {
+  (void)consts;
+  (void)st;
+  return check_device();
+}
+
+void dk_fwd_sizes(long long* o) {
+  o[0] = (long long)g1k::forward_lds_bytes(); o[1] = 0; o[2] = 0; o[3] = 36; o[4] = 35; o[5] = 64;
+  o[6] = -1; o[7] = -1; o[8] = 0;
+}
+
+int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+               const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+               const float* ctrl, float clamp_soft, int clamp_kv, int normal) {
+  (void)st; (void)nw; (void)nsub; (void)tape; (void)fric; (void)com; (void)gq_out; (void)gv_out; (void)gq_in;
+  (void)gv_in; (void)gctrl; (void)info; (void)ctrl; (void)clamp_soft; (void)clamp_kv; (void)normal;
+  return kNotBuilt;
+}
+
+#define DK_VARIANT_DEF(KV, N)                                                                                        \
+  int dk_kv##KV##_n##N##_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric,            \
+                                  const float* com, const float* gq_out, const float* gv_out, float* gq_in,          \
+                                  float* gv_in, float* gctrl, int* info, const float* ctrl, float clamp_soft) {      \
+    return dk_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl, clamp_soft, KV, \
+                      N);                                                                                            \
+  }                                                                                                                  \
+  int dk_kv##KV##_n##N##_upload(const float* consts, hipStream_t st) { return dk_fwd_upload(consts, st); }          \
+  void dk_kv##KV##_n##N##_sizes(long long* o) {                                                                      \
+    dk_fwd_sizes(o);                                                                                                 \
+    o[6] = KV;                                                                                                       \
+    o[7] = N;                                                                                                        \
+  }
+DK_VARIANT_DEF(0, 0) DK_VARIANT_DEF(0, 1) DK_VARIANT_DEF(0, 2) DK_VARIANT_DEF(0, 3)
+DK_VARIANT_DEF(1, 0) DK_VARIANT_DEF(1, 1) DK_VARIANT_DEF(1, 2) DK_VARIANT_DEF(1, 3)
+DK_VARIANT_DEF(2, 0) DK_VARIANT_DEF(2, 1) DK_VARIANT_DEF(2, 2) DK_VARIANT_DEF(2, 3)
+
+}  // extern "C"

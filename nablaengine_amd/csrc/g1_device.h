@@ -1,0 +1,196 @@
+// Device-side building blocks of the G1 control step shared by the forward and adjoint kernels: model constants in
+// constant memory, quaternion / vector helpers, wave64 cross-lane primitives, and the register Cholesky.
+//
+// Layout convention: one world per wave64 (64 lanes); lane l is dof l (l < 35), body l (l < 31), contact l
+// (l < ncon <= 64), geom l (l < 34) depending on the phase. World state that several lanes read lives in LDS.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "g1_tables.h"
+
+namespace g1k {
+using namespace g1t;
+
+constexpr int WL = 64;  // lanes per world: one wave64
+
+template <int N>
+constexpr Arr<int, N> to_int(const int (&a)[N]) {
+  Arr<int, N> r{};
+  for (int i = 0; i < N; i++) r.v[i] = a[i];
+  return r;
+}
+
+// model constants (float) in constant memory
+__constant__ inline Arr<float, NB * 3> cPos = to_float(BODY_POS);
+__constant__ inline Arr<float, NB * 4> cQuat = to_float(BODY_QUAT);
+__constant__ inline Arr<float, NB * 3> cAxis = to_float(BODY_AXIS);
+__constant__ inline Arr<float, NB * 3> cIpos = to_float(BODY_IPOS);
+__constant__ inline Arr<float, NB * 4> cIquat = to_float(BODY_IQUAT);
+__constant__ inline Arr<float, NB> cMass = to_float(BODY_MASS);
+__constant__ inline Arr<float, NB * 3> cInert = to_float(BODY_INERTIA);
+__constant__ inline Arr<float, NB> cBinvw = to_float(BODY_INVWEIGHT0);
+__constant__ inline Arr<int, NB> cParent = to_int(BODY_PARENT);
+__constant__ inline Arr<int, NB> cDepth = to_int(BODY_DEPTH);
+__constant__ inline Arr<int, NB> cQadr = to_int(BODY_QADR);
+__constant__ inline Arr<float, NV> cArm = to_float(DOF_ARMATURE);
+__constant__ inline Arr<float, NV> cDinvw = to_float(DOF_INVWEIGHT0);
+__constant__ inline Arr<float, NV> cKp = to_float(DOF_KP);
+__constant__ inline Arr<float, NV> cKv = to_float(DOF_KV);
+__constant__ inline Arr<float, NV> cFrclim = to_float(DOF_FRCLIM);
+__constant__ inline Arr<float, NV * 2> cRange = to_float(DOF_RANGE);
+__constant__ inline Arr<float, NGEOM * 3> cGsize = to_float(GEOM_SIZE);
+__constant__ inline Arr<float, NGEOM * 3> cGpos = to_float(GEOM_POS);
+__constant__ inline Arr<float, NGEOM * 4> cGquat = to_float(GEOM_QUAT);
+__constant__ inline Arr<float, NGEOM> cGrb = to_float(GEOM_RBOUND);
+__constant__ inline Arr<int, NGEOM> cGbody = to_int(GEOM_BODY);
+__constant__ inline Arr<unsigned, NPAIR> cPairW = PAIRW;
+__constant__ inline Arr<float, NPAIR> cPairMu = to_float(PAIR_MU);
+__constant__ inline Tree cTree = TREE;
+
+constexpr float kH = (float)TIMESTEP;
+constexpr float kGrav[3] = {(float)GRAVITY[0], (float)GRAVITY[1], (float)GRAVITY[2]};
+constexpr float kImpratio = (float)IMPRATIO;
+constexpr float kScale = (float)(1.0 / (MEANINERTIA * NV));  // Newton's cost / gradient scale (step.py:1974)
+constexpr float kTol = (float)TOLERANCE;
+
+// ------------------------------------------------------------------------------------------------ lane helpers
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+__device__ __forceinline__ float rdl(float x, int k) {  // lane k's x, k uniform
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
+}
+__device__ __forceinline__ int rdli(int x, int k) { return __builtin_amdgcn_readlane(x, k); }
+__device__ __forceinline__ unsigned long long ballot(bool p) { return __ballot(p); }
+__device__ __forceinline__ int prefix_count(unsigned long long m, int lane) {  // set bits of m below lane
+  return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+}
+// sum over the wave's 64 lanes, the same fixed butterfly order on every call (bitwise deterministic)
+__device__ __forceinline__ float wsum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float2 wsum2(float a, float b) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { a += __shfl_xor(a, o, 64); b += __shfl_xor(b, o, 64); }
+  return make_float2(a, b);
+}
+__device__ __forceinline__ int wsumi(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// exclusive prefix sum of small non-negative ints over the wave (Hillis-Steele on shuffles)
+__device__ __forceinline__ int wscan_excl(int v, int lane) {
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x - v;
+}
+__device__ __forceinline__ void wsync() { __syncthreads(); }
+
+// ------------------------------------------------------------------------------------------------ 3D helpers
+__device__ __forceinline__ void qmul(const float* a, const float* b, float* o) {
+  float w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];
+  float x = a[0] * b[1] + a[1] * b[0] + a[2] * b[3] - a[3] * b[2];
+  float y = a[0] * b[2] - a[1] * b[3] + a[2] * b[0] + a[3] * b[1];
+  float z = a[0] * b[3] + a[1] * b[2] - a[2] * b[1] + a[3] * b[0];
+  o[0] = w; o[1] = x; o[2] = y; o[3] = z;
+}
+__device__ __forceinline__ void qrot(const float* q, const float* v, float* o) {  // o = q v q^-1
+  float tx = 2.f * (q[2] * v[2] - q[3] * v[1]), ty = 2.f * (q[3] * v[0] - q[1] * v[2]);
+  float tz = 2.f * (q[1] * v[1] - q[2] * v[0]);
+  o[0] = v[0] + q[0] * tx + q[2] * tz - q[3] * ty;
+  o[1] = v[1] + q[0] * ty + q[3] * tx - q[1] * tz;
+  o[2] = v[2] + q[0] * tz + q[1] * ty - q[2] * tx;
+}
+__device__ __forceinline__ void qrot_inv(const float* q, const float* v, float* o) {
+  float qc[4] = {q[0], -q[1], -q[2], -q[3]};
+  qrot(qc, v, o);
+}
+__device__ __forceinline__ void cross(const float* a, const float* b, float* o) {
+  float x = a[1] * b[2] - a[2] * b[1], y = a[2] * b[0] - a[0] * b[2], z = a[0] * b[1] - a[1] * b[0];
+  o[0] = x; o[1] = y; o[2] = z;
+}
+__device__ __forceinline__ float dot3(const float* a, const float* b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2]; }
+
+// 1 / sqrt(d): the hardware estimate (v_rsq_f32) refined by one Newton-Raphson step y (3 - d y^2) / 2
+__device__ __forceinline__ float rsqrt_nr(float d) {
+  float y = __builtin_amdgcn_rsqf(d);
+  return y * (1.5f - 0.5f * d * y * y);
+}
+
+// ------------------------------------------------------------------------------------------------ Cholesky
+// In-place LL^T of the SPD matrix whose row `lane` is a[0..NV-1] (entries j <= lane; above the diagonal ignored),
+// right-looking, pivot column broadcast by v_readlane: afterwards a[j] = L[lane][j] (j < lane), a[lane] = L[lane][lane]
+// and dself = 1 / L[lane][lane]. Lanes >= NV carry garbage that is never read.
+__device__ __forceinline__ void chol_rows(float (&a)[NV], float& dself, int lane) {
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    float d = fmaxf(rdl(a[k], k), 1e-30f);
+    float inv = rsqrt_nr(d);
+    dself = lane == k ? inv : dself;
+    a[k] = lane == k ? d * inv : a[k] * inv;
+#pragma unroll
+    for (int j = k + 1; j < NV; j++) a[j] = fmaf(-a[k], rdl(a[k], j), a[j]);
+  }
+}
+
+// x = A^-1 b given the factor: rows a[] in registers (chol_rows) also stored packed in Lp (LDS, TRI layout); b on
+// lane i (i < NV); returns x on lane i. Forward substitution from the registers, backward from Lp.
+__device__ __forceinline__ float chol_solve_rows(const float (&a)[NV], float dself, const float* Lp, float b,
+                                                 int lane) {
+  float y = b;
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    float yk = rdl(y * dself, k);
+    y = lane == k ? yk : (lane > k ? fmaf(-a[k], yk, y) : y);
+  }
+  // backward: x_k = y_k / L_kk, then y_i -= L[k][i] x_k for i < k
+  float x = y;
+#pragma unroll
+  for (int k = NV - 1; k >= 0; k--) {
+    float xk = rdl(x * dself, k);
+    float lki = lane < k ? Lp[tri(k, lane)] : 0.f;
+    x = lane == k ? xk : (lane < k ? fmaf(-lki, xk, x) : x);
+  }
+  return x;
+}
+
+// the same solve with the factor only in Lp (a factor kept from an earlier Newton iteration)
+__device__ __forceinline__ float chol_resolve(const float* Lp, float b, int lane) {
+  float dself = lane < NV ? 1.f / Lp[tri(lane < NV ? lane : 0, lane < NV ? lane : 0)] : 0.f;
+  float y = b;
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    float yk = rdl(y * dself, k);
+    float lik = lane > k && lane < NV ? Lp[tri(lane, k)] : 0.f;
+    y = lane == k ? yk : (lane > k ? fmaf(-lik, yk, y) : y);
+  }
+  float x = y;
+#pragma unroll
+  for (int k = NV - 1; k >= 0; k--) {
+    float xk = rdl(x * dself, k);
+    float lki = lane < k ? Lp[tri(k, lane)] : 0.f;
+    x = lane == k ? xk : (lane < k ? fmaf(-lki, xk, x) : x);
+  }
+  return x;
+}
+
+// store the factor rows (register a[], lane = row) packed into Lp
+__device__ __forceinline__ void store_rows(const float (&a)[NV], float* Lp, int lane) {
+#pragma unroll
+  for (int j = 0; j < NV; j++)
+    if (lane < NV && j <= lane) Lp[tri(lane, j)] = a[j];
+}
+
+// load row `lane` of a packed symmetric matrix (lower part j <= lane) into registers
+__device__ __forceinline__ void load_rows(const float* Ap, float (&a)[NV], int lane) {
+  int r = lane < NV ? lane : NV - 1;
+#pragma unroll
+  for (int j = 0; j < NV; j++) a[j] = j <= r ? Ap[tri(r, j)] : 0.f;
+}
+
+}  // namespace g1k

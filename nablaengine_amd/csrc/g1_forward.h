@@ -1,0 +1,39 @@
+// LDS state of one world (one wave64) for the G1 forward control step.
+#pragma once
+#include "g1_device.h"
+
+namespace g1k {
+
+struct __align__(16) Sim {
+  float qpos[40], qvel[36], qacc[36], ctrl[32], com[4];
+  float qsm[36], qacc0[36], Ma[36], grad[36], p[36], Mp[36], vtmp[36];
+  float M[NTRI + 2];
+  float L[NTRI + 2];
+  float S[NV][8];             // dof motion subspaces about O: angular (0..2), velocity of O (4..6)
+  float Q[NB][4], X[NB][4];   // body poses
+  float ha[NB][4];            // hinge rotations
+  float O[4];
+  float fric;
+  int ncon, ncon_raw, nlim, nefc, flags, niter;
+  union {
+    struct { float F[NB][4], T[NB][4], Ic[NB][12]; } sm;  // smooth dynamics: subtree force, moment about O, inertia
+    struct { float gx[NGEOM][4], gq[NGEOM][4]; float stage[MAXCON][16]; unsigned short cand[NPAIR + 2]; } col;
+    struct {
+      float bw[NB][8];  // body spatial velocity of a dof vector: angular (0..2), velocity of O (4..6)
+      union {
+        float ft[MAXCON][8];  // contact spatial force about O: torque (0..2), force (4..6); bodies b1 (3), b2 (7)
+        struct { float kc[MAXCON][24]; float kb[NB][24]; float y[NV][8]; } h;  // Hessian scratch
+      };
+    } nt;
+  } u;
+};
+
+// per-lane register state of the constraint rows: lane l holds contact l's rows and dof l's limit row
+struct Rows {
+  float r[3], fr[9], mu, D;  // contact point - O; frame rows n, t1, t2; friction; the rows' D
+  int b1, b2, nr, dim;       // bodies, kept rows (0..4), condim
+  float aref[4], jar[4];     // per pyramid edge (or the normal row)
+  float lsg, lD, laref, ljar;  // the limit row of this lane's dof (active when lsg != 0)
+};
+
+}  // namespace g1k

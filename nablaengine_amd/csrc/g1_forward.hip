@@ -1,0 +1,970 @@
+// The G1 control step, forward: one wave64 per world, all substeps in one launch.
+//
+// Per substep (the reference's substep_pre / substep_post, g1_engine/step.py:1650-2184, restated for wave64):
+//   smooth     FK by each body walking its own chain (no level barriers), RNE bias and composite inertias by subtree
+//              masks, CRBA, clamped PD actuators, qacc_smooth = M^-1 qfrc_smooth (register Cholesky)
+//   collision  geom poses, bounding-sphere broadphase over the 502 pairs (ballot compaction in pair order),
+//              narrowphase one candidate per lane, contacts compacted in (pair, slot) order by a wave prefix sum
+//   rows       limits on their dof's lane, contact rows (4 pyramid edges or 1 normal row) on the contact's lane, all
+//              in registers; impedance from solref / solimp (step.py:1157-1188)
+//   Newton     cost 0.5 (a - a_s)' M (a - a_s) + sum s(J a - aref), warm start vs a_s, H = M + J'DJ, exact line
+//              search (step.py:1974-2137)
+//   implicit   (M + h kv) a_adv = M a*, qvel += h a_adv, qpos integrated (step.py:2153-2182)
+//
+// Contact Jacobians are never stored. J v is the contact point's relative velocity in the contact frame, from the
+// bodies' spatial velocities (sum of the motion subspaces S_d v_d along each body's chain); J' f is the sum of the
+// contacts' spatial forces projected on the dofs whose subtree holds the contact's bodies; J' C J enters the
+// Hessian as a 6x6 contact stiffness K_c = Phi' C Phi composited over subtrees exactly as CRBA composites inertia,
+// plus the cross-chain terms of contacts between two robot bodies.
+#include "g1_forward.h"
+
+namespace g1k {
+
+// ============================================================================================== smooth dynamics
+// motion subspace S_i of dof i about O: angular w (world), velocity of the point O (source.py:316-329 dof_motion)
+__device__ __forceinline__ void dof_motion(const Sim& s, int i, float* w, float* v) {
+  if (i < 3) {
+    w[0] = w[1] = w[2] = 0.f;
+    v[0] = i == 0; v[1] = i == 1; v[2] = i == 2;
+  } else if (i < 6) {
+    const float e[3] = {(float)(i == 3), (float)(i == 4), (float)(i == 5)};
+    qrot(s.Q[1], e, w);
+    v[0] = v[1] = v[2] = 0.f;
+  } else {
+    int b = i - 4;
+    float r[3] = {s.O[0] - s.X[b][0], s.O[1] - s.X[b][1], s.O[2] - s.X[b][2]};
+    const float ax[3] = {cAxis[3 * b], cAxis[3 * b + 1], cAxis[3 * b + 2]};
+    qrot(s.Q[b], ax, w);
+    cross(w, r, v);
+  }
+}
+
+// (n, f) = I (w, v) for a packed spatial inertia about O: n = J w + h x v, f = m v - h x w (source.py:305-313)
+__device__ __forceinline__ void apply_inertia(const float* J, const float* w, const float* v, float* n, float* f) {
+  float hv[3], hw[3];
+  cross(J + 6, v, hv);
+  cross(J + 6, w, hw);
+  n[0] = J[0] * w[0] + J[3] * w[1] + J[4] * w[2] + hv[0];
+  n[1] = J[3] * w[0] + J[1] * w[1] + J[5] * w[2] + hv[1];
+  n[2] = J[4] * w[0] + J[5] * w[1] + J[2] * w[2] + hv[2];
+  for (int k = 0; k < 3; k++) f[k] = J[9] * v[k] - hw[k];
+}
+
+__device__ void smooth(Sim& s, int lane) {
+  if (lane >= 2 && lane < NB) {  // hinge rotations, one lane per body
+    float sn, cs;
+    sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
+    s.ha[lane][0] = cs;
+    s.ha[lane][1] = sn * cAxis[3 * lane];
+    s.ha[lane][2] = sn * cAxis[3 * lane + 1];
+    s.ha[lane][3] = sn * cAxis[3 * lane + 2];
+  }
+  wsync();
+  // FK: each body lane walks its own chain from the root: pose, velocity, and the bias acceleration (qacc = 0;
+  // gravity as the root's -g) (source.py:186-235 fwd_body)
+  float Q[4], X[3], W[3], V[3], AL[3], A[3];
+  {
+    float n = rsqrtf(s.qpos[3] * s.qpos[3] + s.qpos[4] * s.qpos[4] + s.qpos[5] * s.qpos[5] + s.qpos[6] * s.qpos[6]);
+    for (int k = 0; k < 4; k++) Q[k] = s.qpos[3 + k] * n;
+    for (int k = 0; k < 3; k++) { X[k] = s.qpos[k]; V[k] = s.qvel[k]; A[k] = -kGrav[k]; AL[k] = 0.f; }
+    qrot(Q, s.qvel + 3, W);
+  }
+  const int b = lane < NB ? lane : 0;
+  const int depth = cDepth[b];
+#pragma unroll
+  for (int l = 1; l < MAXDEPTH; l++) {
+    if (l < depth) {
+      const int k = cTree.path[b][l];
+      float q0[4], t[3], aw[3], r[3], awd[3], u[3], wr[3], u2[3];
+      const float qb[4] = {cQuat[4 * k], cQuat[4 * k + 1], cQuat[4 * k + 2], cQuat[4 * k + 3]};
+      const float pb[3] = {cPos[3 * k], cPos[3 * k + 1], cPos[3 * k + 2]};
+      const float ax[3] = {cAxis[3 * k], cAxis[3 * k + 1], cAxis[3 * k + 2]};
+      const float ha[4] = {s.ha[k][0], s.ha[k][1], s.ha[k][2], s.ha[k][3]};
+      qmul(Q, qb, q0);
+      qrot(Q, pb, t);  // r = X_child - X_parent
+      for (int c = 0; c < 3; c++) r[c] = t[c];
+      qmul(q0, ha, Q);
+      qrot(Q, ax, aw);
+      const float qd = s.qvel[k + 4];
+      for (int c = 0; c < 3; c++) awd[c] = aw[c] * qd;
+      // from the parent's W, AL (in registers): A, V, AL, then W
+      cross(AL, r, u);
+      cross(W, r, wr);
+      cross(W, wr, u2);
+      for (int c = 0; c < 3; c++) { A[c] += u[c] + u2[c]; V[c] += wr[c]; X[c] += t[c]; }
+      cross(W, awd, u);
+      for (int c = 0; c < 3; c++) { AL[c] += u[c]; W[c] += awd[c]; }
+    }
+  }
+  if (lane < NB) {
+    for (int k = 0; k < 4; k++) s.Q[lane][k] = lane == 0 ? (k == 0 ? 1.f : 0.f) : Q[k];
+    for (int k = 0; k < 3; k++) s.X[lane][k] = lane == 0 ? 0.f : X[k];
+  }
+  if (lane < 3) s.O[lane] = s.qpos[lane];  // O: the root body's origin, the point of M and of the spatial vectors
+  // body force F, moment about O T = N + (X - O) x F, composite-ready spatial inertia about O
+  if (lane >= 1 && lane < NB) {
+    float ip[3], c[3], u[3], wc[3], u2[3], F[3], N[3];
+    for (int k = 0; k < 3; k++) ip[k] = cIpos[3 * lane + k] + (lane == TORSO_BODY ? s.com[k] : 0.f);
+    qrot(Q, ip, c);
+    cross(AL, c, u);
+    cross(W, c, wc);
+    cross(W, wc, u2);
+    const float m = cMass[lane];
+    for (int k = 0; k < 3; k++) F[k] = m * (A[k] + u[k] + u2[k]);
+    float qi[4], l[3], Iw[3], Ia[3], cf[3];
+    const float iq[4] = {cIquat[4 * lane], cIquat[4 * lane + 1], cIquat[4 * lane + 2], cIquat[4 * lane + 3]};
+    const float In[3] = {cInert[3 * lane], cInert[3 * lane + 1], cInert[3 * lane + 2]};
+    qmul(Q, iq, qi);
+    qrot_inv(qi, W, l);
+    for (int k = 0; k < 3; k++) l[k] *= In[k];
+    qrot(qi, l, Iw);
+    qrot_inv(qi, AL, l);
+    for (int k = 0; k < 3; k++) l[k] *= In[k];
+    qrot(qi, l, Ia);
+    cross(W, Iw, u);
+    cross(c, F, cf);
+    for (int k = 0; k < 3; k++) N[k] = Ia[k] + u[k] + cf[k];
+    // moment about O
+    float xo[3] = {X[0] - s.qpos[0], X[1] - s.qpos[1], X[2] - s.qpos[2]}, xf[3];
+    cross(xo, F, xf);
+    for (int k = 0; k < 3; k++) { s.u.sm.F[lane][k] = F[k]; s.u.sm.T[lane][k] = N[k] + xf[k]; }
+    // spatial inertia about O (source.py:280-302 body_inertia)
+    float R[9];
+    for (int k = 0; k < 3; k++) {
+      float e[3] = {(float)(k == 0), (float)(k == 1), (float)(k == 2)};
+      qrot(qi, e, R + 3 * k);
+    }
+    float* J = s.u.sm.Ic[lane];
+    J[0] = In[0] * R[0] * R[0] + In[1] * R[3] * R[3] + In[2] * R[6] * R[6];
+    J[1] = In[0] * R[1] * R[1] + In[1] * R[4] * R[4] + In[2] * R[7] * R[7];
+    J[2] = In[0] * R[2] * R[2] + In[1] * R[5] * R[5] + In[2] * R[8] * R[8];
+    J[3] = In[0] * R[0] * R[1] + In[1] * R[3] * R[4] + In[2] * R[6] * R[7];
+    J[4] = In[0] * R[0] * R[2] + In[1] * R[3] * R[5] + In[2] * R[6] * R[8];
+    J[5] = In[0] * R[1] * R[2] + In[1] * R[4] * R[5] + In[2] * R[7] * R[8];
+    float cc3[3];
+    for (int k = 0; k < 3; k++) cc3[k] = xo[k] + c[k];
+    float cc = dot3(cc3, cc3);
+    J[0] += m * (cc - cc3[0] * cc3[0]); J[1] += m * (cc - cc3[1] * cc3[1]); J[2] += m * (cc - cc3[2] * cc3[2]);
+    J[3] -= m * cc3[0] * cc3[1]; J[4] -= m * cc3[0] * cc3[2]; J[5] -= m * cc3[1] * cc3[2];
+    J[6] = m * cc3[0]; J[7] = m * cc3[1]; J[8] = m * cc3[2]; J[9] = m;
+  }
+  wsync();
+  // subtree sums by masks (lane = body): force, moment about O, spatial inertia
+  float Fs[3] = {0.f, 0.f, 0.f}, Ts[3] = {0.f, 0.f, 0.f}, Js[10];
+  for (int k = 0; k < 10; k++) Js[k] = 0.f;
+  const unsigned sub = lane >= 1 && lane < NB ? cTree.submask[lane] : 0u;
+  for (int c = 1; c < NB; c++) {
+    const float m = (float)((sub >> c) & 1u);
+    for (int k = 0; k < 3; k++) { Fs[k] += m * s.u.sm.F[c][k]; Ts[k] += m * s.u.sm.T[c][k]; }
+    for (int k = 0; k < 10; k++) Js[k] += m * s.u.sm.Ic[c][k];
+  }
+  wsync();
+  if (lane >= 1 && lane < NB) {
+    for (int k = 0; k < 3; k++) { s.u.sm.F[lane][k] = Fs[k]; s.u.sm.T[lane][k] = Ts[k]; }
+    for (int k = 0; k < 10; k++) s.u.sm.Ic[lane][k] = Js[k];
+  }
+  // motion subspaces
+  if (lane < NV) {
+    float w[3], v[3];
+    dof_motion(s, lane, w, v);
+    for (int k = 0; k < 3; k++) { s.S[lane][k] = w[k]; s.S[lane][4 + k] = v[k]; }
+  }
+  wsync();
+  // bias forces (qfrc_bias) projected on the dofs, CRBA row of dof `lane`, actuators
+  float bias = 0.f;
+  if (lane < NV) {
+    const int bi = lane < 6 ? 1 : lane - 4;
+    const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]}, v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
+    // subtree force / moment about the body origin X_b: N_b = T - (X_b - O) x F; the projection on a dof through O:
+    // S . (T, F) with S = (w, w x (O - X_b)) equals w . N_b
+    float Fb[3], Tb[3];
+    for (int k = 0; k < 3; k++) { Fb[k] = s.u.sm.F[bi][k]; Tb[k] = s.u.sm.T[bi][k]; }
+    bias = dot3(w, Tb) + dot3(v, Fb);
+    float Jb[10], n[3], f[3];
+    for (int k = 0; k < 10; k++) Jb[k] = s.u.sm.Ic[bi][k];
+    apply_inertia(Jb, w, v, n, f);
+    const uint64_t anc = cTree.dofanc[lane];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      if (j <= lane && ((anc >> j) & 1ull)) {
+        float mij = s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
+                    + s.S[j][6] * f[2];
+        if (j == lane) mij += cArm[lane];
+        s.M[tri(lane, j)] = mij;
+      } else if (j <= lane) {
+        s.M[tri(lane, j)] = 0.f;
+      }
+    }
+    float act = 0.f;
+    if (lane >= 6) {
+      act = cKp[lane] * (s.ctrl[lane - 6] - s.qpos[lane + 1]) - cKv[lane] * s.qvel[lane];
+      act = fminf(fmaxf(act, -cFrclim[lane]), cFrclim[lane]);
+    }
+    s.qsm[lane] = act - bias;
+  }
+  wsync();
+  // qacc_smooth = M^-1 qfrc_smooth
+  float a[NV], dself = 1.f;
+  load_rows(s.M, a, lane);
+  chol_rows(a, dself, lane);
+  store_rows(a, s.L, lane);
+  wsync();
+  float x = chol_solve_rows(a, dself, s.L, lane < NV ? s.qsm[lane] : 0.f, lane);
+  if (lane < NV) s.qacc0[lane] = x;
+  wsync();
+}
+
+}  // namespace g1k
+
+namespace g1k {
+
+// ============================================================================================== collision
+// MuJoCo's frame from a normal n: rows n, b, n x b with b the unit vector e_y (|n_y| < 0.5) or e_z made orthogonal to
+// n (step.py:378-387 make_frame)
+__device__ __forceinline__ void make_frame(const float* n, float* fr) {
+  float b[3] = {0.f, 0.f, 0.f};
+  if (-0.5f < n[1] && n[1] < 0.5f) b[1] = 1.f; else b[2] = 1.f;
+  float d = dot3(n, b);
+  for (int k = 0; k < 3; k++) b[k] -= n[k] * d;
+  float bn = sqrtf(dot3(b, b));
+  if (bn > 0.f) for (int k = 0; k < 3; k++) b[k] /= bn;
+  float c[3];
+  cross(n, b, c);
+  for (int k = 0; k < 3; k++) { fr[k] = n[k]; fr[3 + k] = b[k]; fr[6 + k] = c[k]; }
+}
+
+__device__ __forceinline__ void sphere_sphere(const float* p1, float r1, const float* p2, float r2, float* dist,
+                                              float* pos, float* n) {
+  float dir[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
+  float d = sqrtf(dot3(dir, dir));
+  if (d == 0.f) { n[0] = 1.f; n[1] = 0.f; n[2] = 0.f; } else { for (int k = 0; k < 3; k++) n[k] = dir[k] / d; }
+  *dist = d - (r1 + r2);
+  float hp = 0.5f * *dist + r1;
+  for (int k = 0; k < 3; k++) pos[k] = p1[k] + n[k] * hp;
+}
+
+__device__ __forceinline__ float plane_point(const float* p1, const float* n, const float* c, float r, float* pos) {
+  float dist = (dot3(c, n) - dot3(p1, n)) - r, hp = 0.5f * dist + r;
+  for (int k = 0; k < 3; k++) pos[k] = c[k] - n[k] * hp;
+  return dist;
+}
+
+__device__ __forceinline__ void zaxis(const float* q, float* a) {
+  const float ez[3] = {0.f, 0.f, 1.f};
+  qrot(q, ez, a);
+}
+
+struct Cand {  // up to two contacts of one pair: A then B
+  float d[2], pos[2][3], fr[2][9];
+  int slot[2];
+  bool has[2];
+};
+
+__device__ __forceinline__ void put(Cand& o, int which, int slot, float dist, const float* pos, const float* fr) {
+  // which is a compile-time 0 / 1 at every call site
+  o.has[which] = true;
+  o.d[which] = dist;
+  o.slot[which] = slot;
+  for (int k = 0; k < 3; k++) o.pos[which][k] = pos[k];
+  for (int k = 0; k < 9; k++) o.fr[which][k] = fr[k];
+}
+
+// narrowphase of pair pr (step.py:1042-1143 collide_pair), zero margin
+__device__ void collide_pair(const Sim& s, int pr, Cand& o) {
+  o.has[0] = o.has[1] = false;
+  const unsigned w = cPairW[pr];
+  const int g1 = w & 255u, g2 = (w >> 8) & 255u, cls = (w >> 21) & 7u;
+  float p1[3], q1[4], p2[3], q2[4];
+  for (int k = 0; k < 3; k++) { p1[k] = s.u.col.gx[g1][k]; p2[k] = s.u.col.gx[g2][k]; }
+  for (int k = 0; k < 4; k++) { q1[k] = s.u.col.gq[g1][k]; q2[k] = s.u.col.gq[g2][k]; }
+  const float r1 = cGsize[3 * g1], hl1 = cGsize[3 * g1 + 1], r2 = cGsize[3 * g2], hl2 = cGsize[3 * g2 + 1];
+  float pos[3], fr[9], n[3], dist;
+  if (cls == 0 || cls == 4) {  // plane (the floor) against a sphere or a capsule
+    zaxis(q1, n);
+    float dif[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
+    if (dot3(dif, n) > cGrb[g2]) return;
+    if (cls == 0) {
+      dist = plane_point(p1, n, p2, r2, pos);
+      make_frame(n, fr);
+      if (dist < 0.f) put(o, 0, 0, dist, pos, fr);
+    } else {
+      float axis[3];
+      zaxis(q2, axis);
+      // plane_capsule_frame (step.py:461-474): b = axis projected on the plane, normalized; make_frame's basis
+      // vector where the projection is shorter than 0.5
+      float na = dot3(n, axis), b[3];
+      for (int k = 0; k < 3; k++) b[k] = axis[k] - n[k] * na;
+      float bn = sqrtf(dot3(b, b));
+      if (bn > 0.f) for (int k = 0; k < 3; k++) b[k] /= bn;
+      if (bn < 0.5f) {
+        b[0] = b[1] = b[2] = 0.f;
+        if (-0.5f < n[1] && n[1] < 0.5f) b[1] = 1.f; else b[2] = 1.f;
+      }
+      float c[3];
+      cross(n, b, c);
+      for (int k = 0; k < 3; k++) { fr[k] = n[k]; fr[3 + k] = b[k]; fr[6 + k] = c[k]; }
+      float ce[3];
+      for (int k = 0; k < 3; k++) ce[k] = p2[k] + axis[k] * hl2;
+      dist = plane_point(p1, n, ce, r2, pos);
+      if (dist < 0.f) put(o, 0, 0, dist, pos, fr);
+      for (int k = 0; k < 3; k++) ce[k] = p2[k] - axis[k] * hl2;
+      dist = plane_point(p1, n, ce, r2, pos);
+      if (dist < 0.f) put(o, 1, 1, dist, pos, fr);
+    }
+    return;
+  }
+  {
+    float dif[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]}, rb = cGrb[g1] + cGrb[g2];
+    if (dot3(dif, dif) > rb * rb) return;
+  }
+  if (cls == 1) {  // sphere-sphere
+    sphere_sphere(p1, r1, p2, r2, &dist, pos, n);
+    if (dist < 0.f) { make_frame(n, fr); put(o, 0, 0, dist, pos, fr); }
+    return;
+  }
+  if (cls == 2) {  // sphere-capsule: the capsule segment's closest point (step.py:487-497 segment_point)
+    float axis[3], a[3], ab[3], ap[3], pt[3];
+    zaxis(q2, axis);
+    for (int k = 0; k < 3; k++) { a[k] = p2[k] - axis[k] * hl2; ab[k] = 2.f * axis[k] * hl2; ap[k] = p1[k] - a[k]; }
+    float gam = dot3(ab, ab) + 1e-6f, t = fminf(fmaxf(dot3(ap, ab) / gam, 0.f), 1.f);
+    for (int k = 0; k < 3; k++) pt[k] = a[k] + t * ab[k];
+    sphere_sphere(p1, r1, pt, r2, &dist, pos, n);
+    if (dist < 0.f) { make_frame(n, fr); put(o, 0, 0, dist, pos, fr); }
+    return;
+  }
+  // capsule-capsule (step.py:501-554 capcap_setup / capcap_params / capcap_candidate)
+  float a1[3], a2[3], d[3];
+  zaxis(q1, a1);
+  zaxis(q2, a2);
+  for (int k = 0; k < 3; k++) { a1[k] *= hl1; a2[k] *= hl2; d[k] = p1[k] - p2[k]; }
+  const float ma = dot3(a1, a1), mb = -dot3(a1, a2), mc = dot3(a2, a2), u = -dot3(a1, d), v = dot3(a2, d);
+  const float det = ma * mc - mb * mb;
+  if (fabsf(det) >= 1e-15f) {
+    float x1 = (mc * u - mb * v) / det, x2 = (ma * v - mb * u) / det;
+    if (x1 > 1.f) { x1 = 1.f; x2 = (v - mb) / mc; }
+    else if (x1 < -1.f) { x1 = -1.f; x2 = (v + mb) / mc; }
+    if (x2 > 1.f || x2 < -1.f) {
+      bool hi = x2 > 1.f;
+      x2 = hi ? 1.f : -1.f;
+      float raw = hi ? (u - mb) / ma : (u + mb) / ma;
+      x1 = fminf(fmaxf(raw, -1.f), 1.f);
+    }
+    float v1[3], v2[3];
+    for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
+    sphere_sphere(v1, r1, v2, r2, &dist, pos, n);
+    if (dist < 0.f) { make_frame(n, fr); put(o, 0, 0, dist, pos, fr); }
+  } else {
+    int cnt = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      if (cnt >= 2) break;
+      float x1, x2;
+      if (e < 2) {
+        x1 = e == 0 ? 1.f : -1.f;
+        float raw = e == 0 ? (v - mb) / mc : (v + mb) / mc;
+        x2 = fminf(fmaxf(raw, -1.f), 1.f);
+      } else {
+        x2 = e == 2 ? 1.f : -1.f;
+        float raw = e == 2 ? (u - mb) / ma : (u + mb) / ma;
+        x1 = fminf(fmaxf(raw, -1.f), 1.f);
+      }
+      float v1[3], v2[3];
+      for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
+      sphere_sphere(v1, r1, v2, r2, &dist, pos, n);
+      if (dist <= 0.f) {
+        if (dist < 0.f) {
+          make_frame(n, fr);
+          if (!o.has[0]) put(o, 0, e, dist, pos, fr); else put(o, 1, e, dist, pos, fr);
+        }
+        cnt++;
+      }
+    }
+  }
+}
+
+// geom poses, broadphase, narrowphase; contacts in (pair, slot) order into s.u.col.stage
+__device__ void collision(Sim& s, int lane) {
+  if (lane < NGEOM) {
+    const int b = cGbody[lane];
+    float t[3], qb[4] = {s.Q[b][0], s.Q[b][1], s.Q[b][2], s.Q[b][3]};
+    const float gp[3] = {cGpos[3 * lane], cGpos[3 * lane + 1], cGpos[3 * lane + 2]};
+    const float gq[4] = {cGquat[4 * lane], cGquat[4 * lane + 1], cGquat[4 * lane + 2], cGquat[4 * lane + 3]};
+    qrot(qb, gp, t);
+    for (int k = 0; k < 3; k++) s.u.col.gx[lane][k] = s.X[b][k] + t[k];
+    qmul(qb, gq, s.u.col.gq[lane]);
+  }
+  wsync();
+  // broadphase: the narrowphase's first test with a relative slack of 1e-5, candidates compacted in pair order
+  float fn[3];
+  {
+    const float q0[4] = {s.u.col.gq[0][0], s.u.col.gq[0][1], s.u.col.gq[0][2], s.u.col.gq[0][3]};
+    zaxis(q0, fn);
+  }
+  int ncand = 0;
+  for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {
+    const int pr = lane + WL * k;
+    bool keep = false;
+    if (pr < NPAIR) {
+      const unsigned w = cPairW[pr];
+      const int g1 = w & 255u, g2 = (w >> 8) & 255u;
+      float dif[3] = {s.u.col.gx[g2][0] - s.u.col.gx[g1][0], s.u.col.gx[g2][1] - s.u.col.gx[g1][1],
+                      s.u.col.gx[g2][2] - s.u.col.gx[g1][2]};
+      const unsigned cls = (w >> 21) & 7u;
+      if (cls == 0u || cls == 4u) keep = dot3(dif, fn) <= cGrb[g2] * (1.f + 1e-5f) + 1e-6f;
+      else {
+        float rb = cGrb[g1] + cGrb[g2];
+        keep = dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f;
+      }
+    }
+    const unsigned long long bal = ballot(keep);
+    if (keep) s.u.col.cand[ncand + prefix_count(bal, lane)] = (unsigned short)pr;
+    ncand += __popcll(bal);
+  }
+  wsync();
+  // narrowphase: one candidate per lane; contacts placed by a prefix sum of the per-lane counts (pair order)
+  int total = 0;
+  for (int c0 = 0; c0 < ncand; c0 += WL) {
+    Cand o;
+    o.has[0] = o.has[1] = false;
+    int pr = -1;
+    if (c0 + lane < ncand) {
+      pr = s.u.col.cand[c0 + lane];
+      collide_pair(s, pr, o);
+    }
+    const int n = (int)o.has[0] + (int)o.has[1];
+    const int off = total + wscan_excl(n, lane);
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int idx = off + (e == 1 ? (int)o.has[0] : 0);
+      if (o.has[e] && idx < MAXCON) {
+        float* st = s.u.col.stage[idx];
+        st[0] = o.d[e];
+        for (int k = 0; k < 3; k++) st[1 + k] = o.pos[e][k];
+        for (int k = 0; k < 9; k++) st[4 + k] = o.fr[e][k];
+        st[13] = __int_as_float(pr);
+        st[14] = __int_as_float(o.slot[e]);
+      }
+    }
+    total += wsumi(n);
+  }
+  if (lane == 0) {
+    s.ncon_raw = total;
+    s.ncon = total < MAXCON ? total : MAXCON;
+    if (total > MAXCON) s.flags |= 4;
+  }
+  wsync();
+}
+
+// ============================================================================================== rows
+// impedance (k, b, imp) of a row at distance pos, solref / solimp with refsafe (step.py:1157-1171 kbimp); the model's
+// solimp power is 2
+__device__ __forceinline__ void kbimp(const float* solref, const float* solimp, float pos, float* k, float* b,
+                                      float* imp) {
+  float tc = fmaxf(solref[0], 2.f * kH), dr = solref[1];
+  float dmin = fminf(fmaxf(solimp[0], 1e-4f), 0.9999f), dmax = fminf(fmaxf(solimp[1], 1e-4f), 0.9999f);
+  float width = fmaxf(1e-15f, solimp[2]), mid = fminf(fmaxf(solimp[3], 1e-4f), 0.9999f);
+  *k = 1.f / fmaxf(1e-15f, dmax * dmax * tc * tc * dr * dr);
+  *b = 2.f / fmaxf(1e-15f, dmax * tc);
+  float x = fabsf(pos) / width;
+  if (dmin == dmax || solimp[2] <= 1e-15f) *imp = 0.5f * (dmin + dmax);
+  else if (x <= 0.f) *imp = dmin;
+  else if (x >= 1.f) *imp = dmax;
+  else {
+    float y = x <= mid ? (x * x) / mid : 1.f - ((1.f - x) * (1.f - x)) / (1.f - mid);
+    *imp = fminf(fmaxf(dmin + y * (dmax - dmin), dmin), dmax);
+  }
+}
+
+__constant__ inline Arr<float, 2> cJSolref = to_float(JNT_SOLREF);
+__constant__ inline Arr<float, 5> cJSolimp = to_float(JNT_SOLIMP);
+__constant__ inline Arr<float, 2> cPSolref = to_float(PAIR_SOLREF);
+__constant__ inline Arr<float, 5> cPSolimp = to_float(PAIR_SOLIMP);
+static_assert(JNT_SOLIMP[4] == 2.0 && PAIR_SOLIMP[4] == 2.0, "kbimp assumes the solimp power 2");
+
+// body spatial velocities of the dof vector v (LDS, NV): bw[b] = sum over b's chain of S_d v_d
+__device__ __forceinline__ void body_vel(Sim& s, const float* v, int lane) {
+  if (lane < NB) {
+    float w[3] = {0.f, 0.f, 0.f}, u[3] = {0.f, 0.f, 0.f};
+    const int n = cTree.nchain[lane];
+    for (int t = 0; t < MAXCHAIN; t++) {
+      if (t < n) {
+        const int d = cTree.chain[lane][t];
+        const float vd = v[d];
+        for (int k = 0; k < 3; k++) { w[k] += s.S[d][k] * vd; u[k] += s.S[d][4 + k] * vd; }
+      }
+    }
+    for (int k = 0; k < 3; k++) { s.u.nt.bw[lane][k] = w[k]; s.u.nt.bw[lane][4 + k] = u[k]; }
+  }
+  wsync();
+}
+
+// relative velocity of body2 against body1 at the contact point, in the contact frame (J_c v): needs body_vel(v)
+__device__ __forceinline__ void contact_dots(const Sim& s, const Rows& R, float* dot) {
+  float dw[3], dv[3], u[3], rel[3];
+  for (int k = 0; k < 3; k++) {
+    dw[k] = s.u.nt.bw[R.b2][k] - s.u.nt.bw[R.b1][k];
+    dv[k] = s.u.nt.bw[R.b2][4 + k] - s.u.nt.bw[R.b1][4 + k];
+  }
+  cross(dw, R.r, u);
+  for (int k = 0; k < 3; k++) rel[k] = dv[k] + u[k];
+  dot[0] = dot3(R.fr, rel);
+  dot[1] = dot3(R.fr + 3, rel);
+  dot[2] = dot3(R.fr + 6, rel);
+}
+
+// J v of this lane's rows: contact rows (pyramid edges n +- mu t1, n +- mu t2, or the normal) and the limit row
+__device__ __forceinline__ void rows_jv(Sim& s, const Rows& R, const float* v, int lane, bool con, float* jv,
+                                        float* ljv) {
+  body_vel(s, v, lane);
+  float dot[3] = {0.f, 0.f, 0.f};
+  if (con) contact_dots(s, R, dot);
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const float sg = (t & 1) ? -1.f : 1.f;
+    jv[t] = R.dim == 3 ? dot[0] + sg * R.mu * dot[1 + (t >> 1)] : dot[0];
+  }
+  *ljv = lane < NV ? R.lsg * v[lane] : 0.f;
+  wsync();
+}
+
+// out = M v (M packed in LDS, v in LDS), lane i < NV
+__device__ __forceinline__ float matvec(const Sim& s, const float* v, int lane) {
+  if (lane >= NV) return 0.f;
+  float acc = 0.f, acc2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const float m = s.M[j <= lane ? tri(lane, j) : tri(j, lane)];
+    if (j & 1) acc2 = fmaf(m, v[j], acc2); else acc = fmaf(m, v[j], acc);
+  }
+  return acc + acc2;
+}
+
+// ============================================================================================== Newton
+struct NewtonOut { int it; bool conv; };
+
+// gradient at the current jar: grad = M a - qfrc_smooth - J' f, f = -D x on the rows with x < 0; returns |grad|
+__device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
+  if (con) {  // the contact's frame force in world coordinates and its moment about O
+    float f[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) f[t] = (t < R.nr && R.jar[t] < 0.f) ? -R.D * R.jar[t] : 0.f;
+    float fn, f1 = 0.f, f2 = 0.f;
+    if (R.dim == 3) { fn = f[0] + f[1] + f[2] + f[3]; f1 = R.mu * (f[0] - f[1]); f2 = R.mu * (f[2] - f[3]); }
+    else fn = f[0];
+    float F[3], T[3];
+    for (int k = 0; k < 3; k++) F[k] = fn * R.fr[k] + f1 * R.fr[3 + k] + f2 * R.fr[6 + k];
+    cross(R.r, F, T);
+    float* o = s.u.nt.ft[lane];
+    o[0] = T[0]; o[1] = T[1]; o[2] = T[2]; o[3] = __int_as_float(R.b1);
+    o[4] = F[0]; o[5] = F[1]; o[6] = F[2]; o[7] = __int_as_float(R.b2);
+  }
+  wsync();
+  float g = 0.f;
+  if (lane < NV) {
+    const unsigned mask = cTree.dofmask32[lane];
+    const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]}, v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
+    float tau = 0.f;
+    const int ncon = s.ncon;
+    for (int c = 0; c < ncon; c++) {
+      const float* o = s.u.nt.ft[c];
+      const int b1 = __float_as_int(o[3]), b2 = __float_as_int(o[7]);
+      const float sg = (float)((int)((mask >> b2) & 1u) - (int)((mask >> b1) & 1u));
+      tau += sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[4] + v[1] * o[5] + v[2] * o[6]);
+    }
+    if (R.lsg != 0.f && R.ljar < 0.f) tau += R.lsg * (-R.lD * R.ljar);
+    g = s.Ma[lane] - s.qsm[lane] - tau;
+    s.grad[lane] = g;
+  }
+  wsync();
+  return sqrtf(wsum(g * g));
+}
+
+__device__ __forceinline__ float lane_cost(const Sim& s, const Rows& R, int lane) {
+  float g = 0.f;
+  if (lane < NV) g = 0.5f * (s.Ma[lane] - s.qsm[lane]) * (s.qacc[lane] - s.qacc0[lane]);
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+    if (t < R.nr && R.jar[t] < 0.f) g += 0.5f * R.D * R.jar[t] * R.jar[t];
+  if (R.lsg != 0.f && R.ljar < 0.f) g += 0.5f * R.lD * R.ljar * R.ljar;
+  return g;
+}
+
+// Ma = M qacc and jar = J qacc - aref
+__device__ void refresh(Sim& s, Rows& R, int lane, bool con) {
+  float ma = matvec(s, s.qacc, lane);
+  if (lane < NV) s.Ma[lane] = ma;
+  float jv[4], ljv;
+  rows_jv(s, R, s.qacc, lane, con, jv, &ljv);
+#pragma unroll
+  for (int t = 0; t < 4; t++) R.jar[t] = jv[t] - R.aref[t];
+  R.ljar = ljv - R.laref;
+}
+
+// H = M + J' D J on the rows with x < 0 (lane = row of H, into registers h), then its factor
+__device__ void hessian(Sim& s, const Rows& R, int lane, bool con, float (&h)[NV]) {
+  const int ncon = s.ncon;
+  // the contact's 6x6 stiffness K = Phi' C Phi about O, C from the pyramid rows' curvatures in the frame basis
+  bool act = false;
+  if (con) {
+    float d[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) d[t] = (t < R.nr && R.jar[t] < 0.f) ? R.D : 0.f;
+    float Cnn, Cn1 = 0.f, C11 = 0.f, Cn2 = 0.f, C22 = 0.f;
+    if (R.dim == 3) {
+      Cnn = d[0] + d[1] + d[2] + d[3];
+      Cn1 = R.mu * (d[0] - d[1]); C11 = R.mu * R.mu * (d[0] + d[1]);
+      Cn2 = R.mu * (d[2] - d[3]); C22 = R.mu * R.mu * (d[2] + d[3]);
+    } else Cnn = d[0];
+    act = Cnn != 0.f;
+    const float *n = R.fr, *t1 = R.fr + 3, *t2 = R.fr + 6;
+    float Kf[3][3];
+    for (int a = 0; a < 3; a++)
+      for (int b = 0; b < 3; b++)
+        Kf[a][b] = Cnn * n[a] * n[b] + Cn1 * (n[a] * t1[b] + t1[a] * n[b]) + C11 * t1[a] * t1[b]
+                   + Cn2 * (n[a] * t2[b] + t2[a] * n[b]) + C22 * t2[a] * t2[b];
+    float Kal[3][3], Kaa[3][3];
+    for (int b = 0; b < 3; b++) {  // column b of r^ Kf = r x Kf[:, b]
+      float col[3] = {Kf[0][b], Kf[1][b], Kf[2][b]}, o[3];
+      cross(R.r, col, o);
+      for (int a = 0; a < 3; a++) Kal[a][b] = o[a];
+    }
+    for (int a = 0; a < 3; a++) {  // row a of r^ Kf r^' = r x (row a of Kal)
+      float row[3] = {Kal[a][0], Kal[a][1], Kal[a][2]}, o[3];
+      cross(R.r, row, o);
+      for (int b = 0; b < 3; b++) Kaa[a][b] = o[b];
+    }
+    float* k = s.u.nt.h.kc[lane];
+    k[0] = Kaa[0][0]; k[1] = Kaa[1][1]; k[2] = Kaa[2][2]; k[3] = Kaa[0][1]; k[4] = Kaa[0][2]; k[5] = Kaa[1][2];
+    for (int a = 0; a < 3; a++) for (int b = 0; b < 3; b++) k[6 + 3 * a + b] = Kal[a][b];
+    k[15] = Kf[0][0]; k[16] = Kf[1][1]; k[17] = Kf[2][2]; k[18] = Kf[0][1]; k[19] = Kf[0][2]; k[20] = Kf[1][2];
+    k[21] = __int_as_float(R.b1); k[22] = __int_as_float(R.b2);
+  }
+  const unsigned long long actm = ballot(act);
+  const unsigned long long selfm = ballot(act && R.b1 != 0);
+  wsync();
+  // composite stiffness of each body's subtree: sum of the contacts whose bodies lie in it (once per body in it)
+  if (lane >= 1 && lane < NB) {
+    float kb[21];
+    for (int e = 0; e < 21; e++) kb[e] = 0.f;
+    const unsigned sub = cTree.submask[lane];
+    for (unsigned long long m = actm; m; m &= m - 1ull) {
+      const int c = __builtin_ctzll(m);
+      const float* k = s.u.nt.h.kc[c];
+      const int b1 = __float_as_int(k[21]), b2 = __float_as_int(k[22]);
+      const float mult = (float)((int)((sub >> b1) & 1u) + (int)((sub >> b2) & 1u));
+      for (int e = 0; e < 21; e++) kb[e] += mult * k[e];
+    }
+    for (int e = 0; e < 21; e++) s.u.nt.h.kb[lane][e] = kb[e];
+  }
+  wsync();
+  // rows of H: M, then S_j . (Kc_body(i) S_i) on the ancestor dofs j of i
+  load_rows(s.M, h, lane);
+  if (lane < NV) {
+    const int bi = lane < 6 ? 1 : lane - 4;
+    const float* k = s.u.nt.h.kb[bi];
+    const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]}, v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
+    float n[3], f[3];
+    // n = Kaa w + Kal v, f = Kal' w + Kll v
+    n[0] = k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
+    n[1] = k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
+    n[2] = k[4] * w[0] + k[5] * w[1] + k[2] * w[2] + k[12] * v[0] + k[13] * v[1] + k[14] * v[2];
+    f[0] = k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
+    f[1] = k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
+    f[2] = k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
+    const uint64_t anc = cTree.dofanc[lane];
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+      if ((anc >> j) & 1ull)
+        h[j] += s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
+                + s.S[j][6] * f[2];
+    if (R.lsg != 0.f && R.ljar < 0.f) {
+#pragma unroll
+      for (int j = 0; j < NV; j++) if (j == lane) h[j] += R.lD;
+    }
+  }
+  // contacts between two robot bodies: the cross-chain terms -(p2_i p1_j + p1_i p2_j) S_i' K S_j
+  for (unsigned long long m = selfm; m; m &= m - 1ull) {
+    const int c = __builtin_ctzll(m);
+    const float* k = s.u.nt.h.kc[c];
+    const int b1 = __float_as_int(k[21]), b2 = __float_as_int(k[22]);
+    if (lane < NV) {
+      const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]},
+                  v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
+      float* y = s.u.nt.h.y[lane];
+      y[0] = k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
+      y[1] = k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
+      y[2] = k[4] * w[0] + k[5] * w[1] + k[2] * w[2] + k[12] * v[0] + k[13] * v[1] + k[14] * v[2];
+      y[4] = k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
+      y[5] = k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
+      y[6] = k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
+      const unsigned dm = cTree.dofmask32[lane];
+      y[3] = (float)((dm >> b1) & 1u);
+      y[7] = (float)((dm >> b2) & 1u);
+    }
+    wsync();
+    if (lane < NV) {
+      const unsigned dm = cTree.dofmask32[lane];
+      const float p1 = (float)((dm >> b1) & 1u), p2 = (float)((dm >> b2) & 1u);
+      const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]},
+                  v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        if (j <= lane) {
+          const float* y = s.u.nt.h.y[j];
+          const float coef = p2 * y[3] + p1 * y[7];
+          h[j] -= coef * (w[0] * y[0] + w[1] * y[1] + w[2] * y[2] + v[0] * y[4] + v[1] * y[5] + v[2] * y[6]);
+        }
+      }
+    }
+    wsync();
+  }
+}
+
+__device__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con, int iterations) {
+  // warm start against qacc_smooth: keep the cheaper (step.py:1974-1988)
+  refresh(s, R, lane, con);
+  float cost = wsum(lane_cost(s, R, lane));
+  float wq = lane < NV ? s.qacc[lane] : 0.f, wma = lane < NV ? s.Ma[lane] : 0.f, wj[4], wl = R.ljar;
+  for (int t = 0; t < 4; t++) wj[t] = R.jar[t];
+  if (lane < NV) s.qacc[lane] = s.qacc0[lane];
+  wsync();
+  refresh(s, R, lane, con);
+  const float cost0 = wsum(lane_cost(s, R, lane));
+  if (cost0 > cost) {
+    if (lane < NV) { s.qacc[lane] = wq; s.Ma[lane] = wma; }
+    for (int t = 0; t < 4; t++) R.jar[t] = wj[t];
+    R.ljar = wl;
+    wsync();
+  } else {
+    cost = cost0;
+  }
+  newton_grad(s, R, lane, con);
+  int it = 0;
+  bool conv = false, zsame = false;
+  while (it < iterations) {
+    float p;
+    if (zsame) {  // no row changed its zone in the last step: H, and so its factor in s.L, are unchanged
+      p = chol_resolve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
+    } else {
+      float h[NV], dself = 1.f;
+      hessian(s, R, lane, con, h);
+      chol_rows(h, dself, lane);
+      store_rows(h, s.L, lane);
+      wsync();
+      p = chol_solve_rows(h, dself, s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
+    }
+    if (lane < NV) s.p[lane] = p;
+    wsync();
+    // exact line search along p on the piecewise-quadratic cost (step.py:2032-2084)
+    float jv[4], ljv;
+    rows_jv(s, R, s.p, lane, con, jv, &ljv);
+    const float mp = matvec(s, s.p, lane);
+    if (lane < NV) s.Mp[lane] = mp;
+    const float2 aa = wsum2(lane < NV ? (s.Ma[lane] - s.qsm[lane]) * p : 0.f, lane < NV ? p * mp : 0.f);
+    const float a1 = aa.x, a2 = aa.y;
+    float alpha = 0.f, lo = 0.f, hi = 1e30f, d0 = 0.f;
+    unsigned zprev = 0u;
+    bool newton_step = false;
+    for (int k = 0; k <= 40; k++) {
+      float fd = 0.f, fdd = 0.f;
+      unsigned z = 0u;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        if (t < R.nr) {
+          const float x = R.jar[t] + alpha * jv[t];
+          if (x < 0.f) { fd += R.D * x * jv[t]; fdd += R.D * jv[t] * jv[t]; z |= 1u << t; }
+        }
+      }
+      if (R.lsg != 0.f) {
+        const float x = R.ljar + alpha * ljv;
+        if (x < 0.f) { fd += R.lD * x * ljv; fdd += R.lD * ljv * ljv; z |= 16u; }
+      }
+      if (ballot(!(newton_step && z == zprev)) == 0ull) break;  // the Newton step kept every row on its piece
+      if (k == 40) break;
+      const float2 ff = wsum2(fd, fdd);
+      fd = ff.x + a1 + alpha * a2;
+      fdd = ff.y + a2;
+      if (k == 0) { d0 = fd; if (d0 >= 0.f) break; }
+      if (fabsf(fd) <= 1e-7f * fabsf(d0)) break;
+      if (fd < 0.f) lo = alpha; else hi = alpha;
+      float nx = alpha - fd / fdd;
+      newton_step = nx > lo && nx < hi;
+      if (!newton_step) nx = hi < 1e29f ? 0.5f * (lo + hi) : 2.f * fmaxf(alpha, 1e-6f);
+      zprev = z;
+      alpha = nx;
+    }
+    // move along p
+    if (lane < NV) {
+      s.qacc[lane] += alpha * p;
+      s.Ma[lane] += alpha * mp;
+    }
+    bool chg = false;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float xn = R.jar[t] + alpha * jv[t];
+      chg |= t < R.nr && ((R.jar[t] < 0.f) != (xn < 0.f));
+      R.jar[t] = xn;
+    }
+    {
+      const float xn = R.ljar + alpha * ljv;
+      chg |= R.lsg != 0.f && ((R.ljar < 0.f) != (xn < 0.f));
+      R.ljar = xn;
+    }
+    zsame = ballot(chg) == 0ull;
+    wsync();
+    const float newcost = wsum(lane_cost(s, R, lane));
+    const float gn = newton_grad(s, R, lane, con);
+    const float improvement = kScale * (cost - newcost);
+    cost = newcost;
+    it++;
+    conv = improvement < kTol || kScale * gn < kTol;
+    if (conv) break;
+  }
+  return NewtonOut{it, conv};
+}
+
+// ============================================================================================== one substep
+__device__ void substep(Sim& s, Rows& R, int lane, int iterations) {
+  smooth(s, lane);
+  collision(s, lane);
+  const int ncon = s.ncon;
+  const bool con = lane < ncon;
+  // this lane's contact
+  int pair = -1;
+  R.nr = 0; R.b1 = 0; R.b2 = 0; R.dim = 1; R.mu = 0.f; R.D = 0.f;
+  for (int k = 0; k < 3; k++) R.r[k] = 0.f;
+  for (int k = 0; k < 9; k++) R.fr[k] = 0.f;
+  float dist = 0.f;
+  if (con) {
+    const float* st = s.u.col.stage[lane];
+    dist = st[0];
+    for (int k = 0; k < 3; k++) R.r[k] = st[1 + k] - s.O[k];
+    for (int k = 0; k < 9; k++) R.fr[k] = st[4 + k];
+    pair = __float_as_int(st[13]);
+    const unsigned w = cPairW[pair];
+    R.b1 = cGbody[w & 255u];
+    R.b2 = cGbody[(w >> 8) & 255u];
+    R.dim = (w >> 16) & 15u;
+    R.mu = ((w >> 20) & 1u) ? s.fric : cPairMu[pair];
+  }
+  wsync();
+  // limit rows (dof order), then the contacts' rows (contact order) up to the row capacity
+  R.lsg = 0.f; R.lD = 0.f; R.laref = 0.f; R.ljar = 0.f;
+  float lpos = 0.f;
+  if (lane >= 6 && lane < NV) {
+    const float q = s.qpos[lane + 1], dmin = q - cRange[2 * lane], dmax = cRange[2 * lane + 1] - q;
+    if (fminf(dmin, dmax) < 0.f) { R.lsg = dmin < dmax ? 1.f : -1.f; lpos = fminf(dmin, dmax); }
+  }
+  const unsigned long long lm = ballot(R.lsg != 0.f);
+  const int nlim = __popcll(lm);
+  const int nrf = con ? (R.dim == 3 ? 4 : 1) : 0;
+  const int r0 = nlim + wscan_excl(nrf, lane);
+  R.nr = con ? max(0, min(nrf, NEFC - r0)) : 0;
+  const int need = nlim + wsumi(nrf);
+  if (lane == 0) {
+    s.nlim = nlim;
+    s.nefc = need < NEFC ? need : NEFC;
+    if (need > NEFC) s.flags |= 16;
+  }
+  // impedance, D, aref (velocities J qvel from the bodies' velocities)
+  float vdot[3] = {0.f, 0.f, 0.f};
+  body_vel(s, s.qvel, lane);
+  if (con) contact_dots(s, R, vdot);
+  if (R.lsg != 0.f) {
+    float k, b, imp;
+    kbimp(cJSolref.v, cJSolimp.v, lpos, &k, &b, &imp);
+    const float iw = cDinvw[lane];
+    R.lD = 1.f / fmaxf(iw * (1.f - imp) / imp, 1e-15f);
+    R.laref = -k * imp * lpos - b * (R.lsg * s.qvel[lane]);
+  }
+  if (con) {
+    float k, b, imp;
+    kbimp(cPSolref.v, cPSolimp.v, dist, &k, &b, &imp);
+    float iw = cBinvw[R.b1] + cBinvw[R.b2];
+    if (R.dim == 3) iw = (R.mu * R.mu * iw + iw) * 2.f * R.mu * R.mu / kImpratio;
+    R.D = 1.f / fmaxf(iw * (1.f - imp) / imp, 1e-15f);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float sg = (t & 1) ? -1.f : 1.f;
+      const float vel = R.dim == 3 ? vdot[0] + sg * R.mu * vdot[1 + (t >> 1)] : vdot[0];
+      R.aref[t] = -k * imp * dist - b * vel;
+    }
+  } else {
+    for (int t = 0; t < 4; t++) R.aref[t] = 0.f;
+  }
+  wsync();
+  const NewtonOut no = newton(s, R, lane, con, iterations);
+  if (lane == 0) s.niter = no.it;
+  // implicitfast: (M + h kv) a_adv = M a*
+  {
+    float a[NV], dself = 1.f;
+    load_rows(s.M, a, lane);
+#pragma unroll
+    for (int j = 0; j < NV; j++) if (j == lane) a[j] += kH * cKv[lane];
+    chol_rows(a, dself, lane);
+    store_rows(a, s.L, lane);
+    wsync();
+    const float adv = chol_solve_rows(a, dself, s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
+    if (lane < NV) s.qvel[lane] += kH * adv;
+    wsync();
+  }
+  if (lane == 0) {  // the free joint: position, then the orientation rotated by h times the local angular velocity
+    for (int k = 0; k < 3; k++) s.qpos[k] += kH * s.qvel[k];
+    float w[3] = {s.qvel[3], s.qvel[4], s.qvel[5]}, nw = sqrtf(dot3(w, w));
+    if (nw > 0.f) {
+      float sa, ca;
+      sincosf(0.5f * kH * nw, &sa, &ca);
+      float dq[4] = {ca, sa * w[0] / nw, sa * w[1] / nw, sa * w[2] / nw};
+      float q[4] = {s.qpos[3], s.qpos[4], s.qpos[5], s.qpos[6]}, o[4];
+      qmul(q, dq, o);
+      float on = rsqrtf(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
+      for (int k = 0; k < 4; k++) s.qpos[3 + k] = o[k] * on;
+    }
+  }
+  if (lane >= 6 && lane < NV) s.qpos[lane + 1] += kH * s.qvel[lane];
+  (void)pair;
+  wsync();
+}
+
+// one world per wave64 (one workgroup of 64 lanes)
+__global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict__ qpos, const float* __restrict__ qvel,
+                                                const float* __restrict__ warm, const float* __restrict__ ctrl,
+                                                const float* __restrict__ fric, const float* __restrict__ com,
+                                                int iterations, int nsub, float* __restrict__ oqpos,
+                                                float* __restrict__ oqvel, float* __restrict__ owarm,
+                                                int* __restrict__ info) {
+  __shared__ Sim s;
+  const int lane = threadIdx.x;
+  const int w = blockIdx.x;
+  if (w >= nw) return;
+  if (lane < NQ) s.qpos[lane] = qpos[(size_t)w * NQ + lane];
+  if (lane < NV) { s.qvel[lane] = qvel[(size_t)w * NV + lane]; s.qacc[lane] = warm[(size_t)w * NV + lane]; }
+  if (lane < NU) s.ctrl[lane] = ctrl[(size_t)w * NU + lane];
+  if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
+  if (lane == 0) { s.fric = fric[w]; s.flags = 0; s.niter = 0; }
+  wsync();
+  Rows R;
+  for (int k = 0; k < nsub; k++) substep(s, R, lane, iterations);
+  if (lane < NQ) oqpos[(size_t)w * NQ + lane] = s.qpos[lane];
+  if (lane < NV) { oqvel[(size_t)w * NV + lane] = s.qvel[lane]; owarm[(size_t)w * NV + lane] = s.qacc[lane]; }
+  if (lane == 0) {
+    info[4 * w] = s.niter;
+    info[4 * w + 1] = s.ncon_raw;
+    info[4 * w + 2] = s.nefc;
+    info[4 * w + 3] = s.flags;
+  }
+}
+
+}  // namespace g1k
+
+namespace g1k {
+int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
+                   const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
+                   int* info) {
+  if (nw <= 0) return 0;
+  hipLaunchKernelGGL(k_forward, dim3(nw), dim3(64), 0, st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub,
+                     oq, ov, ow, info);
+  return (int)hipGetLastError();
+}
+size_t forward_lds_bytes() { return sizeof(Sim); }
+}  // namespace g1k

@@ -1,0 +1,102 @@
+"""GPU parity of the forward control step (HIP kernels through the C ABI, via nablaengine_amd.torch_ffi) against the
+float64 CPU oracle and MuJoCo C float64 truth (golden fixtures)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from nablaengine_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def ffi():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible")
+    from nablaengine_amd import torch_ffi
+    torch_ffi.init(0)
+    return torch_ffi
+
+
+def _gpu(st):
+    import torch
+    return [torch.from_numpy(np.ascontiguousarray(st[k], np.float32)).cuda()
+            for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+
+
+def _rel(a, b, floor=1e-12):
+    return np.linalg.norm(a - b, axis=1) / np.maximum(np.linalg.norm(b, axis=1), floor)
+
+
+def _golden(cname):
+    z = np.load(os.path.join(GOLD, f"truth_{cname}.npz"))
+    st = dict(qpos=z["qpos"], qvel=z["qvel"], warm=z["qacc_warmstart"], ctrl=z["ctrl"], friction=z["friction"],
+              com=z["com"])
+    return st, z["check_out"], z["model_flags"]
+
+
+@pytest.mark.parametrize("cname", ["mf_s0", "mf_s1", "mf_s2", "mf_s3"])
+def test_forward_vs_mujoco_truth(ffi, cname):
+    """MuJoCo C float64 (2000 iterations) on the truth's check states: median qvel relative error <= 2e-6 (the
+    BASELINE gate), at the engine's 10 iterations and in float32."""
+    import torch
+    st, ref, flags = _golden(cname)
+    q1, v1, w1, info = ffi.forward(*_gpu(st))
+    torch.cuda.synchronize()
+    q1, v1 = q1.cpu().numpy().astype(np.float64), v1.cpu().numpy().astype(np.float64)
+    ev, eq = _rel(v1, ref[:, 36:]), _rel(q1, ref[:, :36])
+    print(f"{cname}: qvel median {np.median(ev):.3g} p90 {np.percentile(ev, 90):.3g} max {ev.max():.3g}; "
+          f"qpos median {np.median(eq):.3g}")
+    assert np.median(ev) <= 2e-6
+    assert np.median(eq) <= 2e-6
+
+
+def test_forward_vs_oracle_synthetic(ffi):
+    """Config-1 states (1024 of them) against the float64 oracle at MuJoCo's truth settings: median relative error of
+    qvel <= 2e-6; and every world finite."""
+    import torch
+    st = synthetic.states(1024, config=1)
+    q1, v1, w1, info = ffi.forward(*_gpu(st))
+    torch.cuda.synchronize()
+    oq, ov, ow, oinfo = oracle.step(**{k: st[k].astype(np.float64) for k in st}, **oracle.TRUTH)
+    v1 = v1.cpu().numpy().astype(np.float64)
+    q1 = q1.cpu().numpy().astype(np.float64)
+    assert np.isfinite(v1).all() and np.isfinite(q1).all()
+    ev, eq = _rel(v1, ov), _rel(q1, oq)
+    print(f"synthetic: qvel median {np.median(ev):.3g} p99 {np.percentile(ev, 99):.3g}; qpos median {np.median(eq):.3g}"
+          f"; contacts max {info[:, 1].max().item()} rows max {info[:, 2].max().item()}")
+    assert np.median(ev) <= 2e-6
+    assert np.median(eq) <= 2e-6
+
+
+def test_forward_bitwise_deterministic(ffi):
+    """Two runs of the same inputs give bitwise the same outputs (no float atomics, fixed reduction orders)."""
+    import torch
+    st = synthetic.states(2048, config=1)
+    a = ffi.forward(*_gpu(st))
+    b = ffi.forward(*_gpu(st))
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_forward_errors(ffi):
+    """Shape / dtype / device errors are TypeError, bad options ValueError, B = 0 empty outputs."""
+    import torch
+    st = _gpu(synthetic.states(4, config=1))
+    with pytest.raises(TypeError):
+        ffi.forward(st[0][:, :35].contiguous(), *st[1:])
+    with pytest.raises(TypeError):
+        ffi.forward(st[0].double(), *st[1:])
+    with pytest.raises(TypeError):
+        ffi.forward(st[0].cpu(), *st[1:])
+    with pytest.raises(ValueError):
+        ffi.forward(*st, substeps=0)
+    e = [x[:0] for x in st]
+    q1, v1, w1, info = ffi.forward(*e)
+    assert q1.shape == (0, 36) and info.shape == (0, 4)
+    torch.cuda.synchronize()
