@@ -1,0 +1,140 @@
+"""Benchmark of the MI355X G1 control step (BASELINE.json metric): ms per 20 ms control step at 4096 worlds and
+world-steps/s, forward (and forward+VJP where the library has the adjoint), on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu]
+
+A step is one control step (4 substeps of 5 ms, Newton 10 iterations) of B worlds of BASELINE config 1 (seeded
+synthetic states, inputs resident in HBM before the timed region). K steps are timed back to back between two
+synchronizations; rank 0 prints one JSON line. `roofline` is the dominant kernel's (the forward): algorithmic flops
+per launch (the float64 CPU restatement's closed-form phase counts on the same inputs, counted once before timing)
+divided by the kernel's average duration from HIP events on the stream it is launched on; peak is MI355X's FP32
+(157.3 TFLOP/s). `cpu_baseline` is the float64 CPU restatement ("port", one thread) on 64 config-0 worlds, repeated
+for about 10 s.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "ms per 20 ms control step @4096 worlds, forward and fwd+VJP; world-steps/s"
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+# interface bytes per world-step (inputs 556 B, outputs 440 B), the design-independent HBM traffic of the forward
+IO_BYTES_FWD = (36 + 35 + 35 + 29 + 1 + 3) * 4 + (36 + 35 + 35) * 4 + 16
+
+
+def cpu_baseline(seconds=10.0):
+    """The float64 CPU restatement (test oracle, one thread) on 64 worlds of config 0: world-steps/s."""
+    import oracle
+    from nablaengine_amd import synthetic
+    st = synthetic.states(64, config=0, dtype=np.float64)
+    oracle.step(**st, **oracle.ENGINE)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.step(**st, **oracle.ENGINE)
+        n += 1
+    dt = time.perf_counter() - t0
+    return dict(value=64 * n / dt, unit="world-steps/s", cores=1, kind="port",
+                sample=f"{n} x 64 config-0 worlds (float64 CPU restatement, not MuJoCo; Newton 10 it, tol 1e-8), "
+                       f"{dt:.1f} s, ms per 64-world step {1e3 * dt / n:.2f}")
+
+
+def algorithmic_flops(st):
+    """Mean algorithmic flops per world-step of these states (closed-form counts of the float64 restatement)."""
+    import oracle
+    r = oracle.step(**{k: v.astype(np.float64) for k, v in st.items()}, **oracle.ENGINE, flops=True)
+    return float(np.mean(r[4]))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--worlds", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--flop-sample", type=int, default=512, help="worlds the flop count is taken on")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (the worlds are independent; a multi-GPU "
+              "run is B/G worlds per GPU with no exchange inside a step)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from nablaengine_amd import synthetic, torch_ffi
+    torch_ffi.init(0)
+    B = a.worlds
+    st = synthetic.states(B, config=1)
+    args = [torch.from_numpy(st[k]).cuda() for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    stream = torch.cuda.current_stream()
+    for _ in range(a.warmup):
+        torch_ffi.forward(*args)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        out = torch_ffi.forward(*args)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / a.steps
+    ms = e0.elapsed_time(e1) / a.steps
+    info = out[3].cpu().numpy()
+    # fwd+VJP
+    vjp_ms = None
+    try:
+        gq, gv = synthetic.cotangents(B)
+        gq, gv = torch.from_numpy(gq).cuda(), torch.from_numpy(gv).cuda()
+        r = torch_ffi.forward(*args, tape=True)
+        torch_ffi.backward(r[4], args[4], args[5], gq, gv)
+        torch.cuda.synchronize()
+        for _ in range(a.warmup):
+            r = torch_ffi.forward(*args, tape=True)
+            torch_ffi.backward(r[4], args[4], args[5], gq, gv)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(a.steps):
+            r = torch_ffi.forward(*args, tape=True)
+            torch_ffi.backward(r[4], args[4], args[5], gq, gv)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        vjp_ms = e0.elapsed_time(e1) / a.steps
+    except RuntimeError:
+        vjp_ms = None
+    sub = {k: v[: a.flop_sample] for k, v in st.items()}
+    fl = algorithmic_flops(sub)
+    achieved = fl * B / (ms * 1e-3) / 1e12
+    res = {
+        "metric": METRIC, "value": B * 1e3 / ms, "unit": "world-steps/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (BASELINE config 1: seeded standing states, random ctrl; model g1_train.mjb)",
+        "config": {"workload": f"G1 control step forward, {B} worlds, 4 x 5 ms substeps, Newton 10 it, implicitfast",
+                   "worlds": B, "substeps": 4, "iterations": 10},
+        "ms_per_step_host_wall": wall,
+        "ms_per_step_fwd_vjp": vjp_ms,
+        "world_steps_per_s_fwd_vjp": None if vjp_ms is None else B * 1e3 / vjp_ms,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_FP32_TFLOPS, "traffic": None,
+                     "note": "FP32 vector (VALU) work, no MFMA: achieved = closed-form algorithmic flops "
+                             f"({fl:.3g} per world-step, float64 restatement on {len(sub['qpos'])} of the worlds) x "
+                             "worlds / the forward kernel's mean duration (HIP events, its stream); one kernel "
+                             "launch per step"},
+        "roofline_hbm": {"achieved": IO_BYTES_FWD * B / (ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": IO_BYTES_FWD * B / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                         "note": f"interface bytes {IO_BYTES_FWD} per world-step"},
+        "capacity": {"contacts_max": int(info[:, 1].max()), "rows_max": int(info[:, 2].max()),
+                     "overflow_worlds": int(((info[:, 3] & 20) != 0).sum())},
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -40,8 +40,11 @@ def lib():
         dp = ctypes.POINTER(ctypes.c_double)
         ip = ctypes.POINTER(ctypes.c_int)
         L.g1o_step.argtypes = [ctypes.c_int, dp, dp, dp, dp, dp, dp, ctypes.c_int, ctypes.c_double, ctypes.c_int,
-                               ctypes.c_double, ctypes.c_int, dp, dp, dp, ip]
+                               ctypes.c_double, ctypes.c_int, dp, dp, dp, ip, dp]
         L.g1o_smooth.argtypes = [dp] * 9
+        L.g1o_vjp.argtypes = [ctypes.c_int, dp, dp, dp, dp, dp, dp, ctypes.c_int, ctypes.c_double, ctypes.c_int,
+                              ctypes.c_double, ctypes.c_int, dp, dp, ctypes.c_int, ctypes.c_int, ctypes.c_double, dp, dp,
+                              dp]
         L.g1o_contacts.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp]
         _lib = L
     return _lib
@@ -61,18 +64,62 @@ ENGINE = dict(iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7)
 TRUTH = dict(iterations=2000, tol=1e-13, ls_max=100, ls_tol=1e-12)
 
 
-def step(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4):
-    """One control step of B worlds in float64: (qpos' (B, 36), qvel' (B, 35), warm' (B, 35), info (B, 4) int32)."""
+def step(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4,
+         flops=False):
+    """One control step of B worlds in float64: (qpos' (B, 36), qvel' (B, 35), warm' (B, 35), info (B, 4) int32),
+    and with flops=True the algorithmic flops of each world-step (B,) last."""
     qpos = _c(qpos, (-1, NQ))
     B = qpos.shape[0]
     qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
     friction, com = _c(friction, (B,)), _c(com, (B, 3))
     oq, ov, ow = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NV))
     info = np.empty((B, 4), np.int32)
+    fl = np.empty(B)
     lib().g1o_step(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
                    int(ls_max), float(ls_tol), int(nsub), _p(oq), _p(ov), _p(ow),
-                   info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
-    return oq, ov, ow, info
+                   info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), _p(fl))
+    return (oq, ov, ow, info, fl) if flops else (oq, ov, ow, info)
+
+
+def vjp(qpos, qvel, warm, ctrl, friction, com, g_qpos, g_qvel, clamp_kv=1, normal=0, clamp_soft=0.2, iterations=10,
+        tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4):
+    """Analytic VJP of one control step in float64 (the oracle's adjoint): (g_qpos (B, 36) qpos form, g_qvel (B, 35),
+    g_ctrl (B, 29)) from the output cotangents (g_qpos' (B, 36) qpos form, g_qvel' (B, 35))."""
+    qpos = _c(qpos, (-1, NQ))
+    B = qpos.shape[0]
+    qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
+    friction, com = _c(friction, (B,)), _c(com, (B, 3))
+    gq, gv = _c(g_qpos, (B, NQ)), _c(g_qvel, (B, NV))
+    oq, ov, ou = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NU))
+    lib().g1o_vjp(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
+                  int(ls_max), float(ls_tol), int(nsub), _p(gq), _p(gv), int(clamp_kv), int(normal), float(clamp_soft),
+                  _p(oq), _p(ov), _p(ou))
+    return oq, ov, ou
+
+
+def fd_jacobian(qpos, qvel, warm, ctrl, friction, com, h=1e-6, **kw):
+    """Central-difference Jacobian of one state's control step (71 outputs: qpos' 36 | qvel' 35) in the columns
+    (qpos tangent 35 | qvel 35 | ctrl 29), qpos perturbed with integrate_pos (benchmarks/bench/truth/fdlib.py fd_job's
+    construction)."""
+    q0, v0, u0 = (np.asarray(x, np.float64) for x in (qpos, qvel, ctrl))
+    Q, V, U = [], [], []
+    for j in range(2 * NV + NU):
+        for sg in (1.0, -1.0):
+            q, v, u = q0.copy(), v0.copy(), u0.copy()
+            if j < NV:
+                d = np.zeros(NV)
+                d[j] = sg * h
+                q = integrate_pos(q0, d)
+            elif j < 2 * NV:
+                v[j - NV] += sg * h
+            else:
+                u[j - 2 * NV] += sg * h
+            Q.append(q); V.append(v); U.append(u)
+    n = len(Q)
+    oq, ov, _, _ = step(np.array(Q), np.array(V), np.tile(warm, (n, 1)), np.array(U), np.full(n, float(friction)),
+                        np.tile(com, (n, 1)), **kw)
+    out = np.concatenate([oq, ov], 1).reshape(2 * NV + NU, 2, NQ + NV)
+    return (out[:, 0] - out[:, 1]).T / (2 * h)
 
 
 def smooth(qpos, qvel, ctrl, com):

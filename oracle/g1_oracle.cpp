@@ -47,6 +47,10 @@ struct World {
   int nefc, nlim;
   double efcJ[NEFC][NV], efcD[NEFC], aref[NEFC];
   int niter;
+  double Ib[NB][10];  // each body's own spatial inertia about O (before the subtree sums)
+  double aadv[NV];    // implicitfast's a_adv of the last substep
+  bool clamped[NV];   // dofs whose actuator force is at its limit
+  double flops;  // algorithmic flops of the world-step so far (the closed-form phase counts, see count_* below)
 };
 
 inline void qmul(const double* a, const double* b, double* o) {
@@ -202,7 +206,11 @@ void smooth(World& s, const double* ctrl) {
   for (int k = 0; k < 3; k++) s.X[0][k] = s.W[0][k] = s.V[0][k] = s.AL[0][k] = s.A[0][k] = 0;
   for (int b = 1; b < NB; b++) fwd_body(s, b, zero);  // bodies are in topological order
   for (int k = 0; k < 3; k++) s.O[k] = s.X[1][k];
-  for (int b = 1; b < NB; b++) { body_force(s, b); body_inertia(s, b); }
+  for (int b = 1; b < NB; b++) {
+    body_force(s, b);
+    body_inertia(s, b);
+    std::memcpy(s.Ib[b], s.Jc[b], sizeof(s.Ib[b]));
+  }
   for (int b = NB - 1; b >= 2; b--) {  // subtree sums (children have larger indices)
     int p = BODY_PARENT[b];
     double r[3], u[3];
@@ -256,6 +264,9 @@ void smooth(World& s, const double* ctrl) {
     if (i >= 6) {
       act = DOF_KP[i] * (ctrl[i - 6] - s.qpos[i + 1]) - DOF_KV[i] * s.qvel[i];
       act = std::fmin(std::fmax(act, -DOF_FRCLIM[i]), DOF_FRCLIM[i]);
+      s.clamped[i] = act <= -DOF_FRCLIM[i] || act >= DOF_FRCLIM[i];
+    } else {
+      s.clamped[i] = false;
     }
     s.qsm[i] = act - bias[i];
   }
@@ -449,6 +460,16 @@ void kbimp(const double* solref, const double* solimp, double pos, double h, dou
   }
 }
 
+// support size k_c of a contact: the dofs on exactly one of its bodies' chains
+int support_size(const Contact& c) {
+  int k = 0;
+  for (int i = 0; i < NV; i++) {
+    int bi = DOF_BODY[i];
+    k += ((BODY_ANCMASK[c.b1] >> bi) & 1u) != ((BODY_ANCMASK[c.b2] >> bi) & 1u);
+  }
+  return k;
+}
+
 void rows(World& s) {
   const double h = TIMESTEP;
   int r = 0;
@@ -489,6 +510,7 @@ void rows(World& s) {
     if (ct.dim == 3) iw = (mu * mu * iw + iw) * 2 * mu * mu / IMPRATIO;  // contact_invw (step.py:1181-1185)
     double D = 1.0 / std::fmax(iw * (1 - imp) / imp, 1e-15);
     int nr = ct.dim == 3 ? 4 : 1;
+    s.flops += 200.0 + 25.0 * support_size(ct) + 60.0 * nr;  // narrowphase, Jacobian, rows of one contact
     for (int t = 0; t < nr; t++) {
       if (r >= NEFC) { s.flags |= 16; break; }
       double sg = (t & 1) ? -1 : 1;
@@ -559,7 +581,28 @@ void newton(World& s, int iterations, double tol, int ls_max, double ls_tol) {
   v.gradient();
   int it = 0;
   static thread_local double H[NV][NV];
+  int ksum = 0;
+  for (int c = 0; c < s.ncon; c++) ksum += support_size(s.con[c]);
+  bool zsame = false;
   while (it < iterations) {
+    // algorithmic flops of the iteration (closed form): Hessian assembly over the contacts with a quadratic row and a
+    // factorization (or a re-solve with the kept factor when no row changed its zone), J p and J' f over the supports,
+    // M p; the line search's 6 R flops per evaluation are added below
+    if (!zsame) {
+      int r = s.nlim;
+      for (int c = 0; c < s.ncon; c++) {
+        int nr = s.con[c].dim == 3 ? 4 : 1;
+        bool act = false;
+        for (int t = 0; t < nr && r + t < s.nefc; t++) act |= v.jar[r + t] < 0;
+        r += nr;
+        int k = support_size(s.con[c]);
+        if (act) s.flops += 6.0 * k * (k + 1) / 2 + 12.0 * k;
+      }
+      s.flops += 2.86e4;
+    } else {
+      s.flops += 2.45e3;
+    }
+    s.flops += 12.0 * ksum + 2.45e3;
     for (int i = 0; i < NV; i++)
       for (int j = 0; j < NV; j++) H[i][j] = s.M[i][j];
     for (int r = 0; r < s.nefc; r++) {
@@ -583,6 +626,7 @@ void newton(World& s, int iterations, double tol, int ls_max, double ls_tol) {
     bool zprev_valid = false;
     static thread_local unsigned char zprev[NEFC], z[NEFC];
     for (int k = 0; k <= ls_max; k++) {
+      s.flops += 6.0 * s.nefc;
       double fd = 0, fdd = 0;
       for (int r = 0; r < s.nefc; r++) {
         double x = v.jar[r] + alpha * jv[r];
@@ -604,7 +648,13 @@ void newton(World& s, int iterations, double tol, int ls_max, double ls_tol) {
       alpha = nx;
     }
     for (int i = 0; i < NV; i++) { s.qacc[i] += alpha * p[i]; v.Ma[i] += alpha * Mp[i]; }
-    for (int r = 0; r < s.nefc; r++) v.jar[r] += alpha * jv[r];
+    bool chg = false;
+    for (int r = 0; r < s.nefc; r++) {
+      double xn = v.jar[r] + alpha * jv[r];
+      chg |= (v.jar[r] < 0) != (xn < 0);
+      v.jar[r] = xn;
+    }
+    zsame = !chg;
     double newcost = v.cost(s.qacc);
     double gn = v.gradient();
     double improvement = scale * (cost - newcost);
@@ -627,6 +677,7 @@ void integrate(World& s) {
     Q[i][i] += h * DOF_KV[i];
   }
   chol_solve(Q, Ma, adv);
+  std::memcpy(s.aadv, adv, sizeof(adv));
   for (int i = 0; i < NV; i++) s.qvel[i] += h * adv[i];
   for (int k = 0; k < 3; k++) s.qpos[k] += h * s.qvel[k];
   double w[3] = {s.qvel[3], s.qvel[4], s.qvel[5]}, nw = std::sqrt(dot3(w, w));
@@ -641,6 +692,495 @@ void integrate(World& s) {
   for (int i = 6; i < NV; i++) s.qpos[i + 1] += h * s.qvel[i];
 }
 
+
+// ---------------------------------------------------------------------------------------------- adjoint (float64)
+// The VJP of a control step, restated in spatial algebra about the fixed point O (the root origin at the substep's
+// input state). Per substep, in reverse: the integrator's VJP in the tangent space (root rotation q (+) exp(h w' / 2):
+// t = R(dq) t', w' bar += h J_r(h w')' t'), y = Q^-1 a_adv bar with Q = M + h kv, a* bar = a_adv bar - h kv y, the
+// IFT of Newton's optimum lambda = H^-1 a* bar (H at the final zones), then the gradient of
+//   Psi(q, v) = y' M(q) a~ - lambda' [RNE(q, v, a*) - f_act(q, v, u) + sum_active D_r J_r' (J_r a* - aref_r)]
+// (a~ = a* - a_adv). The derivative of a term in q_j follows from moving the subtree of dof j rigidly by its motion
+// subspace S_j: quantities attached to that subtree change covariantly, the others (the joint's outside: parent body,
+// gravity) do not, so every q-derivative is a subtree sum of force vectors dotted with S_j plus terms with the joint's
+// outside quantities. Contacts enter as wrenches (pose cotangents of the collision primitives, and the change of the
+// bodies' twists at the contact point); limit rows through their distance.
+struct Sv { double w[3], v[3]; };  // a spatial vector (motion: angular, linear at O; force: moment about O, force)
+
+inline Sv sv0() { Sv r; for (int k = 0; k < 3; k++) r.w[k] = r.v[k] = 0; return r; }
+inline Sv sv_add(const Sv& a, const Sv& b, double s = 1) {
+  Sv r;
+  for (int k = 0; k < 3; k++) { r.w[k] = a.w[k] + s * b.w[k]; r.v[k] = a.v[k] + s * b.v[k]; }
+  return r;
+}
+inline Sv sv_scale(const Sv& a, double s) { return sv_add(sv0(), a, s); }
+inline double sv_dot(const Sv& m, const Sv& f) { return dot3(m.w, f.w) + dot3(m.v, f.v); }
+inline Sv cross_mm(const Sv& x, const Sv& y) {  // motion x motion
+  Sv r;
+  double a[3], b[3];
+  cross(x.w, y.w, r.w);
+  cross(x.w, y.v, a);
+  cross(x.v, y.w, b);
+  for (int k = 0; k < 3; k++) r.v[k] = a[k] + b[k];
+  return r;
+}
+inline Sv cross_mf(const Sv& x, const Sv& f) {  // motion x* force
+  Sv r;
+  double a[3], b[3];
+  cross(x.w, f.w, a);
+  cross(x.v, f.v, b);
+  for (int k = 0; k < 3; k++) r.w[k] = a[k] + b[k];
+  cross(x.w, f.v, r.v);
+  return r;
+}
+inline Sv inertia_apply(const double* J, const Sv& x) {
+  Sv r;
+  apply_inertia(J, x.w, x.v, r.w, r.v);
+  return r;
+}
+inline Sv dof_sv(const World& s, int d) {
+  Sv r;
+  for (int k = 0; k < 3; k++) { r.w[k] = s.S[d][k]; r.v[k] = s.S[d][3 + k]; }
+  return r;
+}
+inline bool in_sub(int b, int root) { return b > 0 && ((BODY_ANCMASK[b] >> root) & 1u); }  // b in root's subtree
+
+// chain twists: W[b] = sum over the dofs d moving b of S_d w_d
+void chain_twists(const World& s, const double* w, Sv* W) {
+  for (int b = 0; b < NB; b++) {
+    W[b] = sv0();
+    if (b == 0) continue;
+    for (int d = 0; d < NV; d++)
+      if ((BODY_ANCMASK[b] >> DOF_BODY[d]) & 1u) W[b] = sv_add(W[b], dof_sv(s, d), w[d]);
+  }
+}
+
+// impedance and its derivative in the distance: imp, dimp / dpos (kbimp's curve; 0 where clamped)
+void imp_d(const double* solimp, double pos, double* imp, double* dimp) {
+  double dmin = std::fmin(std::fmax(solimp[0], 1e-4), 0.9999), dmax = std::fmin(std::fmax(solimp[1], 1e-4), 0.9999);
+  double width = std::fmax(1e-15, solimp[2]), mid = std::fmin(std::fmax(solimp[3], 1e-4), 0.9999);
+  double x = std::fabs(pos) / width, sg = pos < 0 ? -1.0 : 1.0;
+  *dimp = 0;
+  if (x <= 0) { *imp = dmin; return; }
+  if (x >= 1) { *imp = dmax; return; }
+  double y, dy;
+  if (x <= mid) { y = x * x / mid; dy = 2 * x / mid; }
+  else { y = 1 - (1 - x) * (1 - x) / (1 - mid); dy = 2 * (1 - x) / (1 - mid); }
+  double v = dmin + y * (dmax - dmin);
+  if (v < dmin || v > dmax) { *imp = std::fmin(std::fmax(v, dmin), dmax); return; }
+  *imp = v;
+  *dimp = dy * (dmax - dmin) * sg / width;
+}
+
+// the normal derivative's factor kappa(nu) (1 / nu exact; the reference's options 1-3: frozen, regularized, frozen
+// below 1e-3 m)
+double kappa(double nu, int normal) {
+  const double eps = 1e-3;
+  if (normal == 0) return 1.0 / nu;
+  if (normal == 1) return 0.0;
+  if (normal == 2) return 1.0 / std::fmax(nu, eps);
+  return nu < eps ? 0.0 : 1.0 / nu;
+}
+
+// make_frame VJP: cotangents of the frame rows (n, b, c) -> n bar
+void make_frame_vjp(const double* n, const double* frb, double* nb) {
+  double e[3] = {0, 0, 0};
+  if (-0.5 < n[1] && n[1] < 0.5) e[1] = 1; else e[2] = 1;
+  double ne = dot3(n, e), b0[3];
+  for (int k = 0; k < 3; k++) b0[k] = e[k] - n[k] * ne;
+  double bl = std::sqrt(dot3(b0, b0)), b[3];
+  for (int k = 0; k < 3; k++) b[k] = b0[k] / bl;
+  const double* cbar = frb + 6;
+  double bbar[3], t[3];
+  cross(b, cbar, t);  // c = n x b: n bar += b x c bar, b bar += c bar x n
+  for (int k = 0; k < 3; k++) nb[k] += frb[k] + t[k];
+  cross(cbar, n, t);
+  for (int k = 0; k < 3; k++) bbar[k] = frb[3 + k] + t[k];
+  double bb = dot3(b, bbar), b0bar[3];
+  for (int k = 0; k < 3; k++) b0bar[k] = (bbar[k] - b[k] * bb) / bl;
+  double nb0 = dot3(n, b0bar);
+  for (int k = 0; k < 3; k++) nb[k] += -ne * b0bar[k] - nb0 * e[k];
+}
+
+// sphere core VJP: (dist, pos, n) = sphere_sphere(p1, r1, p2, r2) with cotangents db, posb, nb -> p1b, p2b
+void sphere_core_vjp(const double* p1, double r1, const double* p2, double r2, double db, const double* posb,
+                     const double* nb, int normal, double* p1b, double* p2b) {
+  double dl[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
+  double l = std::sqrt(dot3(dl, dl));
+  double dlb[3] = {0, 0, 0};
+  for (int k = 0; k < 3; k++) { p1b[k] += posb[k]; dlb[k] += 0.5 * posb[k]; }
+  if (l > 0) {
+    double n[3] = {dl[0] / l, dl[1] / l, dl[2] / l}, nt[3];
+    for (int k = 0; k < 3; k++) nt[k] = nb[k] + 0.5 * (r1 - r2) * posb[k];
+    double nn = dot3(n, nt), kap = kappa(l, normal);
+    for (int k = 0; k < 3; k++) dlb[k] += kap * (nt[k] - n[k] * nn) + n[k] * db;
+  }
+  for (int k = 0; k < 3; k++) { p1b[k] -= dlb[k]; p2b[k] += dlb[k]; }
+}
+
+// geometry VJP of contact c: cotangents of (dist, pos, frame) -> world position / rotation cotangents of its geoms
+void contact_geom_vjp(const World& s, const Contact& c, double db, const double* posb, const double* frb, int normal,
+                      double* x1b, double* t1b, double* x2b, double* t2b) {
+  int g1 = PAIR_G1[c.pair], g2 = PAIR_G2[c.pair], ty1 = GEOM_TYPE[g1], ty2 = GEOM_TYPE[g2];
+  const double *p1 = s.gx[g1], *q1 = s.gq[g1], *p2 = s.gx[g2], *q2 = s.gq[g2];
+  const double *sz1 = GEOM_SIZE + 3 * g1, *sz2 = GEOM_SIZE + 3 * g2;
+  for (int k = 0; k < 3; k++) x1b[k] = t1b[k] = x2b[k] = t2b[k] = 0;
+  if (ty1 == 0) {  // the floor: n constant; pos = ce - n (r + d / 2), d = (ce - p1) . n - r
+    double n[3];
+    zaxis(q1, n);
+    double ceb[3], pn = dot3(n, posb);
+    for (int k = 0; k < 3; k++) ceb[k] = posb[k] - 0.5 * n[k] * pn + n[k] * db;
+    if (ty2 == 2) {
+      for (int k = 0; k < 3; k++) x2b[k] += ceb[k];
+    } else {
+      double axis[3], axb[3] = {0, 0, 0};
+      zaxis(q2, axis);
+      double sg = c.slot == 0 ? 1 : -1;
+      for (int k = 0; k < 3; k++) { x2b[k] += ceb[k]; axb[k] += sg * sz2[1] * ceb[k]; }
+      // plane_capsule_frame: b = normalize(axis - n (n . axis)) when that is >= 0.5 long
+      double na = dot3(n, axis), b0[3];
+      for (int k = 0; k < 3; k++) b0[k] = axis[k] - n[k] * na;
+      double bn = std::sqrt(dot3(b0, b0));
+      if (bn >= 0.5) {
+        double b[3], bbar[3], t[3];
+        for (int k = 0; k < 3; k++) b[k] = b0[k] / bn;
+        cross(frb + 6, n, t);  // c = n x b: b bar += c bar x n
+        for (int k = 0; k < 3; k++) bbar[k] = frb[3 + k] + t[k];
+        double bb = dot3(b, bbar), b0b[3];
+        for (int k = 0; k < 3; k++) b0b[k] = (bbar[k] - b[k] * bb) / bn;
+        double nb0 = dot3(n, b0b);
+        for (int k = 0; k < 3; k++) axb[k] += b0b[k] - n[k] * nb0;
+      }
+      cross(axis, axb, t2b);  // a rotation dth of the capsule moves its axis by dth x axis
+    }
+    return;
+  }
+  double nb[3] = {0, 0, 0};
+  make_frame_vjp(c.frame, frb, nb);
+  if (ty1 == 2 && ty2 == 2) {
+    sphere_core_vjp(p1, sz1[0], p2, sz2[0], db, posb, nb, normal, x1b, x2b);
+    return;
+  }
+  if (ty1 == 2 && ty2 == 3) {
+    double axis[3], a[3], ab[3], ap[3], pt[3];
+    zaxis(q2, axis);
+    for (int k = 0; k < 3; k++) { a[k] = p2[k] - axis[k] * sz2[1]; ab[k] = 2 * axis[k] * sz2[1]; ap[k] = p1[k] - a[k]; }
+    double gam = dot3(ab, ab) + 1e-6, raw = dot3(ap, ab) / gam, t = std::fmin(std::fmax(raw, 0.0), 1.0);
+    for (int k = 0; k < 3; k++) pt[k] = a[k] + t * ab[k];
+    double ptb[3] = {0, 0, 0};
+    sphere_core_vjp(p1, sz1[0], pt, sz2[0], db, posb, nb, normal, x1b, ptb);
+    double abb[3], apb[3] = {0, 0, 0}, axb[3], tb = dot3(ptb, ab);
+    for (int k = 0; k < 3; k++) abb[k] = t * ptb[k];
+    double ab_a[3];
+    for (int k = 0; k < 3; k++) ab_a[k] = ptb[k];  // a bar
+    if (raw > 0 && raw < 1) {
+      for (int k = 0; k < 3; k++) { apb[k] += tb * ab[k] / gam; abb[k] += tb * ap[k] / gam - tb * raw / gam * 2 * ab[k]; }
+    }
+    for (int k = 0; k < 3; k++) { x1b[k] += apb[k]; ab_a[k] -= apb[k]; }
+    for (int k = 0; k < 3; k++) { x2b[k] += ab_a[k]; axb[k] = -sz2[1] * ab_a[k] + 2 * sz2[1] * abb[k]; }
+    cross(axis, axb, t2b);
+    return;
+  }
+  // capsule-capsule: x1, x2 from the segments' normal equations with the forward's clamp cascade
+  double z1[3], z2[3], a1[3], a2[3], d[3];
+  zaxis(q1, z1);
+  zaxis(q2, z2);
+  const double h1 = sz1[1], h2 = sz2[1];
+  for (int k = 0; k < 3; k++) { a1[k] = z1[k] * h1; a2[k] = z2[k] * h2; d[k] = p1[k] - p2[k]; }
+  double ma = dot3(a1, a1), mb = -dot3(a1, a2), mc = dot3(a2, a2), u = -dot3(a1, d), v = dot3(a2, d);
+  double det = ma * mc - mb * mb;
+  double x1, x2;
+  int mode;  // 0 both free, 1 x1 fixed (x2 free), 2 x2 fixed (x1 free), 3 both fixed
+  if (std::fabs(det) >= 1e-15) {
+    x1 = (mc * u - mb * v) / det; x2 = (ma * v - mb * u) / det;
+    mode = 0;
+    if (x1 > 1) { x1 = 1; x2 = (v - mb) / mc; mode = 1; }
+    else if (x1 < -1) { x1 = -1; x2 = (v + mb) / mc; mode = 1; }
+    if (x2 > 1 || x2 < -1) {
+      bool hi = x2 > 1;
+      x2 = hi ? 1 : -1;
+      double raw = hi ? (u - mb) / ma : (u + mb) / ma;
+      x1 = std::fmin(std::fmax(raw, -1.0), 1.0);
+      mode = (raw >= -1 && raw < 1) ? 2 : 3;
+    }
+  } else {
+    int e = c.slot;
+    if (e < 2) {
+      x1 = e == 0 ? 1 : -1;
+      double raw = e == 0 ? (v - mb) / mc : (v + mb) / mc;
+      x2 = std::fmin(std::fmax(raw, -1.0), 1.0);
+      mode = (raw >= -1 && raw < 1) ? 1 : 3;
+    } else {
+      x2 = e == 2 ? 1 : -1;
+      double raw = e == 2 ? (u - mb) / ma : (u + mb) / ma;
+      x1 = std::fmin(std::fmax(raw, -1.0), 1.0);
+      mode = (raw >= -1 && raw < 1) ? 2 : 3;
+    }
+  }
+  double v1[3], v2[3], v1b[3] = {0, 0, 0}, v2b[3] = {0, 0, 0};
+  for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
+  sphere_core_vjp(v1, sz1[0], v2, sz2[0], db, posb, nb, normal, v1b, v2b);
+  double a1b[3], a2b[3], db3[3] = {0, 0, 0};
+  for (int k = 0; k < 3; k++) { x1b[k] += v1b[k]; x2b[k] += v2b[k]; a1b[k] = x1 * v1b[k]; a2b[k] = x2 * v2b[k]; }
+  double x1bar = dot3(a1, v1b), x2bar = dot3(a2, v2b);
+  // near-parallel rule (normal options != 0): both parameters held where sin^2(theta) < 1.2e-3
+  if (mode == 0 && normal != 0) {
+    double cr[3];
+    cross(a1, a2, cr);
+    if (dot3(cr, cr) < 1.2e-3 * ma * mc) { x1bar = 0; x2bar = 0; }
+  }
+  double mab = 0, mbb = 0, mcb = 0, ub = 0, vb = 0;
+  if (mode == 0) {
+    double N1b = x1bar / det, N2b = x2bar / det, detb = -x1bar * x1 / det - x2bar * x2 / det;
+    mcb += N1b * u; ub += N1b * mc; mbb -= N1b * v; vb -= N1b * mb;
+    mab += N2b * v; vb += N2b * ma; mbb -= N2b * u; ub -= N2b * mb;
+    mab += detb * mc; mcb += detb * ma; mbb -= 2 * mb * detb;
+  } else if (mode == 1) {  // x2 = (v - mb x1) / mc
+    vb += x2bar / mc; mbb -= x2bar * x1 / mc; mcb -= x2bar * x2 / mc;
+  } else if (mode == 2) {  // x1 = (u - mb x2) / ma
+    ub += x1bar / ma; mbb -= x1bar * x2 / ma; mab -= x1bar * x1 / ma;
+  }
+  for (int k = 0; k < 3; k++) {
+    a1b[k] += 2 * mab * a1[k] - mbb * a2[k] - ub * d[k];
+    a2b[k] += 2 * mcb * a2[k] - mbb * a1[k] + vb * d[k];
+    db3[k] += -ub * a1[k] + vb * a2[k];
+  }
+  for (int k = 0; k < 3; k++) { x1b[k] += db3[k]; x2b[k] -= db3[k]; a1b[k] *= h1; a2b[k] *= h2; }
+  cross(z1, a1b, t1b);
+  cross(z2, a2b, t2b);
+}
+
+struct Rec { double qpos[NQ], qvel[NV], astar[NV], aadv[NV]; };
+
+// one substep's VJP: (qb tangent, vb) of its output -> of its input; ub accumulates the ctrl gradient
+void substep_vjp(World& s, const Rec& rec, const double* ctrl, double* qb, double* vb, double* ub, int clamp_kv,
+                 int normal, double clamp_soft) {
+  const double h = TIMESTEP;
+  std::memcpy(s.qpos, rec.qpos, sizeof(rec.qpos));
+  std::memcpy(s.qvel, rec.qvel, sizeof(rec.qvel));
+  smooth(s, ctrl);
+  collision(s);
+  rows(s);
+  const double* as = rec.astar;
+  // 1. integrator: v' = v + h a_adv, q' = q (+) h v'
+  double vt[NV], qn[NV];
+  for (int i = 0; i < NV; i++) { vt[i] = vb[i]; qn[i] = qb[i]; }
+  for (int i = 0; i < 3; i++) vt[i] += h * qb[i];
+  for (int i = 6; i < NV; i++) vt[i] += h * qb[i];
+  {
+    double w[3], phi[3];
+    for (int k = 0; k < 3; k++) { w[k] = rec.qvel[3 + k] + h * rec.aadv[3 + k]; phi[k] = h * w[k]; }
+    double th = std::sqrt(dot3(phi, phi));
+    double dq[4];
+    if (th > 0) {
+      double sn = std::sin(0.5 * th) / th;
+      dq[0] = std::cos(0.5 * th); dq[1] = sn * phi[0]; dq[2] = sn * phi[1]; dq[3] = sn * phi[2];
+    } else { dq[0] = 1; dq[1] = dq[2] = dq[3] = 0; }
+    double t[3] = {qb[3], qb[4], qb[5]}, rt[3];
+    qrot(dq, t, rt);  // t = R(dq) t'
+    for (int k = 0; k < 3; k++) qn[3 + k] = rt[k];
+    // J_r(phi)' t' = t' + c1 phi x t' + c2 phi x (phi x t')  (J_r = I - c1 [phi] + c2 [phi]^2)
+    double c1, c2;
+    if (th < 1e-4) { c1 = 0.5 - th * th / 24; c2 = 1.0 / 6 - th * th / 120; }
+    else { c1 = (1 - std::cos(th)) / (th * th); c2 = (th - std::sin(th)) / (th * th * th); }
+    double pt[3], ppt[3];
+    cross(phi, t, pt);
+    cross(phi, pt, ppt);
+    for (int k = 0; k < 3; k++) vt[3 + k] += h * (t[k] + c1 * pt[k] + c2 * ppt[k]);
+  }
+  // 2. implicitfast: y = Q^-1 a_adv bar, a* bar = a_adv bar - h kv y
+  static thread_local double Qm[NV][NV], H[NV][NV];
+  double aab[NV], y[NV], asb[NV], lam[NV], at[NV];
+  for (int i = 0; i < NV; i++) {
+    aab[i] = h * vt[i];
+    for (int j = 0; j < NV; j++) Qm[i][j] = s.M[i][j];
+    Qm[i][i] += h * DOF_KV[i];
+  }
+  chol_solve(Qm, aab, y);
+  for (int i = 0; i < NV; i++) { asb[i] = aab[i] - h * DOF_KV[i] * y[i]; at[i] = as[i] - rec.aadv[i]; }
+  // 3. IFT: lambda = H^-1 a* bar, H = M + J' D J on the rows with J a* - aref < 0
+  double jar[NEFC];
+  for (int r = 0; r < s.nefc; r++) {
+    double a = 0;
+    for (int i = 0; i < NV; i++) a += s.efcJ[r][i] * as[i];
+    jar[r] = a - s.aref[r];
+  }
+  for (int i = 0; i < NV; i++)
+    for (int j = 0; j < NV; j++) H[i][j] = s.M[i][j];
+  for (int r = 0; r < s.nefc; r++)
+    if (jar[r] < 0)
+      for (int i = 0; i < NV; i++)
+        for (int j = 0; j < NV; j++) H[i][j] += s.efcD[r] * s.efcJ[r][i] * s.efcJ[r][j];
+  chol_solve(H, asb, lam);
+  // 4. gradients of Psi
+  double gq[NV] = {0}, gv[NV] = {0};
+  static thread_local Sv V[NB], Lm[NB], Yt[NB], Aw[NB], A1[NB], A2[NB];
+  chain_twists(s, s.qvel, V);
+  chain_twists(s, lam, Lm);
+  chain_twists(s, y, Yt);
+  chain_twists(s, as, Aw);
+  chain_twists(s, at, A2);
+  Sv grav = sv0();
+  for (int k = 0; k < 3; k++) grav.v[k] = -GRAVITY[k];
+  for (int b = 1; b < NB; b++) {  // RNE acceleration: gravity, S a*, and V_c(d) x S_d v_d for the non-translation dofs
+    A1[b] = sv_add(grav, Aw[b]);
+    for (int d = 3; d < NV; d++)
+      if ((BODY_ANCMASK[b] >> DOF_BODY[d]) & 1u) A1[b] = sv_add(A1[b], cross_mm(V[DOF_BODY[d]], dof_sv(s, d)), s.qvel[d]);
+  }
+  // per-body force vectors; Psi's contact wrenches
+  static thread_local Sv f1[NB], P[NB], Qs[NB], Rs[NB], Ts[NB], f2[NB], P2[NB], E[NB], OL[NB], OA[NB], OV[NB], G[NB];
+  for (int b = 0; b < NB; b++) {
+    f1[b] = P[b] = Qs[b] = Rs[b] = Ts[b] = f2[b] = P2[b] = E[b] = OL[b] = OA[b] = OV[b] = G[b] = sv0();
+    if (b == 0) continue;
+    const double* I = s.Ib[b];
+    Sv IV = inertia_apply(I, V[b]), IL = inertia_apply(I, Lm[b]);
+    f1[b] = sv_add(inertia_apply(I, A1[b]), cross_mf(V[b], IV));
+    P[b] = IL;
+    Qs[b] = cross_mf(V[b], IL);
+    Rs[b] = cross_mf(Lm[b], IV);
+    Ts[b] = inertia_apply(I, cross_mm(V[b], Lm[b]));
+    f2[b] = inertia_apply(I, A2[b]);
+    P2[b] = inertia_apply(I, Yt[b]);
+  }
+  // limit rows
+  int r = 0;
+  for (int i = 6; i < NV; i++) {
+    double q = s.qpos[i + 1], dmin = q - DOF_RANGE[2 * i], dmax = DOF_RANGE[2 * i + 1] - q;
+    if (!(std::fmin(dmin, dmax) < 0)) continue;
+    if (r >= s.nefc) break;
+    if (jar[r] < 0) {
+      double sg = dmin < dmax ? 1 : -1, pos = std::fmin(dmin, dmax), k, b, imp, dimp;
+      kbimp(JNT_SOLREF, JNT_SOLIMP, pos, h, &k, &b, &imp);
+      imp_d(JNT_SOLIMP, pos, &imp, &dimp);
+      double iw = DOF_INVWEIGHT0[i], D = s.efcD[r], dD = dimp / (iw * (1 - imp) * (1 - imp));
+      double jl = sg * lam[i], x = jar[r];
+      double dbar = -(dD * jl * x + D * jl * k * (dimp * pos + imp));
+      gq[i] += dbar * sg;
+      gv[i] += -D * jl * b * sg;
+    }
+    r++;
+  }
+  // contacts
+  for (int c = 0; c < s.ncon && r < s.nefc; c++) {
+    const Contact& ct = s.con[c];
+    int nr = ct.dim == 3 ? 4 : 1, r0 = r;
+    r += nr;
+    bool act = false;
+    for (int t = 0; t < nr && r0 + t < s.nefc; t++) act |= jar[r0 + t] < 0;
+    if (!act) continue;
+    double k, b, imp, dimp;
+    kbimp(PAIR_SOLREF, PAIR_SOLIMP, ct.dist, h, &k, &b, &imp);
+    imp_d(PAIR_SOLIMP, ct.dist, &imp, &dimp);
+    double mu = ct.mu, iw = BODY_INVWEIGHT0[ct.b1] + BODY_INVWEIGHT0[ct.b2];
+    if (ct.dim == 3) iw = (mu * mu * iw + iw) * 2 * mu * mu / IMPRATIO;
+    double D = 1.0 / (iw * (1 - imp) / imp), dD = dimp / (iw * (1 - imp) * (1 - imp));
+    double rr[3];
+    for (int q = 0; q < 3; q++) rr[q] = ct.pos[q] - s.O[q];
+    Sv Lc = sv_add(Lm[ct.b2], Lm[ct.b1], -1), Ac = sv_add(Aw[ct.b2], Aw[ct.b1], -1), Vc = sv_add(V[ct.b2], V[ct.b1], -1);
+    double dbar = 0, rb[3] = {0, 0, 0}, frb[9] = {0};
+    Sv OmL = sv0(), OmA = sv0();
+    for (int t = 0; t < nr && r0 + t < s.nefc; t++) {
+      if (!(jar[r0 + t] < 0)) continue;
+      double sg = (t & 1) ? -1 : 1, u[3];
+      const double* tk = ct.frame + 3 * (1 + (t >> 1));
+      for (int q = 0; q < 3; q++) u[q] = ct.dim == 3 ? ct.frame[q] + sg * mu * tk[q] : ct.frame[q];
+      Sv Ph;
+      cross(rr, u, Ph.w);
+      for (int q = 0; q < 3; q++) Ph.v[q] = u[q];
+      double jl = sv_dot(Lc, Ph), x = jar[r0 + t];
+      dbar += -(dD * jl * x + D * jl * k * (dimp * ct.dist + imp));
+      OmL = sv_add(OmL, Ph, -D * x);
+      OmA = sv_add(OmA, Ph, -D * jl);
+      Sv Pb = sv_add(sv_scale(Lc, -D * x), sv_add(Ac, Vc, b), -D * jl);  // Psi's cotangent of Phi
+      double ubar[3], t3[3];
+      cross(Pb.w, rr, t3);
+      for (int q = 0; q < 3; q++) ubar[q] = Pb.v[q] + t3[q];
+      cross(u, Pb.w, t3);
+      for (int q = 0; q < 3; q++) rb[q] += t3[q];
+      for (int q = 0; q < 3; q++) {
+        frb[q] += ubar[q];
+        if (ct.dim == 3) frb[3 * (1 + (t >> 1)) + q] += sg * mu * ubar[q];
+      }
+    }
+    Sv OmV = sv_scale(OmA, b);
+    const int bs[2] = {ct.b1, ct.b2};
+    for (int side = 0; side < 2; side++) {
+      int bb = bs[side];
+      if (bb == 0) continue;
+      double sgn = side ? 1 : -1;
+      Sv e = sv_add(sv_add(cross_mf(Lm[bb], OmL), cross_mf(Aw[bb], OmA)), cross_mf(V[bb], OmV));
+      E[bb] = sv_add(E[bb], e, sgn);
+      OL[bb] = sv_add(OL[bb], OmL, sgn);
+      OA[bb] = sv_add(OA[bb], OmA, sgn);
+      OV[bb] = sv_add(OV[bb], OmV, sgn);
+    }
+    double x1b[3], t1b[3], x2b[3], t2b[3];
+    contact_geom_vjp(s, ct, dbar, rb, frb, normal, x1b, t1b, x2b, t2b);
+    const int gs[2] = {PAIR_G1[ct.pair], PAIR_G2[ct.pair]};
+    const double* xb[2] = {x1b, x2b};
+    const double* tb[2] = {t1b, t2b};
+    for (int side = 0; side < 2; side++) {
+      int g = gs[side], bb = GEOM_BODY[g];
+      if (bb == 0) continue;
+      Sv w;
+      double xo[3], m[3];
+      for (int q = 0; q < 3; q++) xo[q] = s.gx[g][q] - s.O[q];
+      cross(xo, xb[side], m);
+      for (int q = 0; q < 3; q++) { w.w[q] = tb[side][q] + m[q]; w.v[q] = xb[side][q]; }
+      G[bb] = sv_add(G[bb], w);
+    }
+  }
+  // per dof: subtree sums and the joint's outside quantities
+  for (int j = 0; j < NV; j++) {
+    const int bj = DOF_BODY[j];
+    Sv F1s = sv0(), Ps = sv0(), Qss = sv0(), Rss = sv0(), Tss = sv0(), F2s = sv0(), P2s = sv0(), Es = sv0(), Gs = sv0(),
+       OLs = sv0(), OAs = sv0(), OVs = sv0();
+    for (int b = 1; b < NB; b++) {
+      if (!in_sub(b, bj)) continue;
+      F1s = sv_add(F1s, f1[b]); Ps = sv_add(Ps, P[b]); Qss = sv_add(Qss, Qs[b]); Rss = sv_add(Rss, Rs[b]);
+      Tss = sv_add(Tss, Ts[b]); F2s = sv_add(F2s, f2[b]); P2s = sv_add(P2s, P2[b]); Es = sv_add(Es, E[b]);
+      Gs = sv_add(Gs, G[b]); OLs = sv_add(OLs, OL[b]); OAs = sv_add(OAs, OA[b]); OVs = sv_add(OVs, OV[b]);
+    }
+    Sv Vo = sv0(), Lo = sv0(), Yo = sv0(), Awo = sv0(), A1o = grav, A2o = sv0();
+    if (j >= 3 && j < 6) {
+      for (int k = 0; k < 3; k++) {
+        Vo.v[k] = s.qvel[k]; Lo.v[k] = lam[k]; Yo.v[k] = y[k]; Awo.v[k] = as[k]; A1o.v[k] += as[k]; A2o.v[k] = at[k];
+      }
+    } else if (j >= 6) {
+      int p = BODY_PARENT[bj];
+      Vo = V[p]; Lo = Lm[p]; Yo = Yt[p]; Awo = Aw[p]; A1o = A1[p]; A2o = A2[p];
+    }
+    Sv Sj = dof_sv(s, j);
+    Sv sig = cross_mm(Sj, Vo), alp = cross_mm(Sj, A1o), ell = cross_mm(Sj, Lo);
+    double dq1 = -sv_dot(ell, F1s) - sv_dot(alp, Ps) - sv_dot(sig, Qss) + sv_dot(cross_mm(sig, Vo), Ps)
+                 + sv_dot(sig, Rss) + sv_dot(sig, Tss);
+    Sv rho = sv0();
+    if (j >= 3) rho = sv_add(sig, cross_mm(Sj, V[bj]));
+    double dv1 = sv_dot(Sj, sv_add(sv_add(Qss, Rss, -1), Tss, -1)) - sv_dot(rho, Ps);
+    double dq2 = -sv_dot(cross_mm(Sj, Yo), F2s) - sv_dot(cross_mm(Sj, A2o), P2s);
+    double dqc = sv_dot(Sj, sv_add(Es, Gs)) - sv_dot(Sj, sv_add(sv_add(cross_mf(Lo, OLs), cross_mf(Awo, OAs)),
+                                                               cross_mf(Vo, OVs)));
+    gq[j] += dq2 - dq1 + dqc;
+    gv[j] += -dv1 + sv_dot(Sj, OVs);
+  }
+  // actuators (the PD force kp (u - q) - kv v, clamped at +-frclim)
+  for (int i = 6; i < NV; i++) {
+    double wq = 1, wv = 1;
+    if (s.clamped[i]) {
+      if (clamp_kv == 0) { wq = 0; wv = 1; }
+      else if (clamp_kv == 1) { wq = wv = 0; }
+      else {
+        double raw = DOF_KP[i] * (ctrl[i - 6] - s.qpos[i + 1]) - DOF_KV[i] * s.qvel[i];
+        double o = (std::fabs(raw) - DOF_FRCLIM[i]) / DOF_FRCLIM[i];
+        wq = wv = clamp_soft > 0 ? std::exp(-o / clamp_soft) : 0.0;
+      }
+    }
+    gq[i] -= wq * DOF_KP[i] * lam[i];
+    gv[i] -= wv * DOF_KV[i] * lam[i];
+    ub[i - 6] += wq * DOF_KP[i] * lam[i];
+  }
+  for (int i = 0; i < NV; i++) { qb[i] = qn[i] + gq[i]; vb[i] = vt[i] + gv[i]; }
+}
+
 }  // namespace
 
 extern "C" {
@@ -649,10 +1189,14 @@ extern "C" {
 // iterations / tol: Newton's iteration cap and tolerance (the engine: 10, the model's 1e-8; MuJoCo C truth: 2000,
 // 1e-13); ls_max / ls_tol: the line search's evaluation cap and relative derivative tolerance (40, 1e-7).
 // info (nw, 4): last substep's Newton iterations, contacts (found, before the cap), rows, flags (4 contacts over
-// capacity, 16 rows over capacity). Returns 0.
+// capacity, 16 rows over capacity). flops (nw) or NULL: the world-step's algorithmic flops by the closed-form phase
+// counts (smooth 2.5e4, each factor + solve 3.1e4, broadphase 5e3 per substep; per contact 200 + 25 k + 60 rows;
+// per Newton iteration the Hessian assembly 6 k (k + 1) / 2 + 12 k over the contacts with a quadratic row and a
+// factorization 2.86e4, or 2.45e3 for a re-solve, plus 12 sum k + 2.45e3 and 6 R per line-search evaluation), k the
+// contact's support size and R the rows. Returns 0.
 int g1o_step(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
              const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
-             double* oqpos, double* oqvel, double* owarm, int* info) {
+             double* oqpos, double* oqvel, double* owarm, int* info, double* flops) {
   World* s = new World;
   for (int w = 0; w < nw; w++) {
     std::memcpy(s->qpos, qpos + (size_t)w * NQ, sizeof(double) * NQ);
@@ -661,7 +1205,10 @@ int g1o_step(int nw, const double* qpos, const double* qvel, const double* warm,
     std::memcpy(s->com, com + (size_t)w * 3, sizeof(double) * 3);
     s->fric = fric[w];
     s->flags = 0;
+    s->flops = 0;
     for (int k = 0; k < nsub; k++) {
+      // smooth dynamics 2.5e4, qacc_smooth factor + solve 3.1e4, implicitfast factor + solve 3.1e4, broadphase 5e3
+      s->flops += 2.5e4 + 3.1e4 + 3.1e4 + 5e3;
       smooth(*s, ctrl + (size_t)w * NU);
       collision(*s);
       rows(*s);
@@ -674,6 +1221,7 @@ int g1o_step(int nw, const double* qpos, const double* qvel, const double* warm,
     if (info) {
       info[4 * w] = s->niter; info[4 * w + 1] = s->ncon_raw; info[4 * w + 2] = s->nefc; info[4 * w + 3] = s->flags;
     }
+    if (flops) flops[w] = s->flops;
   }
   delete s;
   return 0;
@@ -718,6 +1266,68 @@ int g1o_contacts(const double* qpos, const double* qvel, const double* ctrl, con
   int n = s->ncon;
   delete s;
   return n;
+}
+
+
+// VJP of one control step (float64): the forward as g1o_step, then the substeps' VJPs in reverse. Cotangents of the
+// outputs gq_out (nw, 36) qpos form, gv_out (nw, 35); gradients gq_in (nw, 36) qpos form (its quaternion part
+// 2 q (x) (0, t) of the tangent cotangent t), gv_in (nw, 35), gu (nw, 29). clamp_kv 0 / 1 / 2, normal 0..3 as the
+// reference's adjoint options; clamp_soft the soft clamp's delta.
+int g1o_vjp(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl, const double* fric,
+            const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub, const double* gq_out,
+            const double* gv_out, int clamp_kv, int normal, double clamp_soft, double* gq_in, double* gv_in,
+            double* gu) {
+  World* s = new World;
+  Rec* rec = new Rec[nsub];
+  for (int w = 0; w < nw; w++) {
+    std::memcpy(s->qpos, qpos + (size_t)w * NQ, sizeof(double) * NQ);
+    std::memcpy(s->qvel, qvel + (size_t)w * NV, sizeof(double) * NV);
+    std::memcpy(s->qacc, warm + (size_t)w * NV, sizeof(double) * NV);
+    std::memcpy(s->com, com + (size_t)w * 3, sizeof(double) * 3);
+    s->fric = fric[w];
+    s->flags = 0;
+    const double* u = ctrl + (size_t)w * NU;
+    for (int k = 0; k < nsub; k++) {
+      std::memcpy(rec[k].qpos, s->qpos, sizeof(rec[k].qpos));
+      std::memcpy(rec[k].qvel, s->qvel, sizeof(rec[k].qvel));
+      smooth(*s, u);
+      collision(*s);
+      rows(*s);
+      newton(*s, iterations, tol, ls_max, ls_tol);
+      integrate(*s);
+      std::memcpy(rec[k].astar, s->qacc, sizeof(rec[k].astar));
+      std::memcpy(rec[k].aadv, s->aadv, sizeof(rec[k].aadv));
+    }
+    // output cotangent in the tangent space at q'
+    double qb[NV], vb[NV], ub[NU] = {0};
+    const double* g = gq_out + (size_t)w * NQ;
+    const double* q1 = s->qpos + 3;
+    for (int k = 0; k < 3; k++) qb[k] = g[k];
+    for (int k = 0; k < 3; k++) {
+      double e[4] = {0, 0, 0, 0}, t[4];
+      e[1 + k] = 1;
+      qmul(q1, e, t);
+      qb[3 + k] = 0.5 * (t[0] * g[3] + t[1] * g[4] + t[2] * g[5] + t[3] * g[6]);
+    }
+    for (int i = 6; i < NV; i++) qb[i] = g[i + 1];
+    std::memcpy(vb, gv_out + (size_t)w * NV, sizeof(double) * NV);
+    for (int k = nsub - 1; k >= 0; k--) substep_vjp(*s, rec[k], u, qb, vb, ub, clamp_kv, normal, clamp_soft);
+    double* o = gq_in + (size_t)w * NQ;
+    for (int k = 0; k < 3; k++) o[k] = qb[k];
+    {
+      const double* q0 = qpos + (size_t)w * NQ + 3;
+      double qn = std::sqrt(q0[0] * q0[0] + q0[1] * q0[1] + q0[2] * q0[2] + q0[3] * q0[3]);
+      double qq[4] = {q0[0] / qn, q0[1] / qn, q0[2] / qn, q0[3] / qn}, t[4] = {0, qb[3], qb[4], qb[5]}, r[4];
+      qmul(qq, t, r);
+      for (int k = 0; k < 4; k++) o[3 + k] = 2 * r[k];
+    }
+    for (int i = 6; i < NV; i++) o[i + 1] = qb[i];
+    std::memcpy(gv_in + (size_t)w * NV, vb, sizeof(double) * NV);
+    std::memcpy(gu + (size_t)w * NU, ub, sizeof(double) * NU);
+  }
+  delete[] rec;
+  delete s;
+  return 0;
 }
 
 }  // extern "C"
