@@ -8,7 +8,7 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnablaengine_g1.so")
-SOURCES = ["g1_forward.hip", "g1_capi.hip"]
+SOURCES = ["g1_forward.hip", "g1_adjoint.hip", "g1_capi.hip"]
 ARCH = os.environ.get("NABLA_OFFLOAD_ARCH", "gfx950")
 # packed FP32 instructions off (-packed-fp32-ops): the kernels are written for scalar FP32
 FLAGS = ["-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared", "-Xclang", "-target-feature", "-Xclang",

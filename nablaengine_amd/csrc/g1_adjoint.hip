@@ -1,0 +1,768 @@
+// The G1 control step's adjoint: the VJP of one control step from its forward tape, one wave64 per world, the
+// substeps in reverse. Per substep (the reference's k_adjoint phases A0-A8, adjoint.py:1-83, restated):
+//   record    the substep's input state, a*, a_adv, the contact table, zones, clamp mask (tape)
+//   poses     FK at the input state (each body walks its chain), motion subspaces S about O, own spatial inertias
+//   integ.    the integrator's VJP in the tangent space: hinges and root position q' = q + h v'; root rotation
+//             q' = q (x) exp(h w' / 2): t = R(dq) t', w' bar += h J_r(h w')' t'
+//   solves    y = Q^-1 (h v' bar) with L_Q, a* bar = h v' bar - h kv y; lambda = H^-1 a* bar with L_H (IFT)
+//   gradient  of Psi(q, v) = y' M(q) a~ - lambda' [RNE(q, v, a*) - f_act + sum_active D J' (J a* - aref)]:
+//             every q-derivative is a subtree sum of force vectors dotted with S_j plus the joint's outside terms
+//             (moving dof j's subtree rigidly by S_j: attached quantities change covariantly, the outside does not);
+//             contacts as wrenches (the primitives' pose cotangents, the twist changes at the contact point), limit
+//             rows through their distance; actuators kp / kv on the unclamped dofs (clamp_kv 0 / 1 / 2)
+// Determinism: every sum has a fixed order (lane = body sums over contacts in contact order; lane = dof sums over
+// bodies in body order); no atomics.
+#include "g1_collide.h"
+#include "g1_tape.h"
+
+namespace g1k {
+
+struct Sv { float w[3], v[3]; };
+
+__device__ __forceinline__ Sv sv0() { Sv r; for (int k = 0; k < 3; k++) r.w[k] = r.v[k] = 0.f; return r; }
+__device__ __forceinline__ Sv sv_add(const Sv& a, const Sv& b, float s = 1.f) {
+  Sv r;
+  for (int k = 0; k < 3; k++) { r.w[k] = a.w[k] + s * b.w[k]; r.v[k] = a.v[k] + s * b.v[k]; }
+  return r;
+}
+__device__ __forceinline__ float sv_dot(const Sv& m, const Sv& f) { return dot3(m.w, f.w) + dot3(m.v, f.v); }
+__device__ __forceinline__ Sv cross_mm(const Sv& x, const Sv& y) {
+  Sv r;
+  float a[3], b[3];
+  cross(x.w, y.w, r.w);
+  cross(x.w, y.v, a);
+  cross(x.v, y.w, b);
+  for (int k = 0; k < 3; k++) r.v[k] = a[k] + b[k];
+  return r;
+}
+__device__ __forceinline__ Sv cross_mf(const Sv& x, const Sv& f) {
+  Sv r;
+  float a[3], b[3];
+  cross(x.w, f.w, a);
+  cross(x.v, f.v, b);
+  for (int k = 0; k < 3; k++) r.w[k] = a[k] + b[k];
+  cross(x.w, f.v, r.v);
+  return r;
+}
+// (n, f) = I (w, v) for a packed spatial inertia about O
+__device__ __forceinline__ Sv inertia_apply(const float* J, const Sv& x) {
+  float hv[3], hw[3];
+  cross(J + 6, x.v, hv);
+  cross(J + 6, x.w, hw);
+  Sv r;
+  r.w[0] = J[0] * x.w[0] + J[3] * x.w[1] + J[4] * x.w[2] + hv[0];
+  r.w[1] = J[3] * x.w[0] + J[1] * x.w[1] + J[5] * x.w[2] + hv[1];
+  r.w[2] = J[4] * x.w[0] + J[5] * x.w[1] + J[2] * x.w[2] + hv[2];
+  for (int k = 0; k < 3; k++) r.v[k] = J[9] * x.v[k] - hw[k];
+  return r;
+}
+__device__ __forceinline__ Sv ld_sv(const float* p) {
+  Sv r;
+  for (int k = 0; k < 3; k++) { r.w[k] = p[k]; r.v[k] = p[4 + k]; }
+  return r;
+}
+__device__ __forceinline__ void st_sv(float* p, const Sv& x) {
+  for (int k = 0; k < 3; k++) { p[k] = x.w[k]; p[4 + k] = x.v[k]; }
+}
+
+enum { TW_V = 0, TW_L, TW_Y, TW_AW, TW_A2, TW_A1, NTW };  // per-body twists
+enum { FB_F1 = 0, FB_P, FB_X1, FB_F2, FB_P2, FB_EG, FB_OL, FB_OA, FB_OV, NFB };  // per-body force vectors
+constexpr int CRES = 48;  // per-contact result words
+
+struct __align__(16) Adj {
+  float qpos[40], qvel[36], astar[36], aadv[36], at[36];
+  float qb[36], vb[36], vt[36], qn[36], y[36], lam[36], ub[32], ctrl[32], com[4];
+  float L[NTRI + 2];
+  float S[NV][8];
+  float Q[NB][4], X[NB][4], ha[NB][4];
+  float O[4];
+  float fric;
+  float Ib[NB][12];
+  float tw[NB][NTW][8];
+  float gx[NGEOM][4], gq[NGEOM][4];
+  union {
+    float cres[MAXCON][CRES];
+    float fb[NB][NFB][8];
+  };
+  int ncon, flags;
+  unsigned clampm[2], limzone[2], limrow[2], czone[8];
+  unsigned short con[MAXCON];
+};
+
+// impedance and its derivative in the distance (kbimp's curve, solimp power 2; 0 where the curve is clamped)
+__device__ __forceinline__ void imp_d(const float* solimp, float pos, float* imp, float* dimp) {
+  const float dmin = fminf(fmaxf(solimp[0], 1e-4f), 0.9999f), dmax = fminf(fmaxf(solimp[1], 1e-4f), 0.9999f);
+  const float width = fmaxf(1e-15f, solimp[2]), mid = fminf(fmaxf(solimp[3], 1e-4f), 0.9999f);
+  const float x = fabsf(pos) / width, sg = pos < 0.f ? -1.f : 1.f;
+  *dimp = 0.f;
+  if (x <= 0.f) { *imp = dmin; return; }
+  if (x >= 1.f) { *imp = dmax; return; }
+  float y, dy;
+  if (x <= mid) { y = x * x / mid; dy = 2.f * x / mid; }
+  else { y = 1.f - (1.f - x) * (1.f - x) / (1.f - mid); dy = 2.f * (1.f - x) / (1.f - mid); }
+  const float v = dmin + y * (dmax - dmin);
+  if (v < dmin || v > dmax) { *imp = fminf(fmaxf(v, dmin), dmax); return; }
+  *imp = v;
+  *dimp = dy * (dmax - dmin) * sg / width;
+}
+__device__ __forceinline__ void kb_consts(const float* solref, const float* solimp, float* k, float* b) {
+  const float tc = fmaxf(solref[0], 2.f * kH), dr = solref[1];
+  const float dmax = fminf(fmaxf(solimp[1], 1e-4f), 0.9999f);
+  *k = 1.f / fmaxf(1e-15f, dmax * dmax * tc * tc * dr * dr);
+  *b = 2.f / fmaxf(1e-15f, dmax * tc);
+}
+
+__constant__ inline Arr<float, 2> caJSolref = to_float(JNT_SOLREF);
+__constant__ inline Arr<float, 5> caJSolimp = to_float(JNT_SOLIMP);
+__constant__ inline Arr<float, 2> caPSolref = to_float(PAIR_SOLREF);
+__constant__ inline Arr<float, 5> caPSolimp = to_float(PAIR_SOLIMP);
+
+// the normal derivative's factor kappa(nu): 1 / nu exact (0), frozen (1), 1 / max(nu, eps) (2), frozen below eps (3)
+__device__ __forceinline__ float kappa(float nu, int normal) {
+  const float eps = 1e-3f;
+  if (normal == 0) return 1.f / nu;
+  if (normal == 1) return 0.f;
+  if (normal == 2) return 1.f / fmaxf(nu, eps);
+  return nu < eps ? 0.f : 1.f / nu;
+}
+
+// make_frame VJP: cotangents of the frame rows (n, b, c) -> n bar (added)
+__device__ __forceinline__ void make_frame_vjp(const float* n, const float* frb, float* nb) {
+  float e[3] = {0.f, 0.f, 0.f};
+  if (-0.5f < n[1] && n[1] < 0.5f) e[1] = 1.f; else e[2] = 1.f;
+  const float ne = dot3(n, e);
+  float b0[3];
+  for (int k = 0; k < 3; k++) b0[k] = e[k] - n[k] * ne;
+  const float bl = sqrtf(dot3(b0, b0));
+  float b[3], bbar[3], t[3];
+  for (int k = 0; k < 3; k++) b[k] = b0[k] / bl;
+  cross(b, frb + 6, t);
+  for (int k = 0; k < 3; k++) nb[k] += frb[k] + t[k];
+  cross(frb + 6, n, t);
+  for (int k = 0; k < 3; k++) bbar[k] = frb[3 + k] + t[k];
+  const float bb = dot3(b, bbar);
+  float b0b[3];
+  for (int k = 0; k < 3; k++) b0b[k] = (bbar[k] - b[k] * bb) / bl;
+  const float nb0 = dot3(n, b0b);
+  for (int k = 0; k < 3; k++) nb[k] += -ne * b0b[k] - nb0 * e[k];
+}
+
+// sphere core VJP: (dist, pos, n) of two spheres with cotangents db, posb, nb -> p1b, p2b (added)
+__device__ __forceinline__ void sphere_core_vjp(const float* p1, float r1, const float* p2, float r2, float db,
+                                                const float* posb, const float* nb, int normal, float* p1b, float* p2b) {
+  const float dl[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
+  const float l = sqrtf(dot3(dl, dl));
+  float dlb[3];
+  for (int k = 0; k < 3; k++) { p1b[k] += posb[k]; dlb[k] = 0.5f * posb[k]; }
+  if (l > 0.f) {
+    float n[3], nt[3];
+    for (int k = 0; k < 3; k++) { n[k] = dl[k] / l; nt[k] = nb[k] + 0.5f * (r1 - r2) * posb[k]; }
+    const float nn = dot3(n, nt), kap = kappa(l, normal);
+    for (int k = 0; k < 3; k++) dlb[k] += kap * (nt[k] - n[k] * nn) + n[k] * db;
+  }
+  for (int k = 0; k < 3; k++) { p1b[k] -= dlb[k]; p2b[k] += dlb[k]; }
+}
+
+// the contact geometry's VJP (pair pr, its contact `slot`, normal frame fr): cotangents of (dist, pos, frame) -> the
+// geoms' world position and rotation cotangents
+__device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr, float db, const float* posb,
+                                 const float* frb, int normal, float* x1b, float* t1b, float* x2b, float* t2b) {
+  const unsigned w = cPairW[pr];
+  const int g1 = w & 255u, g2 = (w >> 8) & 255u, cls = (w >> 21) & 7u;
+  float p1[3], q1[4], p2[3], q2[4];
+  for (int k = 0; k < 3; k++) { p1[k] = s.gx[g1][k]; p2[k] = s.gx[g2][k]; }
+  for (int k = 0; k < 4; k++) { q1[k] = s.gq[g1][k]; q2[k] = s.gq[g2][k]; }
+  const float r1 = cGsize[3 * g1], h1 = cGsize[3 * g1 + 1], r2 = cGsize[3 * g2], h2 = cGsize[3 * g2 + 1];
+  for (int k = 0; k < 3; k++) x1b[k] = t1b[k] = x2b[k] = t2b[k] = 0.f;
+  if (cls == 0 || cls == 4) {  // the floor: n constant
+    float n[3];
+    zaxis(q1, n);
+    const float pn = dot3(n, posb);
+    float ceb[3];
+    for (int k = 0; k < 3; k++) ceb[k] = posb[k] - 0.5f * n[k] * pn + n[k] * db;
+    if (cls == 0) {
+      for (int k = 0; k < 3; k++) x2b[k] += ceb[k];
+    } else {
+      float axis[3], axb[3];
+      zaxis(q2, axis);
+      const float sg = slot == 0 ? 1.f : -1.f;
+      for (int k = 0; k < 3; k++) { x2b[k] += ceb[k]; axb[k] = sg * h2 * ceb[k]; }
+      const float na = dot3(n, axis);
+      float b0[3];
+      for (int k = 0; k < 3; k++) b0[k] = axis[k] - n[k] * na;
+      const float bn = sqrtf(dot3(b0, b0));
+      if (bn >= 0.5f) {
+        float b[3], bbar[3], t[3];
+        for (int k = 0; k < 3; k++) b[k] = b0[k] / bn;
+        cross(frb + 6, n, t);
+        for (int k = 0; k < 3; k++) bbar[k] = frb[3 + k] + t[k];
+        const float bb = dot3(b, bbar);
+        float b0b[3];
+        for (int k = 0; k < 3; k++) b0b[k] = (bbar[k] - b[k] * bb) / bn;
+        const float nb0 = dot3(n, b0b);
+        for (int k = 0; k < 3; k++) axb[k] += b0b[k] - n[k] * nb0;
+      }
+      cross(axis, axb, t2b);
+    }
+    return;
+  }
+  float nb[3] = {0.f, 0.f, 0.f};
+  make_frame_vjp(fr, frb, nb);
+  if (cls == 1) {
+    sphere_core_vjp(p1, r1, p2, r2, db, posb, nb, normal, x1b, x2b);
+    return;
+  }
+  if (cls == 2) {
+    float axis[3], a[3], ab[3], ap[3], pt[3], ptb[3] = {0.f, 0.f, 0.f};
+    zaxis(q2, axis);
+    for (int k = 0; k < 3; k++) { a[k] = p2[k] - axis[k] * h2; ab[k] = 2.f * axis[k] * h2; ap[k] = p1[k] - a[k]; }
+    const float gam = dot3(ab, ab) + 1e-6f, raw = dot3(ap, ab) / gam, t = fminf(fmaxf(raw, 0.f), 1.f);
+    for (int k = 0; k < 3; k++) pt[k] = a[k] + t * ab[k];
+    sphere_core_vjp(p1, r1, pt, r2, db, posb, nb, normal, x1b, ptb);
+    const float tb = dot3(ptb, ab);
+    float abb[3], apb[3] = {0.f, 0.f, 0.f}, aab[3], axb[3];
+    for (int k = 0; k < 3; k++) { abb[k] = t * ptb[k]; aab[k] = ptb[k]; }
+    if (raw > 0.f && raw < 1.f)
+      for (int k = 0; k < 3; k++) {
+        apb[k] = tb * ab[k] / gam;
+        abb[k] += tb * ap[k] / gam - tb * raw / gam * 2.f * ab[k];
+      }
+    for (int k = 0; k < 3; k++) { x1b[k] += apb[k]; aab[k] -= apb[k]; }
+    for (int k = 0; k < 3; k++) { x2b[k] += aab[k]; axb[k] = -h2 * aab[k] + 2.f * h2 * abb[k]; }
+    cross(axis, axb, t2b);
+    return;
+  }
+  // capsule-capsule: the segment parameters' clamp cascade, then the sphere core on the closest points
+  float z1[3], z2[3], a1[3], a2[3], d[3];
+  zaxis(q1, z1);
+  zaxis(q2, z2);
+  for (int k = 0; k < 3; k++) { a1[k] = z1[k] * h1; a2[k] = z2[k] * h2; d[k] = p1[k] - p2[k]; }
+  const float ma = dot3(a1, a1), mb = -dot3(a1, a2), mc = dot3(a2, a2), u = -dot3(a1, d), v = dot3(a2, d);
+  const float det = ma * mc - mb * mb;
+  float x1, x2;
+  int mode;  // 0 both free, 1 x2 free (x1 fixed), 2 x1 free (x2 fixed), 3 both fixed
+  if (fabsf(det) >= 1e-15f) {
+    x1 = (mc * u - mb * v) / det;
+    x2 = (ma * v - mb * u) / det;
+    mode = 0;
+    if (x1 > 1.f) { x1 = 1.f; x2 = (v - mb) / mc; mode = 1; }
+    else if (x1 < -1.f) { x1 = -1.f; x2 = (v + mb) / mc; mode = 1; }
+    if (x2 > 1.f || x2 < -1.f) {
+      const bool hi = x2 > 1.f;
+      x2 = hi ? 1.f : -1.f;
+      const float raw = hi ? (u - mb) / ma : (u + mb) / ma;
+      x1 = fminf(fmaxf(raw, -1.f), 1.f);
+      mode = (raw >= -1.f && raw < 1.f) ? 2 : 3;
+    }
+  } else if (slot < 2) {
+    x1 = slot == 0 ? 1.f : -1.f;
+    const float raw = slot == 0 ? (v - mb) / mc : (v + mb) / mc;
+    x2 = fminf(fmaxf(raw, -1.f), 1.f);
+    mode = (raw >= -1.f && raw < 1.f) ? 1 : 3;
+  } else {
+    x2 = slot == 2 ? 1.f : -1.f;
+    const float raw = slot == 2 ? (u - mb) / ma : (u + mb) / ma;
+    x1 = fminf(fmaxf(raw, -1.f), 1.f);
+    mode = (raw >= -1.f && raw < 1.f) ? 2 : 3;
+  }
+  float v1[3], v2[3], v1b[3] = {0.f, 0.f, 0.f}, v2b[3] = {0.f, 0.f, 0.f};
+  for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
+  sphere_core_vjp(v1, r1, v2, r2, db, posb, nb, normal, v1b, v2b);
+  float a1b[3], a2b[3];
+  for (int k = 0; k < 3; k++) { x1b[k] += v1b[k]; x2b[k] += v2b[k]; a1b[k] = x1 * v1b[k]; a2b[k] = x2 * v2b[k]; }
+  float x1bar = dot3(a1, v1b), x2bar = dot3(a2, v2b);
+  if (mode == 0 && normal != 0) {  // near-parallel capsules: both parameters held where sin^2(theta) < 1.2e-3
+    float cr[3];
+    cross(a1, a2, cr);
+    if (dot3(cr, cr) < 1.2e-3f * ma * mc) { x1bar = 0.f; x2bar = 0.f; }
+  }
+  float mab = 0.f, mbb = 0.f, mcb = 0.f, ub = 0.f, vb = 0.f;
+  if (mode == 0) {
+    const float N1b = x1bar / det, N2b = x2bar / det, detb = -x1bar * x1 / det - x2bar * x2 / det;
+    mcb += N1b * u; ub += N1b * mc; mbb -= N1b * v; vb -= N1b * mb;
+    mab += N2b * v; vb += N2b * ma; mbb -= N2b * u; ub -= N2b * mb;
+    mab += detb * mc; mcb += detb * ma; mbb -= 2.f * mb * detb;
+  } else if (mode == 1) {
+    vb += x2bar / mc; mbb -= x2bar * x1 / mc; mcb -= x2bar * x2 / mc;
+  } else if (mode == 2) {
+    ub += x1bar / ma; mbb -= x1bar * x2 / ma; mab -= x1bar * x1 / ma;
+  }
+  float dbv[3];
+  for (int k = 0; k < 3; k++) {
+    a1b[k] += 2.f * mab * a1[k] - mbb * a2[k] - ub * d[k];
+    a2b[k] += 2.f * mcb * a2[k] - mbb * a1[k] + vb * d[k];
+    dbv[k] = -ub * a1[k] + vb * a2[k];
+  }
+  for (int k = 0; k < 3; k++) { x1b[k] += dbv[k]; x2b[k] -= dbv[k]; a1b[k] *= h1; a2b[k] *= h2; }
+  cross(z1, a1b, t1b);
+  cross(z2, a2b, t2b);
+}
+
+// ---------------------------------------------------------------------------------------------- one substep
+__device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int clamp_kv, int normal,
+                            float clamp_soft) {
+  // the record
+  if (lane < NQ) s.qpos[lane] = rec[REC_QPOS + lane];
+  if (lane < NV) {
+    s.qvel[lane] = rec[REC_QVEL + lane];
+    s.astar[lane] = rec[REC_ASTAR + lane];
+    s.aadv[lane] = rec[REC_AADV + lane];
+    s.at[lane] = s.astar[lane] - s.aadv[lane];
+  }
+  if (lane < 2) {
+    s.clampm[lane] = __float_as_uint(rec[REC_CLAMP + lane]);
+    s.limzone[lane] = __float_as_uint(rec[REC_LIMZONE + lane]);
+    s.limrow[lane] = __float_as_uint(rec[REC_LIMROW + lane]);
+  }
+  if (lane < 8) s.czone[lane] = __float_as_uint(rec[REC_CZONE + lane]);
+  if (lane < MAXCON / 2) {
+    const unsigned e = __float_as_uint(rec[REC_CON + lane]);
+    s.con[2 * lane] = (unsigned short)(e & 0xFFFFu);
+    s.con[2 * lane + 1] = (unsigned short)(e >> 16);
+  }
+  if (lane == 0) s.ncon = min((int)(__float_as_uint(rec[REC_HDR]) & 255u), MAXCON);
+  wsync();
+  // poses
+  if (lane >= 2 && lane < NB) {
+    float sn, cs;
+    sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
+    s.ha[lane][0] = cs;
+    s.ha[lane][1] = sn * cAxis[3 * lane];
+    s.ha[lane][2] = sn * cAxis[3 * lane + 1];
+    s.ha[lane][3] = sn * cAxis[3 * lane + 2];
+  }
+  if (lane < 3) s.O[lane] = s.qpos[lane];
+  wsync();
+  {
+    float Q[4], X[3];
+    const float n = rsqrtf(s.qpos[3] * s.qpos[3] + s.qpos[4] * s.qpos[4] + s.qpos[5] * s.qpos[5] + s.qpos[6] * s.qpos[6]);
+    for (int k = 0; k < 4; k++) Q[k] = s.qpos[3 + k] * n;
+    for (int k = 0; k < 3; k++) X[k] = s.qpos[k];
+    const int b = lane < NB ? lane : 0;
+    const int depth = cDepth[b];
+#pragma unroll
+    for (int l = 1; l < MAXDEPTH; l++) {
+      if (l < depth) {
+        const int k = cTree.path[b][l];
+        const float qb[4] = {cQuat[4 * k], cQuat[4 * k + 1], cQuat[4 * k + 2], cQuat[4 * k + 3]};
+        const float pb[3] = {cPos[3 * k], cPos[3 * k + 1], cPos[3 * k + 2]};
+        const float ha[4] = {s.ha[k][0], s.ha[k][1], s.ha[k][2], s.ha[k][3]};
+        float q0[4], t[3];
+        qmul(Q, qb, q0);
+        qrot(Q, pb, t);
+        qmul(q0, ha, Q);
+        for (int c = 0; c < 3; c++) X[c] += t[c];
+      }
+    }
+    if (lane < NB) {
+      for (int k = 0; k < 4; k++) s.Q[lane][k] = lane == 0 ? (k == 0 ? 1.f : 0.f) : Q[k];
+      for (int k = 0; k < 3; k++) s.X[lane][k] = lane == 0 ? 0.f : X[k];
+    }
+    if (lane >= 1 && lane < NB) {  // own spatial inertia about O
+      float ip[3], c[3], qi[4], R[9];
+      for (int k = 0; k < 3; k++) ip[k] = cIpos[3 * lane + k] + (lane == TORSO_BODY ? s.com[k] : 0.f);
+      qrot(Q, ip, c);
+      const float iq[4] = {cIquat[4 * lane], cIquat[4 * lane + 1], cIquat[4 * lane + 2], cIquat[4 * lane + 3]};
+      const float In[3] = {cInert[3 * lane], cInert[3 * lane + 1], cInert[3 * lane + 2]};
+      qmul(Q, iq, qi);
+      for (int k = 0; k < 3; k++) {
+        float e[3] = {(float)(k == 0), (float)(k == 1), (float)(k == 2)};
+        qrot(qi, e, R + 3 * k);
+      }
+      float* J = s.Ib[lane];
+      J[0] = In[0] * R[0] * R[0] + In[1] * R[3] * R[3] + In[2] * R[6] * R[6];
+      J[1] = In[0] * R[1] * R[1] + In[1] * R[4] * R[4] + In[2] * R[7] * R[7];
+      J[2] = In[0] * R[2] * R[2] + In[1] * R[5] * R[5] + In[2] * R[8] * R[8];
+      J[3] = In[0] * R[0] * R[1] + In[1] * R[3] * R[4] + In[2] * R[6] * R[7];
+      J[4] = In[0] * R[0] * R[2] + In[1] * R[3] * R[5] + In[2] * R[6] * R[8];
+      J[5] = In[0] * R[1] * R[2] + In[1] * R[4] * R[5] + In[2] * R[7] * R[8];
+      float cc3[3];
+      for (int k = 0; k < 3; k++) cc3[k] = X[k] - s.qpos[k] + c[k];
+      const float m = cMass[lane], cc = dot3(cc3, cc3);
+      J[0] += m * (cc - cc3[0] * cc3[0]); J[1] += m * (cc - cc3[1] * cc3[1]); J[2] += m * (cc - cc3[2] * cc3[2]);
+      J[3] -= m * cc3[0] * cc3[1]; J[4] -= m * cc3[0] * cc3[2]; J[5] -= m * cc3[1] * cc3[2];
+      J[6] = m * cc3[0]; J[7] = m * cc3[1]; J[8] = m * cc3[2]; J[9] = m;
+    }
+  }
+  wsync();
+  if (lane < NV) {  // motion subspaces about O
+    float w[3], v[3];
+    if (lane < 3) {
+      w[0] = w[1] = w[2] = 0.f;
+      v[0] = lane == 0; v[1] = lane == 1; v[2] = lane == 2;
+    } else if (lane < 6) {
+      const float e[3] = {(float)(lane == 3), (float)(lane == 4), (float)(lane == 5)};
+      qrot(s.Q[1], e, w);
+      v[0] = v[1] = v[2] = 0.f;
+    } else {
+      const int b = lane - 4;
+      const float r[3] = {s.O[0] - s.X[b][0], s.O[1] - s.X[b][1], s.O[2] - s.X[b][2]};
+      const float ax[3] = {cAxis[3 * b], cAxis[3 * b + 1], cAxis[3 * b + 2]};
+      qrot(s.Q[b], ax, w);
+      cross(w, r, v);
+    }
+    for (int k = 0; k < 3; k++) { s.S[lane][k] = w[k]; s.S[lane][4 + k] = v[k]; }
+  }
+  if (lane < NGEOM) {  // geom poses
+    const int b = cGbody[lane];
+    float t[3], qb[4] = {s.Q[b][0], s.Q[b][1], s.Q[b][2], s.Q[b][3]};
+    const float gp[3] = {cGpos[3 * lane], cGpos[3 * lane + 1], cGpos[3 * lane + 2]};
+    const float gq[4] = {cGquat[4 * lane], cGquat[4 * lane + 1], cGquat[4 * lane + 2], cGquat[4 * lane + 3]};
+    qrot(qb, gp, t);
+    for (int k = 0; k < 3; k++) s.gx[lane][k] = s.X[b][k] + t[k];
+    qmul(qb, gq, s.gq[lane]);
+  }
+  // the integrator's VJP (tangent space): hinges and root position directly; the root rotation on lane 0
+  if (lane < NV) {
+    const bool dir = lane < 3 || lane >= 6;
+    s.vt[lane] = s.vb[lane] + (dir ? kH * s.qb[lane] : 0.f);
+    s.qn[lane] = s.qb[lane];
+  }
+  wsync();
+  if (lane == 0) {
+    float phi[3], t[3] = {s.qb[3], s.qb[4], s.qb[5]};
+    for (int k = 0; k < 3; k++) phi[k] = kH * (s.qvel[3 + k] + kH * s.aadv[3 + k]);
+    const float th = sqrtf(dot3(phi, phi));
+    float dq[4] = {1.f, 0.f, 0.f, 0.f};
+    if (th > 0.f) {
+      float sn, cs;
+      sincosf(0.5f * th, &sn, &cs);
+      dq[0] = cs; dq[1] = sn * phi[0] / th; dq[2] = sn * phi[1] / th; dq[3] = sn * phi[2] / th;
+    }
+    float rt[3];
+    qrot(dq, t, rt);  // t = R(dq) t'
+    for (int k = 0; k < 3; k++) s.qn[3 + k] = rt[k];
+    // J_r(phi)' t' = t' + c1 phi x t' + c2 phi x (phi x t')
+    float c1, c2;
+    if (th < 1e-2f) { c1 = 0.5f - th * th / 24.f; c2 = 1.f / 6.f - th * th / 120.f; }
+    else { c1 = (1.f - cosf(th)) / (th * th); c2 = (th - sinf(th)) / (th * th * th); }
+    float pt[3], ppt[3];
+    cross(phi, t, pt);
+    cross(phi, pt, ppt);
+    for (int k = 0; k < 3; k++) s.vt[3 + k] += kH * (t[k] + c1 * pt[k] + c2 * ppt[k]);
+  }
+  wsync();
+  // y = Q^-1 a_adv bar (L_Q), a* bar = a_adv bar - h kv y; lambda = H^-1 a* bar (L_H)
+  for (int i = lane; i < NTRI; i += WL) s.L[i] = rec[REC_LQ + i];
+  wsync();
+  const float aab = lane < NV ? kH * s.vt[lane] : 0.f;
+  const float y = chol_resolve(s.L, aab, lane);
+  if (lane < NV) s.y[lane] = y;
+  wsync();
+  for (int i = lane; i < NTRI; i += WL) s.L[i] = rec[REC_LH + i];
+  wsync();
+  const float asb = lane < NV ? aab - kH * cKv[lane] * y : 0.f;
+  const float lam = chol_resolve(s.L, asb, lane);
+  if (lane < NV) s.lam[lane] = lam;
+  wsync();
+  // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body
+  if (lane >= 1 && lane < NB) {
+    Sv V = sv0(), Lm = sv0(), Y = sv0(), Aw = sv0(), A2 = sv0(), Ac = sv0();
+    const int n = cTree.nchain[lane];
+    for (int t = 0; t < MAXCHAIN; t++) {
+      if (t < n) {
+        const int d = cTree.chain[lane][t];
+        const Sv Sd = ld_sv(s.S[d]);
+        const float vd = s.qvel[d];
+        V = sv_add(V, Sd, vd);
+        Lm = sv_add(Lm, Sd, s.lam[d]);
+        Y = sv_add(Y, Sd, s.y[d]);
+        Aw = sv_add(Aw, Sd, s.astar[d]);
+        A2 = sv_add(A2, Sd, s.at[d]);
+        if (d == 5) {
+          for (int r = 3; r < 6; r++) Ac = sv_add(Ac, cross_mm(V, ld_sv(s.S[r])), s.qvel[r]);
+        } else if (d >= 6) {
+          Ac = sv_add(Ac, cross_mm(V, Sd), vd);
+        }
+      }
+    }
+    Sv A1 = sv_add(Aw, Ac);
+    for (int k = 0; k < 3; k++) A1.v[k] -= kGrav[k];
+    st_sv(s.tw[lane][TW_V], V);
+    st_sv(s.tw[lane][TW_L], Lm);
+    st_sv(s.tw[lane][TW_Y], Y);
+    st_sv(s.tw[lane][TW_AW], Aw);
+    st_sv(s.tw[lane][TW_A2], A2);
+    st_sv(s.tw[lane][TW_A1], A1);
+  }
+  if (lane == 0)
+    for (int t = 0; t < NTW; t++) st_sv(s.tw[0][t], sv0());
+  wsync();
+  // limit rows (their dof's lane): through the distance only (J constant)
+  float lgq = 0.f, lgv = 0.f;
+  if (lane >= 6 && lane < NV) {
+    const unsigned long long lr = (unsigned long long)s.limrow[0] | (unsigned long long)s.limrow[1] << 32;
+    const unsigned long long lz = (unsigned long long)s.limzone[0] | (unsigned long long)s.limzone[1] << 32;
+    if ((lz >> lane) & 1ull && (lr >> lane) & 1ull) {
+      const float q = s.qpos[lane + 1], dmin = q - cRange[2 * lane], dmax = cRange[2 * lane + 1] - q;
+      const float sg = dmin < dmax ? 1.f : -1.f, pos = fminf(dmin, dmax);
+      float k, b, imp, dimp;
+      kb_consts(caJSolref.v, caJSolimp.v, &k, &b);
+      imp_d(caJSolimp.v, pos, &imp, &dimp);
+      const float iw = cDinvw[lane];
+      const float D = 1.f / fmaxf(iw * (1.f - imp) / imp, 1e-15f), dD = dimp / (iw * (1.f - imp) * (1.f - imp));
+      const float jl = sg * s.lam[lane], x = sg * s.astar[lane] + k * imp * pos + b * sg * s.qvel[lane];
+      const float dbar = -(dD * jl * x + D * jl * k * (dimp * pos + imp));
+      lgq = dbar * sg;
+      lgv = -D * jl * b * sg;
+    }
+  }
+  // contacts (lane = contact of the tape's table): replay, row terms, geometry VJP -> wrenches
+  const int ncon = s.ncon;
+  if (lane < ncon) {
+    float* o = s.cres[lane];
+    for (int e = 0; e < CRES; e++) o[e] = 0.f;
+    const unsigned zc = (s.czone[lane >> 3] >> (4 * (lane & 7))) & 15u;
+    const int pr = min((int)(s.con[lane] & 511u), NPAIR - 1), slot = s.con[lane] >> 9;
+    const unsigned w = cPairW[pr];
+    const int b1 = cGbody[w & 255u], b2 = cGbody[(w >> 8) & 255u], dim = (w >> 16) & 15u;
+    o[46] = __int_as_float(b1);
+    o[47] = __int_as_float(b2);
+    if (zc) {
+      Cand cd;
+      collide_pair(s.gx, s.gq, pr, cd);
+      const int which = (cd.has[0] && cd.slot[0] == slot) ? 0 : 1;
+      if (!cd.has[which] || cd.slot[which] != slot) {
+        s.flags |= 1 << 13;  // the replay does not find the tape's contact (a benign race on the same bit)
+      } else {
+        const float dist = cd.d[which];
+        float pos[3], fr[9];
+        for (int k = 0; k < 3; k++) pos[k] = which ? cd.pos[1][k] : cd.pos[0][k];
+        for (int k = 0; k < 9; k++) fr[k] = which ? cd.fr[1][k] : cd.fr[0][k];
+        const float mu = ((w >> 20) & 1u) ? s.fric : cPairMu[pr];
+        float k, b, imp, dimp;
+        kb_consts(caPSolref.v, caPSolimp.v, &k, &b);
+        imp_d(caPSolimp.v, dist, &imp, &dimp);
+        float iw = cBinvw[b1] + cBinvw[b2];
+        if (dim == 3) iw = (mu * mu * iw + iw) * 2.f * mu * mu / kImpratio;
+        const float D = 1.f / fmaxf(iw * (1.f - imp) / imp, 1e-15f), dD = dimp / (iw * (1.f - imp) * (1.f - imp));
+        float rr[3];
+        for (int q = 0; q < 3; q++) rr[q] = pos[q] - s.O[q];
+        const Sv Lc = sv_add(ld_sv(s.tw[b2][TW_L]), ld_sv(s.tw[b1][TW_L]), -1.f);
+        const Sv Ac = sv_add(ld_sv(s.tw[b2][TW_AW]), ld_sv(s.tw[b1][TW_AW]), -1.f);
+        const Sv Vc = sv_add(ld_sv(s.tw[b2][TW_V]), ld_sv(s.tw[b1][TW_V]), -1.f);
+        float dbar = 0.f, rb[3] = {0.f, 0.f, 0.f}, frb[9];
+        for (int q = 0; q < 9; q++) frb[q] = 0.f;
+        Sv OmL = sv0(), OmA = sv0();
+        const int nr = dim == 3 ? 4 : 1;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          if (t >= nr || !((zc >> t) & 1u)) continue;
+          const float sg = (t & 1) ? -1.f : 1.f;
+          const float* tk = fr + 3 * (1 + (t >> 1));
+          float u[3];
+          for (int q = 0; q < 3; q++) u[q] = dim == 3 ? fr[q] + sg * mu * tk[q] : fr[q];
+          Sv Ph;
+          cross(rr, u, Ph.w);
+          for (int q = 0; q < 3; q++) Ph.v[q] = u[q];
+          const float jl = sv_dot(Lc, Ph), x = sv_dot(Ph, Ac) + k * imp * dist + b * sv_dot(Ph, Vc);
+          dbar += -(dD * jl * x + D * jl * k * (dimp * dist + imp));
+          OmL = sv_add(OmL, Ph, -D * x);
+          OmA = sv_add(OmA, Ph, -D * jl);
+          const Sv Pb = sv_add(sv_add(sv0(), Lc, -D * x), sv_add(Ac, Vc, b), -D * jl);
+          float ubar[3], t3[3];
+          cross(Pb.w, rr, t3);
+          for (int q = 0; q < 3; q++) ubar[q] = Pb.v[q] + t3[q];
+          cross(u, Pb.w, t3);
+          for (int q = 0; q < 3; q++) rb[q] += t3[q];
+          for (int q = 0; q < 3; q++) {
+            frb[q] += ubar[q];
+            if (dim == 3) frb[3 * (1 + (t >> 1)) + q] += sg * mu * ubar[q];
+          }
+        }
+        const Sv OmV = sv_add(sv0(), OmA, b);
+        // the bodies' twist changes at the contact (side b2 +, b1 -)
+        const Sv e1 = sv_add(sv_add(cross_mf(ld_sv(s.tw[b1][TW_L]), OmL), cross_mf(ld_sv(s.tw[b1][TW_AW]), OmA)),
+                             cross_mf(ld_sv(s.tw[b1][TW_V]), OmV));
+        const Sv e2 = sv_add(sv_add(cross_mf(ld_sv(s.tw[b2][TW_L]), OmL), cross_mf(ld_sv(s.tw[b2][TW_AW]), OmA)),
+                             cross_mf(ld_sv(s.tw[b2][TW_V]), OmV));
+        float x1b[3], t1b[3], x2b[3], t2b[3];
+        contact_geom_vjp(s, pr, slot, fr, dbar, rb, frb, normal, x1b, t1b, x2b, t2b);
+        const int g1 = w & 255u, g2 = (w >> 8) & 255u;
+        Sv G1, G2;
+        {
+          float xo[3], m[3];
+          for (int q = 0; q < 3; q++) xo[q] = s.gx[g1][q] - s.O[q];
+          cross(xo, x1b, m);
+          for (int q = 0; q < 3; q++) { G1.w[q] = t1b[q] + m[q]; G1.v[q] = x1b[q]; }
+          for (int q = 0; q < 3; q++) xo[q] = s.gx[g2][q] - s.O[q];
+          cross(xo, x2b, m);
+          for (int q = 0; q < 3; q++) { G2.w[q] = t2b[q] + m[q]; G2.v[q] = x2b[q]; }
+        }
+        st_sv(o + 0, OmL);
+        st_sv(o + 8, OmA);
+        st_sv(o + 16, sv_add(G1, e1, -1.f));  // the b1 side's wrench (its twists enter with -)
+        st_sv(o + 24, sv_add(G2, e2));        // the b2 side's wrench
+        o[32] = b;
+      }
+    }
+  }
+  wsync();
+  // per body: the contacts' wrenches (contact order), then the RNE force vectors
+  Sv EG = sv0(), OL = sv0(), OA = sv0(), OV = sv0();
+  if (lane >= 1 && lane < NB) {
+    for (int c = 0; c < ncon; c++) {
+      const float* o = s.cres[c];
+      const int b1 = __float_as_int(o[46]), b2 = __float_as_int(o[47]);
+      const float bb = o[32];
+      const float s2 = b2 == lane ? 1.f : 0.f, s1 = b1 == lane ? 1.f : 0.f;
+      if (s1 == 0.f && s2 == 0.f) continue;
+      const Sv OmL = ld_sv(o), OmA = ld_sv(o + 8);
+      EG = sv_add(EG, ld_sv(o + 24), s2);
+      EG = sv_add(EG, ld_sv(o + 16), s1);
+      OL = sv_add(OL, OmL, s2 - s1);
+      OA = sv_add(OA, OmA, s2 - s1);
+      OV = sv_add(OV, OmA, (s2 - s1) * bb);
+    }
+  }
+  wsync();
+  if (lane >= 1 && lane < NB) {
+    const float* I = s.Ib[lane];
+    const Sv V = ld_sv(s.tw[lane][TW_V]), Lm = ld_sv(s.tw[lane][TW_L]);
+    const Sv IV = inertia_apply(I, V), IL = inertia_apply(I, Lm);
+    const Sv F1 = sv_add(inertia_apply(I, ld_sv(s.tw[lane][TW_A1])), cross_mf(V, IV));
+    const Sv Qs = cross_mf(V, IL), Rs = cross_mf(Lm, IV), Ts = inertia_apply(I, cross_mm(V, Lm));
+    const Sv X1 = sv_add(sv_add(Rs, Ts), Qs, -1.f);
+    st_sv(s.fb[lane][FB_F1], F1);
+    st_sv(s.fb[lane][FB_P], IL);
+    st_sv(s.fb[lane][FB_X1], X1);
+    st_sv(s.fb[lane][FB_F2], inertia_apply(I, ld_sv(s.tw[lane][TW_A2])));
+    st_sv(s.fb[lane][FB_P2], inertia_apply(I, ld_sv(s.tw[lane][TW_Y])));
+    st_sv(s.fb[lane][FB_EG], EG);
+    st_sv(s.fb[lane][FB_OL], OL);
+    st_sv(s.fb[lane][FB_OA], OA);
+    st_sv(s.fb[lane][FB_OV], OV);
+  }
+  wsync();
+  // per dof: subtree sums and the joint's outside terms
+  if (lane < NV) {
+    const int j = lane;
+    const int bj = j < 6 ? 1 : j - 4;
+    const unsigned sub = cTree.submask[bj];
+    Sv F1 = sv0(), P = sv0(), X1 = sv0(), F2 = sv0(), P2 = sv0(), EGs = sv0(), OLs = sv0(), OAs = sv0(), OVs = sv0();
+    for (int b = 1; b < NB; b++) {
+      if (!((sub >> b) & 1u)) continue;
+      F1 = sv_add(F1, ld_sv(s.fb[b][FB_F1]));
+      P = sv_add(P, ld_sv(s.fb[b][FB_P]));
+      X1 = sv_add(X1, ld_sv(s.fb[b][FB_X1]));
+      F2 = sv_add(F2, ld_sv(s.fb[b][FB_F2]));
+      P2 = sv_add(P2, ld_sv(s.fb[b][FB_P2]));
+      EGs = sv_add(EGs, ld_sv(s.fb[b][FB_EG]));
+      OLs = sv_add(OLs, ld_sv(s.fb[b][FB_OL]));
+      OAs = sv_add(OAs, ld_sv(s.fb[b][FB_OA]));
+      OVs = sv_add(OVs, ld_sv(s.fb[b][FB_OV]));
+    }
+    Sv Vo = sv0(), Lo = sv0(), Yo = sv0(), Awo = sv0(), A1o = sv0(), A2o = sv0();
+    for (int k = 0; k < 3; k++) A1o.v[k] = -kGrav[k];
+    if (j >= 3 && j < 6) {
+      for (int k = 0; k < 3; k++) {
+        Vo.v[k] = s.qvel[k]; Lo.v[k] = s.lam[k]; Yo.v[k] = s.y[k]; Awo.v[k] = s.astar[k];
+        A1o.v[k] += s.astar[k]; A2o.v[k] = s.at[k];
+      }
+    } else if (j >= 6) {
+      const int p = cParent[bj];
+      Vo = ld_sv(s.tw[p][TW_V]); Lo = ld_sv(s.tw[p][TW_L]); Yo = ld_sv(s.tw[p][TW_Y]);
+      Awo = ld_sv(s.tw[p][TW_AW]); A1o = ld_sv(s.tw[p][TW_A1]); A2o = ld_sv(s.tw[p][TW_A2]);
+    }
+    const Sv Sj = ld_sv(s.S[j]);
+    const Sv sig = cross_mm(Sj, Vo), alp = cross_mm(Sj, A1o), ell = cross_mm(Sj, Lo);
+    const float dq1 = -sv_dot(ell, F1) - sv_dot(alp, P) + sv_dot(cross_mm(sig, Vo), P) + sv_dot(sig, X1);
+    Sv rho = sv0();
+    if (j >= 3) rho = sv_add(sig, cross_mm(Sj, ld_sv(s.tw[bj][TW_V])));
+    const float dv1 = -sv_dot(Sj, X1) - sv_dot(rho, P);
+    const float dq2 = -sv_dot(cross_mm(Sj, Yo), F2) - sv_dot(cross_mm(Sj, A2o), P2);
+    const float dqc = sv_dot(Sj, EGs) - sv_dot(Sj, sv_add(sv_add(cross_mf(Lo, OLs), cross_mf(Awo, OAs)),
+                                                          cross_mf(Vo, OVs)));
+    float gq = dq2 - dq1 + dqc + lgq, gv = -dv1 + sv_dot(Sj, OVs) + lgv;
+    if (j >= 6) {  // the PD actuator kp (u - q) - kv v, clamped at +-frclim
+      float wq = 1.f, wv = 1.f;
+      const unsigned long long cm = (unsigned long long)s.clampm[0] | (unsigned long long)s.clampm[1] << 32;
+      if ((cm >> j) & 1ull) {
+        if (clamp_kv == 0) { wq = 0.f; wv = 1.f; }
+        else if (clamp_kv == 1) { wq = wv = 0.f; }
+        else {
+          const float raw = cKp[j] * (s.ctrl[j - 6] - s.qpos[j + 1]) - cKv[j] * s.qvel[j];
+          const float ov = (fabsf(raw) - cFrclim[j]) / cFrclim[j];
+          wq = wv = clamp_soft > 0.f ? expf(-ov / clamp_soft) : 0.f;
+        }
+      }
+      gq -= wq * cKp[j] * s.lam[j];
+      gv -= wv * cKv[j] * s.lam[j];
+      s.ub[j - 6] += wq * cKp[j] * s.lam[j];
+    }
+    s.qb[j] = s.qn[j] + gq;
+    s.vb[j] = s.vt[j] + gv;
+  }
+  wsync();
+}
+
+__global__ __launch_bounds__(64) void k_adjoint(int nw, int nsub, const float* __restrict__ tape,
+                                                const float* __restrict__ fric, const float* __restrict__ com,
+                                                const float* __restrict__ gq_out, const float* __restrict__ gv_out,
+                                                float* __restrict__ gq_in, float* __restrict__ gv_in,
+                                                float* __restrict__ gctrl, int* __restrict__ info,
+                                                const float* __restrict__ ctrl, float clamp_soft, int clamp_kv,
+                                                int normal) {
+  __shared__ Adj s;
+  const int lane = threadIdx.x, w = blockIdx.x;
+  if (w >= nw) return;
+  const float* wt = tape + (size_t)w * nsub * REC_WORDS;
+  if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
+  if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = ctrl ? ctrl[(size_t)w * NU + lane] : 0.f; }
+  if (lane == 0) { s.fric = fric[w]; s.flags = 0; }
+  // the output cotangents in the tangent space at the output state (its root quaternion: the last substep's
+  // integration replayed from the record)
+  if (lane < NV) s.vb[lane] = gv_out[(size_t)w * NV + lane];
+  if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = gq_out[(size_t)w * NQ + (lane < 3 ? lane : lane + 1)];
+  if (lane == 0) {
+    const float* rec = wt + (size_t)(nsub - 1) * REC_WORDS;
+    float wv[3], q[4];
+    for (int k = 0; k < 3; k++) wv[k] = rec[REC_QVEL + 3 + k] + kH * rec[REC_AADV + 3 + k];
+    for (int k = 0; k < 4; k++) q[k] = rec[REC_QPOS + 3 + k];
+    const float nw = sqrtf(dot3(wv, wv));
+    if (nw > 0.f) {
+      float sa, ca, o[4];
+      sincosf(0.5f * kH * nw, &sa, &ca);
+      const float dq[4] = {ca, sa * wv[0] / nw, sa * wv[1] / nw, sa * wv[2] / nw};
+      qmul(q, dq, o);
+      const float on = rsqrtf(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
+      for (int k = 0; k < 4; k++) q[k] = o[k] * on;
+    }
+    const float* g = gq_out + (size_t)w * NQ + 3;
+    for (int k = 0; k < 3; k++) {
+      float e[4] = {0.f, 0.f, 0.f, 0.f}, t[4];
+      e[1 + k] = 1.f;
+      qmul(q, e, t);
+      s.qb[3 + k] = 0.5f * (t[0] * g[0] + t[1] * g[1] + t[2] * g[2] + t[3] * g[3]);
+    }
+  }
+  wsync();
+  for (int k = nsub - 1; k >= 0; k--) adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
+  // gradients: qpos form (the quaternion's 2 q (x) (0, t)), qvel, ctrl
+  float* oq = gq_in + (size_t)w * NQ;
+  if (lane < 3) oq[lane] = s.qb[lane];
+  if (lane >= 6 && lane < NV) oq[lane + 1] = s.qb[lane];
+  if (lane == 0) {
+    const float* q0 = wt + REC_QPOS + 3;
+    const float n = rsqrtf(q0[0] * q0[0] + q0[1] * q0[1] + q0[2] * q0[2] + q0[3] * q0[3]);
+    const float qq[4] = {q0[0] * n, q0[1] * n, q0[2] * n, q0[3] * n}, t[4] = {0.f, s.qb[3], s.qb[4], s.qb[5]};
+    float r[4];
+    qmul(qq, t, r);
+    for (int k = 0; k < 4; k++) oq[3 + k] = 2.f * r[k];
+  }
+  if (lane < NV) gv_in[(size_t)w * NV + lane] = s.vb[lane];
+  if (lane < NU) gctrl[(size_t)w * NU + lane] = s.ub[lane];
+  if (lane == 0) info[w] = s.flags;
+}
+
+int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                   const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal) {
+  if (nw <= 0) return 0;
+  hipLaunchKernelGGL(k_adjoint, dim3(nw), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in,
+                     gctrl, info, ctrl, clamp_soft, clamp_kv, normal);
+  return (int)hipGetLastError();
+}
+size_t adjoint_lds_bytes() { return sizeof(Adj); }
+
+}  // namespace g1k

@@ -6,12 +6,15 @@
 namespace g1k {
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info);
+                   int* info, float* ocon, float* tape);
 size_t forward_lds_bytes();
+size_t adjoint_lds_bytes();
+int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                   const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal);
 }  // namespace g1k
 
 namespace {
-constexpr int kNotBuilt = -2;  // an entry whose kernel is not in this build
 int check_device() {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -30,8 +33,7 @@ int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel,
                    int* info, float* ocon, float* tape, void* work) {
   (void)work;
   if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0) return (int)hipErrorInvalidValue;
-  if (tape || ocon) return kNotBuilt;
-  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info);
+  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape);
 }
 
 long long dk_fwd_work_bytes(int nw) {
@@ -46,16 +48,18 @@ int dk_fwd_upload(const float* consts, hipStream_t st) {
 }
 
 void dk_fwd_sizes(long long* o) {
-  o[0] = (long long)g1k::forward_lds_bytes(); o[1] = 0; o[2] = 0; o[3] = 36; o[4] = 35; o[5] = 64;
-  o[6] = -1; o[7] = -1; o[8] = 0;
+  o[0] = (long long)g1k::forward_lds_bytes(); o[1] = (long long)g1k::adjoint_lds_bytes(); o[2] = 1472; o[3] = 36;
+  o[4] = 35; o[5] = 64; o[6] = -1; o[7] = -1; o[8] = 1;
 }
 
 int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                const float* ctrl, float clamp_soft, int clamp_kv, int normal) {
-  (void)st; (void)nw; (void)nsub; (void)tape; (void)fric; (void)com; (void)gq_out; (void)gv_out; (void)gq_in;
-  (void)gv_in; (void)gctrl; (void)info; (void)ctrl; (void)clamp_soft; (void)clamp_kv; (void)normal;
-  return kNotBuilt;
+  if (nw < 0 || nsub < 1 || nsub > 32 || clamp_kv < 0 || clamp_kv > 2 || normal < 0 || normal > 3)
+    return (int)hipErrorInvalidValue;
+  if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
+  return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
+                             clamp_soft, clamp_kv, normal);
 }
 
 #define DK_VARIANT_DEF(KV, N)                                                                                        \

@@ -15,6 +15,7 @@ struct __align__(16) Sim {
   float O[4];
   float fric;
   int ncon, ncon_raw, nlim, nefc, flags, niter;
+  unsigned clampm[2];  // dofs whose actuator force is at its limit (tape)
   union {
     struct { float F[NB][4], T[NB][4], Ic[NB][12]; } sm;  // smooth dynamics: subtree force, moment about O, inertia
     struct { float gx[NGEOM][4], gq[NGEOM][4]; float stage[MAXCON][16]; unsigned short cand[NPAIR + 2]; } col;

@@ -17,6 +17,8 @@
 // Hessian as a 6x6 contact stiffness K_c = Phi' C Phi composited over subtrees exactly as CRBA composites inertia,
 // plus the cross-chain terms of contacts between two robot bodies.
 #include "g1_forward.h"
+#include "g1_collide.h"
+#include "g1_tape.h"
 
 namespace g1k {
 
@@ -202,6 +204,15 @@ __device__ void smooth(Sim& s, int lane) {
     }
     s.qsm[lane] = act - bias;
   }
+  {  // the clamp mask: the force at its limit (MuJoCo Warp's actuator_lam test, step.py:1773-1775)
+    float act = lane >= 6 && lane < NV ? cKp[lane] * (s.ctrl[lane - 6] - s.qpos[lane + 1]) - cKv[lane] * s.qvel[lane]
+                                       : 0.f;
+    const bool clamp = lane >= 6 && lane < NV &&
+                       (fminf(fmaxf(act, -cFrclim[lane]), cFrclim[lane]) <= -cFrclim[lane] ||
+                        fminf(fmaxf(act, -cFrclim[lane]), cFrclim[lane]) >= cFrclim[lane]);
+    const unsigned long long cm = ballot(clamp);
+    if (lane == 0) { s.clampm[0] = (unsigned)cm; s.clampm[1] = (unsigned)(cm >> 32); }
+  }
   wsync();
   // qacc_smooth = M^-1 qfrc_smooth
   float a[NV], dself = 1.f;
@@ -219,169 +230,6 @@ __device__ void smooth(Sim& s, int lane) {
 namespace g1k {
 
 // ============================================================================================== collision
-// MuJoCo's frame from a normal n: rows n, b, n x b with b the unit vector e_y (|n_y| < 0.5) or e_z made orthogonal to
-// n (step.py:378-387 make_frame)
-__device__ __forceinline__ void make_frame(const float* n, float* fr) {
-  float b[3] = {0.f, 0.f, 0.f};
-  if (-0.5f < n[1] && n[1] < 0.5f) b[1] = 1.f; else b[2] = 1.f;
-  float d = dot3(n, b);
-  for (int k = 0; k < 3; k++) b[k] -= n[k] * d;
-  float bn = sqrtf(dot3(b, b));
-  if (bn > 0.f) for (int k = 0; k < 3; k++) b[k] /= bn;
-  float c[3];
-  cross(n, b, c);
-  for (int k = 0; k < 3; k++) { fr[k] = n[k]; fr[3 + k] = b[k]; fr[6 + k] = c[k]; }
-}
-
-__device__ __forceinline__ void sphere_sphere(const float* p1, float r1, const float* p2, float r2, float* dist,
-                                              float* pos, float* n) {
-  float dir[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
-  float d = sqrtf(dot3(dir, dir));
-  if (d == 0.f) { n[0] = 1.f; n[1] = 0.f; n[2] = 0.f; } else { for (int k = 0; k < 3; k++) n[k] = dir[k] / d; }
-  *dist = d - (r1 + r2);
-  float hp = 0.5f * *dist + r1;
-  for (int k = 0; k < 3; k++) pos[k] = p1[k] + n[k] * hp;
-}
-
-__device__ __forceinline__ float plane_point(const float* p1, const float* n, const float* c, float r, float* pos) {
-  float dist = (dot3(c, n) - dot3(p1, n)) - r, hp = 0.5f * dist + r;
-  for (int k = 0; k < 3; k++) pos[k] = c[k] - n[k] * hp;
-  return dist;
-}
-
-__device__ __forceinline__ void zaxis(const float* q, float* a) {
-  const float ez[3] = {0.f, 0.f, 1.f};
-  qrot(q, ez, a);
-}
-
-struct Cand {  // up to two contacts of one pair: A then B
-  float d[2], pos[2][3], fr[2][9];
-  int slot[2];
-  bool has[2];
-};
-
-__device__ __forceinline__ void put(Cand& o, int which, int slot, float dist, const float* pos, const float* fr) {
-  // which is a compile-time 0 / 1 at every call site
-  o.has[which] = true;
-  o.d[which] = dist;
-  o.slot[which] = slot;
-  for (int k = 0; k < 3; k++) o.pos[which][k] = pos[k];
-  for (int k = 0; k < 9; k++) o.fr[which][k] = fr[k];
-}
-
-// narrowphase of pair pr (step.py:1042-1143 collide_pair), zero margin
-__device__ void collide_pair(const Sim& s, int pr, Cand& o) {
-  o.has[0] = o.has[1] = false;
-  const unsigned w = cPairW[pr];
-  const int g1 = w & 255u, g2 = (w >> 8) & 255u, cls = (w >> 21) & 7u;
-  float p1[3], q1[4], p2[3], q2[4];
-  for (int k = 0; k < 3; k++) { p1[k] = s.u.col.gx[g1][k]; p2[k] = s.u.col.gx[g2][k]; }
-  for (int k = 0; k < 4; k++) { q1[k] = s.u.col.gq[g1][k]; q2[k] = s.u.col.gq[g2][k]; }
-  const float r1 = cGsize[3 * g1], hl1 = cGsize[3 * g1 + 1], r2 = cGsize[3 * g2], hl2 = cGsize[3 * g2 + 1];
-  float pos[3], fr[9], n[3], dist;
-  if (cls == 0 || cls == 4) {  // plane (the floor) against a sphere or a capsule
-    zaxis(q1, n);
-    float dif[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
-    if (dot3(dif, n) > cGrb[g2]) return;
-    if (cls == 0) {
-      dist = plane_point(p1, n, p2, r2, pos);
-      make_frame(n, fr);
-      if (dist < 0.f) put(o, 0, 0, dist, pos, fr);
-    } else {
-      float axis[3];
-      zaxis(q2, axis);
-      // plane_capsule_frame (step.py:461-474): b = axis projected on the plane, normalized; make_frame's basis
-      // vector where the projection is shorter than 0.5
-      float na = dot3(n, axis), b[3];
-      for (int k = 0; k < 3; k++) b[k] = axis[k] - n[k] * na;
-      float bn = sqrtf(dot3(b, b));
-      if (bn > 0.f) for (int k = 0; k < 3; k++) b[k] /= bn;
-      if (bn < 0.5f) {
-        b[0] = b[1] = b[2] = 0.f;
-        if (-0.5f < n[1] && n[1] < 0.5f) b[1] = 1.f; else b[2] = 1.f;
-      }
-      float c[3];
-      cross(n, b, c);
-      for (int k = 0; k < 3; k++) { fr[k] = n[k]; fr[3 + k] = b[k]; fr[6 + k] = c[k]; }
-      float ce[3];
-      for (int k = 0; k < 3; k++) ce[k] = p2[k] + axis[k] * hl2;
-      dist = plane_point(p1, n, ce, r2, pos);
-      if (dist < 0.f) put(o, 0, 0, dist, pos, fr);
-      for (int k = 0; k < 3; k++) ce[k] = p2[k] - axis[k] * hl2;
-      dist = plane_point(p1, n, ce, r2, pos);
-      if (dist < 0.f) put(o, 1, 1, dist, pos, fr);
-    }
-    return;
-  }
-  {
-    float dif[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]}, rb = cGrb[g1] + cGrb[g2];
-    if (dot3(dif, dif) > rb * rb) return;
-  }
-  if (cls == 1) {  // sphere-sphere
-    sphere_sphere(p1, r1, p2, r2, &dist, pos, n);
-    if (dist < 0.f) { make_frame(n, fr); put(o, 0, 0, dist, pos, fr); }
-    return;
-  }
-  if (cls == 2) {  // sphere-capsule: the capsule segment's closest point (step.py:487-497 segment_point)
-    float axis[3], a[3], ab[3], ap[3], pt[3];
-    zaxis(q2, axis);
-    for (int k = 0; k < 3; k++) { a[k] = p2[k] - axis[k] * hl2; ab[k] = 2.f * axis[k] * hl2; ap[k] = p1[k] - a[k]; }
-    float gam = dot3(ab, ab) + 1e-6f, t = fminf(fmaxf(dot3(ap, ab) / gam, 0.f), 1.f);
-    for (int k = 0; k < 3; k++) pt[k] = a[k] + t * ab[k];
-    sphere_sphere(p1, r1, pt, r2, &dist, pos, n);
-    if (dist < 0.f) { make_frame(n, fr); put(o, 0, 0, dist, pos, fr); }
-    return;
-  }
-  // capsule-capsule (step.py:501-554 capcap_setup / capcap_params / capcap_candidate)
-  float a1[3], a2[3], d[3];
-  zaxis(q1, a1);
-  zaxis(q2, a2);
-  for (int k = 0; k < 3; k++) { a1[k] *= hl1; a2[k] *= hl2; d[k] = p1[k] - p2[k]; }
-  const float ma = dot3(a1, a1), mb = -dot3(a1, a2), mc = dot3(a2, a2), u = -dot3(a1, d), v = dot3(a2, d);
-  const float det = ma * mc - mb * mb;
-  if (fabsf(det) >= 1e-15f) {
-    float x1 = (mc * u - mb * v) / det, x2 = (ma * v - mb * u) / det;
-    if (x1 > 1.f) { x1 = 1.f; x2 = (v - mb) / mc; }
-    else if (x1 < -1.f) { x1 = -1.f; x2 = (v + mb) / mc; }
-    if (x2 > 1.f || x2 < -1.f) {
-      bool hi = x2 > 1.f;
-      x2 = hi ? 1.f : -1.f;
-      float raw = hi ? (u - mb) / ma : (u + mb) / ma;
-      x1 = fminf(fmaxf(raw, -1.f), 1.f);
-    }
-    float v1[3], v2[3];
-    for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
-    sphere_sphere(v1, r1, v2, r2, &dist, pos, n);
-    if (dist < 0.f) { make_frame(n, fr); put(o, 0, 0, dist, pos, fr); }
-  } else {
-    int cnt = 0;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      if (cnt >= 2) break;
-      float x1, x2;
-      if (e < 2) {
-        x1 = e == 0 ? 1.f : -1.f;
-        float raw = e == 0 ? (v - mb) / mc : (v + mb) / mc;
-        x2 = fminf(fmaxf(raw, -1.f), 1.f);
-      } else {
-        x2 = e == 2 ? 1.f : -1.f;
-        float raw = e == 2 ? (u - mb) / ma : (u + mb) / ma;
-        x1 = fminf(fmaxf(raw, -1.f), 1.f);
-      }
-      float v1[3], v2[3];
-      for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
-      sphere_sphere(v1, r1, v2, r2, &dist, pos, n);
-      if (dist <= 0.f) {
-        if (dist < 0.f) {
-          make_frame(n, fr);
-          if (!o.has[0]) put(o, 0, e, dist, pos, fr); else put(o, 1, e, dist, pos, fr);
-        }
-        cnt++;
-      }
-    }
-  }
-}
-
 // geom poses, broadphase, narrowphase; contacts in (pair, slot) order into s.u.col.stage
 __device__ void collision(Sim& s, int lane) {
   if (lane < NGEOM) {
@@ -429,7 +277,7 @@ __device__ void collision(Sim& s, int lane) {
     int pr = -1;
     if (c0 + lane < ncand) {
       pr = s.u.col.cand[c0 + lane];
-      collide_pair(s, pr, o);
+      collide_pair(s.u.col.gx, s.u.col.gq, pr, o);
     }
     const int n = (int)o.has[0] + (int)o.has[1];
     const int off = total + wscan_excl(n, lane);
@@ -540,7 +388,7 @@ __device__ __forceinline__ float matvec(const Sim& s, const float* v, int lane) 
 }
 
 // ============================================================================================== Newton
-struct NewtonOut { int it; bool conv; };
+struct NewtonOut { int it; bool conv, fresh; };  // fresh: s.L holds H's factor at the final zones
 
 // gradient at the current jar: grad = M a - qfrc_smooth - J' f, f = -D x on the rows with x < 0; returns |grad|
 __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
@@ -820,13 +668,36 @@ __device__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con, int iterations)
     conv = improvement < kTol || kScale * gn < kTol;
     if (conv) break;
   }
-  return NewtonOut{it, conv};
+  return NewtonOut{it, conv, it > 0 && zsame};
 }
 
 // ============================================================================================== one substep
-__device__ void substep(Sim& s, Rows& R, int lane, int iterations) {
+// tape store helper: n words of src (LDS) into the record and zeros up to the field's end (the padding: a record
+// does not depend on what the buffer held), lane-strided (coalesced)
+__device__ __forceinline__ void tape_put(float* dst, const float* src, int n, int end, int lane) {
+  for (int i = lane; i < end; i += WL) dst[i] = i < n ? src[i] : 0.f;
+}
+
+__device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, float* ocon) {
+  if (rec) {
+    tape_put(rec + REC_QPOS, s.qpos, NQ, REC_QVEL - REC_QPOS, lane);
+    tape_put(rec + REC_QVEL, s.qvel, NV, REC_ASTAR - REC_QVEL, lane);
+  }
   smooth(s, lane);
   collision(s, lane);
+  if (rec) {  // the contact table (pair | slot << 9), two per word, in contact (= row) order
+    const int nc = s.ncon;
+    if (lane < MAXCON / 2) {
+      unsigned e[2];
+      for (int t = 0; t < 2; t++) {
+        const int c = 2 * lane + t;
+        e[t] = c < nc ? ((unsigned)__float_as_int(s.u.col.stage[c][13]) | (unsigned)__float_as_int(s.u.col.stage[c][14]) << 9)
+                      : TAPE_CON_NONE;
+      }
+      rec[REC_CON + lane] = __uint_as_float(e[0] | e[1] << 16);
+    }
+    if (lane < 2) rec[REC_CLAMP + lane] = __uint_as_float(s.clampm[lane]);
+  }
   const int ncon = s.ncon;
   const bool con = lane < ncon;
   // this lane's contact
@@ -895,6 +766,34 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations) {
   wsync();
   const NewtonOut no = newton(s, R, lane, con, iterations);
   if (lane == 0) s.niter = no.it;
+  if (rec) {  // the final zones, and H's factor at them (assembled again when the last step changed a zone)
+    if (!no.fresh) {
+      float h[NV], dself = 1.f;
+      hessian(s, R, lane, con, h);
+      chol_rows(h, dself, lane);
+      store_rows(h, s.L, lane);
+      wsync();
+    }
+    tape_put(rec + REC_LH, s.L, NTRI, REC_LQ - REC_LH, lane);
+    unsigned cz = 0u;
+    for (int t = 0; t < 4; t++) cz |= (t < R.nr && R.jar[t] < 0.f) ? 1u << t : 0u;
+    // 4 bits per contact: lanes 8 w .. 8 w + 7 into word w (gathered by shuffles)
+    unsigned word = 0u;
+    for (int k = 0; k < 8; k++) word |= (unsigned)__shfl(cz, (lane & 7) * 8 + k, 64) << (4 * k);
+    if (lane < 8) rec[REC_CZONE + lane] = __uint_as_float(word);
+    const unsigned long long lz = ballot(R.lsg != 0.f && R.ljar < 0.f), lr = ballot(R.lsg != 0.f);
+    if (lane < 2) {
+      rec[REC_LIMZONE + lane] = __uint_as_float((unsigned)(lane ? lz >> 32 : lz));
+      rec[REC_LIMROW + lane] = __uint_as_float((unsigned)(lane ? lr >> 32 : lr));
+    }
+    tape_put(rec + REC_ASTAR, s.qacc, NV, REC_AADV - REC_ASTAR, lane);
+    if (lane == 0) {
+      rec[REC_HDR] = __uint_as_float((unsigned)s.ncon | (unsigned)s.nefc << 8 | (unsigned)s.nlim << 16
+                                     | (unsigned)min(no.it, 255) << 24);
+      rec[REC_FLAGS] = __uint_as_float((unsigned)(s.flags & 20) | (no.fresh ? 0u : (unsigned)FLAG_REFACT));
+    }
+    wsync();
+  }
   // implicitfast: (M + h kv) a_adv = M a*
   {
     float a[NV], dself = 1.f;
@@ -906,6 +805,10 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations) {
     wsync();
     const float adv = chol_solve_rows(a, dself, s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
     if (lane < NV) s.qvel[lane] += kH * adv;
+    if (rec) {
+      tape_put(rec + REC_LQ, s.L, NTRI, REC_WORDS - REC_LQ, lane);
+      if (lane < REC_LH - REC_AADV) rec[REC_AADV + lane] = lane < NV ? adv : 0.f;
+    }
     wsync();
   }
   if (lane == 0) {  // the free joint: position, then the orientation rotated by h times the local angular velocity
@@ -922,7 +825,12 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations) {
     }
   }
   if (lane >= 6 && lane < NV) s.qpos[lane + 1] += kH * s.qvel[lane];
-  (void)pair;
+  if (ocon) {  // this substep's contacts: pair, dist, pos, normal (pair -1 past the count)
+    float* o = ocon + 8 * lane;
+    o[0] = con ? (float)pair : -1.f;
+    o[1] = con ? dist : 0.f;
+    for (int k = 0; k < 3; k++) { o[2 + k] = con ? R.r[k] + s.O[k] : 0.f; o[5 + k] = con ? R.fr[k] : 0.f; }
+  }
   wsync();
 }
 
@@ -932,7 +840,8 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
                                                 const float* __restrict__ fric, const float* __restrict__ com,
                                                 int iterations, int nsub, float* __restrict__ oqpos,
                                                 float* __restrict__ oqvel, float* __restrict__ owarm,
-                                                int* __restrict__ info) {
+                                                int* __restrict__ info, float* __restrict__ ocon,
+                                                float* __restrict__ tape) {
   __shared__ Sim s;
   const int lane = threadIdx.x;
   const int w = blockIdx.x;
@@ -944,7 +853,9 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
   if (lane == 0) { s.fric = fric[w]; s.flags = 0; s.niter = 0; }
   wsync();
   Rows R;
-  for (int k = 0; k < nsub; k++) substep(s, R, lane, iterations);
+  for (int k = 0; k < nsub; k++)
+    substep(s, R, lane, iterations, tape ? tape + ((size_t)w * nsub + k) * REC_WORDS : nullptr,
+            ocon && k == nsub - 1 ? ocon + (size_t)w * MAXCON * 8 : nullptr);
   if (lane < NQ) oqpos[(size_t)w * NQ + lane] = s.qpos[lane];
   if (lane < NV) { oqvel[(size_t)w * NV + lane] = s.qvel[lane]; owarm[(size_t)w * NV + lane] = s.qacc[lane]; }
   if (lane == 0) {
@@ -960,10 +871,10 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
 namespace g1k {
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info) {
+                   int* info, float* ocon, float* tape) {
   if (nw <= 0) return 0;
   hipLaunchKernelGGL(k_forward, dim3(nw), dim3(64), 0, st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub,
-                     oq, ov, ow, info);
+                     oq, ov, ow, info, ocon, tape);
   return (int)hipGetLastError();
 }
 size_t forward_lds_bytes() { return sizeof(Sim); }

@@ -1,0 +1,23 @@
+// The forward tape: one record of REC_WORDS float32 words per world and substep (record w * nsub + k), what the
+// adjoint needs to differentiate the substep without re-solving it. Own layout (the reference's is tape.py:28-45):
+// integer fields are bit-cast into float words.
+#pragma once
+
+namespace g1k {
+constexpr int REC_HDR = 0;        // ncon | nefc << 8 | nlim << 16 | Newton iterations << 24
+constexpr int REC_FLAGS = 1;      // 4 contacts beyond capacity, 16 rows beyond capacity, 32 refactored at final zones
+constexpr int REC_CLAMP = 2;      // 2 words: dofs whose actuator force is at its limit (bit i: dof i)
+constexpr int REC_LIMZONE = 4;    // 2 words: dofs whose limit row is in its quadratic zone at a*
+constexpr int REC_LIMROW = 6;     // 2 words: dofs with a limit row
+constexpr int REC_CZONE = 8;      // 8 words: 4 bits per contact (bit t: pyramid edge t / the normal row quadratic)
+constexpr int REC_CON = 16;       // 32 words: contacts in row order, 16 bits each: pair | slot << 9
+constexpr int REC_QPOS = 48;      // 36: the substep's input qpos
+constexpr int REC_QVEL = 84;      // 35: input qvel
+constexpr int REC_ASTAR = 128;    // 35: Newton's final acceleration a*
+constexpr int REC_AADV = 164;     // 35: implicitfast's a_adv = (M + h kv)^-1 M a*
+constexpr int REC_LH = 200;       // 630: Cholesky factor of H = M + J'DJ at the final zones (packed lower, row-major)
+constexpr int REC_LQ = 832;       // 630: Cholesky factor of M + h kv
+constexpr int REC_WORDS = 1472;
+constexpr unsigned TAPE_CON_NONE = 0xFFFFu;
+constexpr int FLAG_REFACT = 32;
+}  // namespace g1k

@@ -1,0 +1,151 @@
+"""GPU parity of the adjoint (HIP kernel through the C ABI, via nablaengine_amd.torch_ffi) against float64 central
+finite differences (MuJoCo C's fd_vjp golden fixtures, and the float64 oracle's own FD) and the oracle's float64
+analytic VJP."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from nablaengine_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = 1e-4  # gradient median relative error <= 1e-4 against float64 central FD
+
+
+@pytest.fixture(scope="module")
+def ffi():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible")
+    from nablaengine_amd import torch_ffi
+    torch_ffi.init(0)
+    return torch_ffi
+
+
+def _t(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def _vjp_gpu(ffi, st, cq, cv, clamp_kv=1, normal=0):
+    import torch
+    args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    r = ffi.forward(*args, tape=True)
+    kw = dict(ctrl=args[3], clamp_soft=None) if clamp_kv == 2 else {}
+    gq, gv, gu, info = ffi.backward(r[4], args[4], args[5], _t(cq), _t(cv), clamp_kv=clamp_kv, normal=normal, **kw)
+    torch.cuda.synchronize()
+    return gq.cpu().numpy().astype(np.float64), gv.cpu().numpy().astype(np.float64), gu.cpu().numpy().astype(
+        np.float64), info.cpu().numpy(), r
+
+
+def _rel_rows(a, b):
+    return np.linalg.norm(a - b, axis=1) / np.maximum(np.linalg.norm(b, axis=1), 1e-12)
+
+
+@pytest.mark.parametrize("cname", ["mf_s0", "mf_s1"])
+def test_adjoint_vs_mujoco_fd_truth(ffi, cname):
+    """MuJoCo C float64 central FD VJPs (h = 1e-6, 3 cotangents per state) on the truth's G0 states, exact mode
+    (clamp_kv=1, normal=0): median relative error per block (qpos tangent / qvel / ctrl) <= 1e-4 (BASELINE gate), on
+    the columns the truth marks valid."""
+    g = np.load(os.path.join(GOLD, f"grad_{cname}.npz"))
+    sel = np.nonzero(g["G0"])[0]
+    n = len(sel)
+    st = {k: np.repeat(g[src][sel], 3, axis=0) for k, src in (("qpos", "qpos"), ("qvel", "qvel"),
+                                                              ("warm", "qacc_warmstart"), ("ctrl", "ctrl"),
+                                                              ("friction", "friction"), ("com", "com"))}
+    cq = g["cot_qpos"][sel].reshape(3 * n, 36)
+    cv = g["cot_qvel"][sel].reshape(3 * n, 35)
+    gq, gv, gu, info, _ = _vjp_gpu(ffi, st, cq, cv)
+    an = np.concatenate([oracle.qpos_tangent(st["qpos"].astype(np.float64), gq), gv, gu], 1)
+    fd = g["fd_vjp"][sel].reshape(3 * n, 99)
+    bad = np.repeat(g["bad"][sel] != 0, 3, axis=0)
+    for name, sl in (("qpos", slice(0, 35)), ("qvel", slice(35, 70)), ("ctrl", slice(70, 99))):
+        a, b = np.where(bad[:, sl], 0, an[:, sl]), np.where(bad[:, sl], 0, fd[:, sl])
+        e = _rel_rows(a, b)
+        print(f"{cname} {name}: median {np.median(e):.3g} p90 {np.percentile(e, 90):.3g}")
+        assert np.median(e) <= TOL, (name, np.median(e))
+    assert not (info & (1 << 13)).any(), "a replayed contact was not found"
+
+
+def test_adjoint_vs_oracle_config2(ffi):
+    """256 config-1 worlds, output cotangents N(0, 1); the float32 GPU VJP against the float64
+    oracle's analytic VJP (exact mode) at the engine's settings, and on 8 of the worlds against the oracle's float64
+    central FD (eps 1e-6): median relative error per block <= 1e-4."""
+    st = synthetic.states(256, config=1)
+    cq, cv = synthetic.cotangents(256)
+    gq, gv, gu, info, _ = _vjp_gpu(ffi, st, cq, cv)
+    s64 = {k: st[k].astype(np.float64) for k in st}
+    oq, ov, ou = oracle.vjp(**s64, g_qpos=cq, g_qvel=cv, clamp_kv=1, normal=0, **oracle.ENGINE)
+    for name, a, b in (("qpos", oracle.qpos_tangent(s64["qpos"], gq), oracle.qpos_tangent(s64["qpos"], oq)),
+                       ("qvel", gv, ov), ("ctrl", gu, ou)):
+        e = _rel_rows(a, b)
+        print(f"config2 vs analytic {name}: median {np.median(e):.3g} p90 {np.percentile(e, 90):.3g}")
+        assert np.median(e) <= TOL
+    errs = {"qpos": [], "qvel": [], "ctrl": []}
+    for i in range(8):
+        J = oracle.fd_jacobian(s64["qpos"][i], s64["qvel"][i], s64["warm"][i], s64["ctrl"][i], s64["friction"][i],
+                               s64["com"][i], h=1e-6, **oracle.TRUTH)
+        fd = np.concatenate([cq[i], cv[i]]).astype(np.float64) @ J
+        an = np.concatenate([oracle.qpos_tangent(s64["qpos"][i], gq[i]), gv[i], gu[i]])
+        for name, sl in (("qpos", slice(0, 35)), ("qvel", slice(35, 70)), ("ctrl", slice(70, 99))):
+            errs[name].append(np.linalg.norm(an[sl] - fd[sl]) / max(np.linalg.norm(fd[sl]), 1e-12))
+    for name, e in errs.items():
+        print(f"config2 vs FD {name}: median {np.median(e):.3g}")
+        assert np.median(e) <= TOL
+
+
+def test_tape_does_not_change_outputs(ffi):
+    """The forward's outputs are bitwise the same with and without the tape, and the tape is bitwise deterministic."""
+    import torch
+    st = synthetic.states(1024, config=1)
+    args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    a = ffi.forward(*args)
+    b = ffi.forward(*args, tape=True)
+    c = ffi.forward(*args, tape=True)
+    torch.cuda.synchronize()
+    for x, y in zip(a[:4], b[:4]):
+        assert torch.equal(x, y)
+    assert torch.equal(b[4].view(torch.int32), c[4].view(torch.int32))  # bitwise (the tape holds bit-cast ints)
+
+
+def test_autograd_matches_backward(ffi):
+    """torch_ffi.step under autograd: the gradients are backward()'s, warm' is not differentiable, grad_decay scales
+    the state gradients only; the backward is bitwise deterministic."""
+    import torch
+    st = synthetic.states(64, config=1)
+    cq, cv = synthetic.cotangents(64)
+    q, v, w, u, f, c = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    q.requires_grad_(True); v.requires_grad_(True); u.requires_grad_(True)
+    q1, v1, w1 = ffi.step(q, v, w, u, f, c)
+    assert not w1.requires_grad
+    ((q1 * _t(cq)).sum() + (v1 * _t(cv)).sum()).backward()
+    r = ffi.forward(q.detach(), v.detach(), w, u.detach(), f, c, tape=True)
+    gq, gv, gu, _ = ffi.backward(r[4], f, c, _t(cq), _t(cv))
+    gq2, gv2, gu2, _ = ffi.backward(r[4], f, c, _t(cq), _t(cv))
+    torch.cuda.synchronize()
+    assert torch.equal(q.grad, gq) and torch.equal(v.grad, gv) and torch.equal(u.grad, gu)
+    assert torch.equal(gq, gq2) and torch.equal(gv, gv2) and torch.equal(gu, gu2)
+    q.grad = v.grad = u.grad = None
+    q1, v1, w1 = ffi.step(q, v, w, u, f, c, grad_decay=0.5)
+    ((q1 * _t(cq)).sum() + (v1 * _t(cv)).sum()).backward()
+    torch.cuda.synchronize()
+    assert torch.allclose(q.grad, 0.5 * gq) and torch.allclose(v.grad, 0.5 * gv) and torch.equal(u.grad, gu)
+
+
+def test_adjoint_variants_run(ffi):
+    """Every (clamp_kv, normal) variant runs and is finite; clamp_kv 2 needs ctrl (ValueError without)."""
+    import torch
+    st = synthetic.states(128, config=1)
+    cq, cv = synthetic.cotangents(128)
+    args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    r = ffi.forward(*args, tape=True)
+    for kv in (0, 1, 2):
+        for n in (0, 1, 2, 3):
+            kw = dict(ctrl=args[3]) if kv == 2 else {}
+            out = ffi.backward(r[4], args[4], args[5], _t(cq), _t(cv), clamp_kv=kv, normal=n, **kw)
+            torch.cuda.synchronize()
+            assert all(torch.isfinite(x).all() for x in out[:3])
+    with pytest.raises(ValueError):
+        ffi.backward(r[4], args[4], args[5], _t(cq), _t(cv), clamp_kv=2)
