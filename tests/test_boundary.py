@@ -1,0 +1,80 @@
+"""The drop-in boundary without a GPU: the C ABI library exports every entry include/nablaengine_g1.h declares, the
+model constants committed match the model file, the Python surface validates its arguments and fails loudly without a
+GPU (no CPU fallback), and bench.py refuses more than one GPU."""
+import ctypes
+import json
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nablaengine_g1.h")
+LIB = os.path.join(ROOT, "nablaengine_amd", "libnablaengine_g1.so")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    names = set(re.findall(r"\b(dk_\w+)\s*\(", txt))
+    names = {n for n in names if "##" not in n and not n.startswith("dk_kv##")}
+    for kv in (0, 1, 2):
+        for n in (0, 1, 2, 3):
+            names |= {f"dk_kv{kv}_n{n}_adjoint", f"dk_kv{kv}_n{n}_upload", f"dk_kv{kv}_n{n}_sizes"}
+    return names
+
+
+def test_library_exports_every_declared_entry():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built (python -m nablaengine_amd.build)")
+    lib = ctypes.CDLL(LIB)
+    names = _declared()
+    assert len(names) >= 40
+    for n in sorted(names):
+        assert hasattr(lib, n), n
+    sizes = (ctypes.c_longlong * 9)()
+    lib.dk_fwd_sizes(sizes)
+    assert list(sizes)[2:6] == [1472, 36, 35, 64]
+    lib.dk_kv2_n1_sizes(sizes)
+    assert sizes[6] == 2 and sizes[7] == 1
+    assert lib.dk_fwd_work_bytes(4096) == 0
+
+
+def test_model_header_matches_json():
+    d = json.load(open(os.path.join(ROOT, "nablaengine_amd", "model", "g1_model.json")))
+    h = open(os.path.join(ROOT, "nablaengine_amd", "csrc", "g1_model.h")).read()
+    assert f"MEANINERTIA = {d['meaninertia']!r}" in h and "NPAIR = 502" in h and f"TORSO_BODY = {d['torso_body']}" in h
+    assert d["nq"] == 36 and d["nv"] == 35 and len(d["pair_g1"]) == 502 and d["body_names"][16] == "torso_link"
+
+
+@pytest.mark.skipif(not os.path.exists("/root/reference/fixtures/mjlab/g1_train.mjb"), reason="no model file here")
+def test_model_extraction_reproduces_committed_constants():
+    from nablaengine_amd.model import mjb_extract
+    f, bn = mjb_extract.extract()
+    d = mjb_extract.derive(f, bn)
+    committed = json.load(open(os.path.join(ROOT, "nablaengine_amd", "model", "g1_model.json")))
+    assert json.loads(json.dumps(d)) == committed
+
+
+def test_python_surface_errors_without_gpu():
+    import torch
+    from nablaengine_amd import synthetic, torch_ffi
+    st = synthetic.states(2, config=1)
+    args = [torch.from_numpy(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    with pytest.raises(TypeError):
+        torch_ffi.forward(*args)  # CPU tensors: no implicit copy, no CPU fallback
+    with pytest.raises(ValueError):
+        torch_ffi.step(*args, clamp_kv=5)
+    with pytest.raises(ValueError):
+        torch_ffi.backward(None, None, None, None, None, clamp_kv=0, clamp_soft=0.1)
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError):
+            torch_ffi.init()
+    assert torch_ffi.tape_bytes(4096) == 4096 * 4 * 1472 * 4
+
+
+def test_bench_refuses_several_gpus():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode != 0 and "one GPU" in r.stderr
