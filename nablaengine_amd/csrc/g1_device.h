@@ -138,46 +138,29 @@ __device__ __forceinline__ void chol_rows(float (&a)[NV], float& dself, int lane
   }
 }
 
-// x = A^-1 b given the factor: rows a[] in registers (chol_rows) also stored packed in Lp (LDS, TRI layout); b on
-// lane i (i < NV); returns x on lane i. Forward substitution from the registers, backward from Lp.
-__device__ __forceinline__ float chol_solve_rows(const float (&a)[NV], float dself, const float* Lp, float b,
-                                                 int lane) {
+// x = A^-1 b with the factor L packed in Lp (LDS, TRI layout; from chol_rows + store_rows); b and x on lane i < NV.
+// Forward substitution reads column k of L (lane i: L[i][k]), backward row k (lane i: L[k][i]); one v_readlane per
+// pivot broadcasts the solved entry.
+__device__ __forceinline__ float chol_solve(const float* Lp, float b, int lane) {
+  const int r = lane < NV ? lane : NV - 1;
+  const float dself = 1.f / Lp[tri(r, r)];
   float y = b;
-#pragma unroll
+#pragma unroll 7
   for (int k = 0; k < NV; k++) {
-    float yk = rdl(y * dself, k);
-    y = lane == k ? yk : (lane > k ? fmaf(-a[k], yk, y) : y);
-  }
-  // backward: x_k = y_k / L_kk, then y_i -= L[k][i] x_k for i < k
-  float x = y;
-#pragma unroll
-  for (int k = NV - 1; k >= 0; k--) {
-    float xk = rdl(x * dself, k);
-    float lki = lane < k ? Lp[tri(k, lane)] : 0.f;
-    x = lane == k ? xk : (lane < k ? fmaf(-lki, xk, x) : x);
-  }
-  return x;
-}
-
-// the same solve with the factor only in Lp (a factor kept from an earlier Newton iteration)
-__device__ __forceinline__ float chol_resolve(const float* Lp, float b, int lane) {
-  float dself = lane < NV ? 1.f / Lp[tri(lane < NV ? lane : 0, lane < NV ? lane : 0)] : 0.f;
-  float y = b;
-#pragma unroll
-  for (int k = 0; k < NV; k++) {
-    float yk = rdl(y * dself, k);
-    float lik = lane > k && lane < NV ? Lp[tri(lane, k)] : 0.f;
+    const float yk = rdl(y * dself, k);
+    const float lik = lane > k && lane < NV ? Lp[tri(lane, k)] : 0.f;
     y = lane == k ? yk : (lane > k ? fmaf(-lik, yk, y) : y);
   }
   float x = y;
-#pragma unroll
+#pragma unroll 7
   for (int k = NV - 1; k >= 0; k--) {
-    float xk = rdl(x * dself, k);
-    float lki = lane < k ? Lp[tri(k, lane)] : 0.f;
+    const float xk = rdl(x * dself, k);
+    const float lki = lane < k ? Lp[tri(k, lane)] : 0.f;
     x = lane == k ? xk : (lane < k ? fmaf(-lki, xk, x) : x);
   }
   return x;
 }
+__device__ __forceinline__ float chol_resolve(const float* Lp, float b, int lane) { return chol_solve(Lp, b, lane); }
 
 // store the factor rows (register a[], lane = row) packed into Lp
 __device__ __forceinline__ void store_rows(const float (&a)[NV], float* Lp, int lane) {

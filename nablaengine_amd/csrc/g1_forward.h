@@ -6,18 +6,18 @@ namespace g1k {
 
 struct __align__(16) Sim {
   float qpos[40], qvel[36], qacc[36], ctrl[32], com[4];
-  float qsm[36], qacc0[36], Ma[36], grad[36], p[36], Mp[36], vtmp[36];
+  float qsm[36], qacc0[36], Ma[36], grad[36], p[36], Mp[36];
   float M[NTRI + 2];
   float L[NTRI + 2];
   float S[NV][8];             // dof motion subspaces about O: angular (0..2), velocity of O (4..6)
   float Q[NB][4], X[NB][4];   // body poses
-  float ha[NB][4];            // hinge rotations
   float O[4];
   float fric;
   int ncon, ncon_raw, nlim, nefc, flags, niter;
   unsigned clampm[2];  // dofs whose actuator force is at its limit (tape)
   union {
-    struct { float F[NB][4], T[NB][4], Ic[NB][12]; } sm;  // smooth dynamics: subtree force, moment about O, inertia
+    struct { float F[NB][4], T[NB][4], Ic[NB][12], ha[NB][4]; } sm;  // smooth dynamics: subtree force, moment about O,
+                                                                     // inertia; hinge rotations
     struct { float gx[NGEOM][4], gq[NGEOM][4]; float stage[MAXCON][16]; unsigned short cand[NPAIR + 2]; } col;
     struct {
       float bw[NB][8];  // body spatial velocity of a dof vector: angular (0..2), velocity of O (4..6)

@@ -22,6 +22,15 @@
 
 namespace g1k {
 
+// factor the packed matrix in s.L in place (rows in registers on the way, lane = row)
+__device__ __forceinline__ void factor_L(Sim& s, int lane) {
+  float h[NV], dself = 1.f;
+  load_rows(s.L, h, lane);
+  chol_rows(h, dself, lane);
+  store_rows(h, s.L, lane);
+  wsync();
+}
+
 // ============================================================================================== smooth dynamics
 // motion subspace S_i of dof i about O: angular w (world), velocity of the point O (source.py:316-329 dof_motion)
 __device__ __forceinline__ void dof_motion(const Sim& s, int i, float* w, float* v) {
@@ -56,10 +65,10 @@ __device__ void smooth(Sim& s, int lane) {
   if (lane >= 2 && lane < NB) {  // hinge rotations, one lane per body
     float sn, cs;
     sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
-    s.ha[lane][0] = cs;
-    s.ha[lane][1] = sn * cAxis[3 * lane];
-    s.ha[lane][2] = sn * cAxis[3 * lane + 1];
-    s.ha[lane][3] = sn * cAxis[3 * lane + 2];
+    s.u.sm.ha[lane][0] = cs;
+    s.u.sm.ha[lane][1] = sn * cAxis[3 * lane];
+    s.u.sm.ha[lane][2] = sn * cAxis[3 * lane + 1];
+    s.u.sm.ha[lane][3] = sn * cAxis[3 * lane + 2];
   }
   wsync();
   // FK: each body lane walks its own chain from the root: pose, velocity, and the bias acceleration (qacc = 0;
@@ -81,7 +90,7 @@ __device__ void smooth(Sim& s, int lane) {
       const float qb[4] = {cQuat[4 * k], cQuat[4 * k + 1], cQuat[4 * k + 2], cQuat[4 * k + 3]};
       const float pb[3] = {cPos[3 * k], cPos[3 * k + 1], cPos[3 * k + 2]};
       const float ax[3] = {cAxis[3 * k], cAxis[3 * k + 1], cAxis[3 * k + 2]};
-      const float ha[4] = {s.ha[k][0], s.ha[k][1], s.ha[k][2], s.ha[k][3]};
+      const float ha[4] = {s.u.sm.ha[k][0], s.u.sm.ha[k][1], s.u.sm.ha[k][2], s.u.sm.ha[k][3]};
       qmul(Q, qb, q0);
       qrot(Q, pb, t);  // r = X_child - X_parent
       for (int c = 0; c < 3; c++) r[c] = t[c];
@@ -186,16 +195,15 @@ __device__ void smooth(Sim& s, int lane) {
     for (int k = 0; k < 10; k++) Jb[k] = s.u.sm.Ic[bi][k];
     apply_inertia(Jb, w, v, n, f);
     const uint64_t anc = cTree.dofanc[lane];
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-      if (j <= lane && ((anc >> j) & 1ull)) {
-        float mij = s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
-                    + s.S[j][6] * f[2];
+#pragma unroll 2
+    for (int j = 0; j <= lane; j++) {
+      float mij = 0.f;
+      if ((anc >> j) & 1ull) {
+        mij = s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
+              + s.S[j][6] * f[2];
         if (j == lane) mij += cArm[lane];
-        s.M[tri(lane, j)] = mij;
-      } else if (j <= lane) {
-        s.M[tri(lane, j)] = 0.f;
       }
+      s.M[tri(lane, j)] = mij;
     }
     float act = 0.f;
     if (lane >= 6) {
@@ -215,12 +223,10 @@ __device__ void smooth(Sim& s, int lane) {
   }
   wsync();
   // qacc_smooth = M^-1 qfrc_smooth
-  float a[NV], dself = 1.f;
-  load_rows(s.M, a, lane);
-  chol_rows(a, dself, lane);
-  store_rows(a, s.L, lane);
+  for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
   wsync();
-  float x = chol_solve_rows(a, dself, s.L, lane < NV ? s.qsm[lane] : 0.f, lane);
+  factor_L(s, lane);
+  float x = chol_solve(s.L, lane < NV ? s.qsm[lane] : 0.f, lane);
   if (lane < NV) s.qacc0[lane] = x;
   wsync();
 }
@@ -379,7 +385,7 @@ __device__ __forceinline__ void rows_jv(Sim& s, const Rows& R, const float* v, i
 __device__ __forceinline__ float matvec(const Sim& s, const float* v, int lane) {
   if (lane >= NV) return 0.f;
   float acc = 0.f, acc2 = 0.f;
-#pragma unroll
+#pragma unroll 5
   for (int j = 0; j < NV; j++) {
     const float m = s.M[j <= lane ? tri(lane, j) : tri(j, lane)];
     if (j & 1) acc2 = fmaf(m, v[j], acc2); else acc = fmaf(m, v[j], acc);
@@ -448,8 +454,8 @@ __device__ void refresh(Sim& s, Rows& R, int lane, bool con) {
   R.ljar = ljv - R.laref;
 }
 
-// H = M + J' D J on the rows with x < 0 (lane = row of H, into registers h), then its factor
-__device__ void hessian(Sim& s, const Rows& R, int lane, bool con, float (&h)[NV]) {
+// H = M + J' D J on the rows with x < 0, packed into s.L (lane i writes row i)
+__device__ __forceinline__ void hessian(Sim& s, const Rows& R, int lane, bool con) {
   const int ncon = s.ncon;
   // the contact's 6x6 stiffness K = Phi' C Phi about O, C from the pyramid rows' curvatures in the frame basis
   bool act = false;
@@ -506,7 +512,7 @@ __device__ void hessian(Sim& s, const Rows& R, int lane, bool con, float (&h)[NV
   }
   wsync();
   // rows of H: M, then S_j . (Kc_body(i) S_i) on the ancestor dofs j of i
-  load_rows(s.M, h, lane);
+  for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
   if (lane < NV) {
     const int bi = lane < 6 ? 1 : lane - 4;
     const float* k = s.u.nt.h.kb[bi];
@@ -519,16 +525,15 @@ __device__ void hessian(Sim& s, const Rows& R, int lane, bool con, float (&h)[NV
     f[0] = k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
     f[1] = k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
     f[2] = k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
-    const uint64_t anc = cTree.dofanc[lane];
-#pragma unroll
-    for (int j = 0; j < NV; j++)
-      if ((anc >> j) & 1ull)
-        h[j] += s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
-                + s.S[j][6] * f[2];
-    if (R.lsg != 0.f && R.ljar < 0.f) {
-#pragma unroll
-      for (int j = 0; j < NV; j++) if (j == lane) h[j] += R.lD;
+    const int nch = cTree.nchain[bi];
+#pragma unroll 2
+    for (int t = 0; t < nch; t++) {  // the chain of dof i's body: its ancestor dofs (and the root's j <= i)
+      const int j = cTree.chain[bi][t];
+      if (j <= lane)
+        s.L[tri(lane, j)] += s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0]
+                             + s.S[j][5] * f[1] + s.S[j][6] * f[2];
     }
+    if (R.lsg != 0.f && R.ljar < 0.f) s.L[tri(lane, lane)] += R.lD;
   }
   // contacts between two robot bodies: the cross-chain terms -(p2_i p1_j + p1_i p2_j) S_i' K S_j
   for (unsigned long long m = selfm; m; m &= m - 1ull) {
@@ -555,20 +560,21 @@ __device__ void hessian(Sim& s, const Rows& R, int lane, bool con, float (&h)[NV
       const float p1 = (float)((dm >> b1) & 1u), p2 = (float)((dm >> b2) & 1u);
       const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]},
                   v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
-#pragma unroll
-      for (int j = 0; j < NV; j++) {
-        if (j <= lane) {
-          const float* y = s.u.nt.h.y[j];
-          const float coef = p2 * y[3] + p1 * y[7];
-          h[j] -= coef * (w[0] * y[0] + w[1] * y[1] + w[2] * y[2] + v[0] * y[4] + v[1] * y[5] + v[2] * y[6]);
-        }
+#pragma unroll 2
+      for (int j = 0; j <= lane; j++) {
+        const float* y = s.u.nt.h.y[j];
+        const float coef = p2 * y[3] + p1 * y[7];
+        s.L[tri(lane, j)] -= coef * (w[0] * y[0] + w[1] * y[1] + w[2] * y[2] + v[0] * y[4] + v[1] * y[5]
+                                     + v[2] * y[6]);
       }
     }
     wsync();
   }
+  wsync();
 }
 
-__device__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con, int iterations) {
+
+__device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con, int iterations) {
   // warm start against qacc_smooth: keep the cheaper (step.py:1974-1988)
   refresh(s, R, lane, con);
   float cost = wsum(lane_cost(s, R, lane));
@@ -594,12 +600,9 @@ __device__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con, int iterations)
     if (zsame) {  // no row changed its zone in the last step: H, and so its factor in s.L, are unchanged
       p = chol_resolve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     } else {
-      float h[NV], dself = 1.f;
-      hessian(s, R, lane, con, h);
-      chol_rows(h, dself, lane);
-      store_rows(h, s.L, lane);
-      wsync();
-      p = chol_solve_rows(h, dself, s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
+      hessian(s, R, lane, con);
+      factor_L(s, lane);
+      p = chol_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     }
     if (lane < NV) s.p[lane] = p;
     wsync();
@@ -768,11 +771,8 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
   if (lane == 0) s.niter = no.it;
   if (rec) {  // the final zones, and H's factor at them (assembled again when the last step changed a zone)
     if (!no.fresh) {
-      float h[NV], dself = 1.f;
-      hessian(s, R, lane, con, h);
-      chol_rows(h, dself, lane);
-      store_rows(h, s.L, lane);
-      wsync();
+      hessian(s, R, lane, con);
+      factor_L(s, lane);
     }
     tape_put(rec + REC_LH, s.L, NTRI, REC_LQ - REC_LH, lane);
     unsigned cz = 0u;
@@ -796,14 +796,12 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
   }
   // implicitfast: (M + h kv) a_adv = M a*
   {
-    float a[NV], dself = 1.f;
-    load_rows(s.M, a, lane);
-#pragma unroll
-    for (int j = 0; j < NV; j++) if (j == lane) a[j] += kH * cKv[lane];
-    chol_rows(a, dself, lane);
-    store_rows(a, s.L, lane);
+    for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
     wsync();
-    const float adv = chol_solve_rows(a, dself, s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
+    if (lane < NV) s.L[tri(lane, lane)] += kH * cKv[lane];
+    wsync();
+    factor_L(s, lane);
+    const float adv = chol_solve(s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
     if (lane < NV) s.qvel[lane] += kH * adv;
     if (rec) {
       tape_put(rec + REC_LQ, s.L, NTRI, REC_WORDS - REC_LQ, lane);
