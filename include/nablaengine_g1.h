@@ -28,6 +28,12 @@ int dk_fwd_upload(const float* consts, hipStream_t st);
  * world and substep, nq, nv, max contacts, clamp_kv, normal, the tape's flags word offset (o[6], o[7] -1: runtime). */
 void dk_fwd_sizes(long long* o);
 
+/* No counterpart in the reference's ABI (its DK_PROFILE builds read g_prof the same way, host.py:13-17): in a build
+ * with -DG1_PROFILE, copies the last forward's per-world phase cycles (s_memtime) of the first nw worlds, nw x 13
+ * uint64 (smooth, collision, rows, Newton init, Hessian, factor, solve, line search, update, gradient, implicitfast,
+ * tape, Newton iterations); returns -1 in the production build. */
+int dk_prof_read(unsigned long long* out, int nw);
+
 /* Replaces <variant>_adjoint (jax_ffi.py:228-241) for every (clamp_kv, normal) variant at once: the VJP of one control
  * step from its tape. in: tape (nw, nsub * DK_REC_WORDS), fric, com as the forward's, gq_out (nw, 36), gv_out (nw, 35)
  * the output cotangents, ctrl (nw, 29) (clamp_kv 2 only, else may be NULL), clamp_soft (clamp_kv 2); out: gq_in (nw, 36)

@@ -8,6 +8,7 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnablaengine_g1.so")
+PROF_LIB = os.path.join(HERE, "libnablaengine_g1_prof.so")
 SOURCES = ["g1_forward.hip", "g1_adjoint.hip", "g1_capi.hip"]
 ARCH = os.environ.get("NABLA_OFFLOAD_ARCH", "gfx950")
 # packed FP32 instructions off (-packed-fp32-ops): the kernels are written for scalar FP32
@@ -15,13 +16,15 @@ FLAGS = ["-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared", "-Xc
          "-packed-fp32-ops", "-ffp-contract=fast", "-Wno-unused-command-line-argument"]
 
 
-def build(verbose=False):
+def build(verbose=False, profile=False):
     """Compile every HIP source into the library (a temporary file renamed into place: a running process that
-    has the old library loaded keeps it)."""
+    has the old library loaded keeps it). profile=True builds libnablaengine_g1_prof.so with the phase counters
+    (-DG1_PROFILE), a measurement build."""
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    target = PROF_LIB if profile else LIB
     fd, tmp = tempfile.mkstemp(prefix="libnablaengine_g1.", suffix=".so.tmp", dir=HERE)
     os.close(fd)
-    cmd = [hipcc] + FLAGS + ["-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES]
+    cmd = [hipcc] + FLAGS + (["-DG1_PROFILE"] if profile else []) + ["-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES]
     if verbose:
         print(" ".join(cmd))
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -29,9 +32,9 @@ def build(verbose=False):
         os.unlink(tmp)
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError(f"hipcc failed ({r.returncode})")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, target)
+    return target
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, profile="--profile" in sys.argv))

@@ -9,6 +9,7 @@ int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel,
                    int* info, float* ocon, float* tape);
 size_t forward_lds_bytes();
 size_t adjoint_lds_bytes();
+int prof_read(unsigned long long* out, int nw);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                    const float* ctrl, float clamp_soft, int clamp_kv, int normal);
@@ -46,6 +47,9 @@ int dk_fwd_upload(const float* consts, hipStream_t st) {
   (void)st;
   return check_device();
 }
+
+// the profiling build's per-world phase cycles of the last forward (test and measurement helper; -1 in production)
+int dk_prof_read(unsigned long long* out, int nw) { return g1k::prof_read(out, nw); }
 
 void dk_fwd_sizes(long long* o) {
   o[0] = (long long)g1k::forward_lds_bytes(); o[1] = (long long)g1k::adjoint_lds_bytes(); o[2] = 1472; o[3] = 36;

@@ -63,21 +63,31 @@ __device__ __forceinline__ unsigned long long ballot(bool p) { return __ballot(p
 __device__ __forceinline__ int prefix_count(unsigned long long m, int lane) {  // set bits of m below lane
   return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
 }
-// sum over the wave's 64 lanes, the same fixed butterfly order on every call (bitwise deterministic)
+// Sum over the wave's 64 lanes by DPP: an inclusive scan within each row of 16 lanes (row_shr 1, 2, 4, 8), then
+// row_bcast 15 / 31 carry the row totals up, so lane 63 holds the total; v_readlane broadcasts it as a wave-uniform
+// scalar. A fixed order on every call (bitwise deterministic); lanes without a DPP source add +0.
+#define G1_DPP(x, ctrl, rmask) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), (ctrl), (rmask), 0xf, false))
 __device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += G1_DPP(v, 0x111, 0xf);  // row_shr:1
+  v += G1_DPP(v, 0x112, 0xf);  // row_shr:2
+  v += G1_DPP(v, 0x114, 0xf);  // row_shr:4
+  v += G1_DPP(v, 0x118, 0xf);  // row_shr:8
+  v += G1_DPP(v, 0x142, 0xa);  // row_bcast:15 into rows 1, 3
+  v += G1_DPP(v, 0x143, 0xc);  // row_bcast:31 into rows 2, 3
+  return rdl(v, 63);
 }
 __device__ __forceinline__ float2 wsum2(float a, float b) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) { a += __shfl_xor(a, o, 64); b += __shfl_xor(b, o, 64); }
-  return make_float2(a, b);
+  a += G1_DPP(a, 0x111, 0xf); b += G1_DPP(b, 0x111, 0xf);
+  a += G1_DPP(a, 0x112, 0xf); b += G1_DPP(b, 0x112, 0xf);
+  a += G1_DPP(a, 0x114, 0xf); b += G1_DPP(b, 0x114, 0xf);
+  a += G1_DPP(a, 0x118, 0xf); b += G1_DPP(b, 0x118, 0xf);
+  a += G1_DPP(a, 0x142, 0xa); b += G1_DPP(b, 0x142, 0xa);
+  a += G1_DPP(a, 0x143, 0xc); b += G1_DPP(b, 0x143, 0xc);
+  return make_float2(rdl(a, 63), rdl(b, 63));
 }
-__device__ __forceinline__ int wsumi(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+__device__ __forceinline__ int wsumi(int v) {  // small counts: exact in float
+  return (int)wsum((float)v);
 }
 // exclusive prefix sum of small non-negative ints over the wave (Hillis-Steele on shuffles)
 __device__ __forceinline__ int wscan_excl(int v, int lane) {
@@ -90,6 +100,21 @@ __device__ __forceinline__ int wscan_excl(int v, int lane) {
   return x - v;
 }
 __device__ __forceinline__ void wsync() { __syncthreads(); }
+
+// Phase profile (a G1_PROFILE build only): per world, s_memtime cycles of the forward's phases summed over the substeps
+// (lane 0's clock at phase ends, after a barrier), written to g_prof[world][phase] for the first PROF_WORLDS worlds
+// and read by dk_prof_read. The production build compiles every mark to nothing.
+enum { PH_SMOOTH = 0, PH_COLLIDE, PH_ROWS, PH_NINIT, PH_HESS, PH_FACTOR, PH_SOLVE, PH_LSEARCH, PH_UPDATE, PH_GRAD,
+       PH_IMPLICIT, PH_TAPE, PH_ITERS, NPHASE };
+constexpr int PROF_WORLDS = 16384;
+#ifdef G1_PROFILE
+__device__ inline unsigned long long g_prof[PROF_WORLDS][NPHASE];
+#define PROF_DECL unsigned long long prof_t = __builtin_amdgcn_s_memtime(); unsigned long long prof_acc[NPHASE] = {0};
+#define PROF_MARK(acc, t, k) do { wsync(); unsigned long long t_ = __builtin_amdgcn_s_memtime(); (acc)[k] += t_ - (t); (t) = t_; } while (0)
+#else
+#define PROF_DECL
+#define PROF_MARK(acc, t, k) do { } while (0)
+#endif
 
 // ------------------------------------------------------------------------------------------------ 3D helpers
 __device__ __forceinline__ void qmul(const float* a, const float* b, float* o) {

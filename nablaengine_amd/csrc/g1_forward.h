@@ -15,6 +15,9 @@ struct __align__(16) Sim {
   float fric;
   int ncon, ncon_raw, nlim, nefc, flags, niter;
   unsigned clampm[2];  // dofs whose actuator force is at its limit (tape)
+#ifdef G1_PROFILE
+  unsigned long long prof_t, prof_acc[NPHASE];
+#endif
   union {
     struct { float F[NB][4], T[NB][4], Ic[NB][12], ha[NB][4]; } sm;  // smooth dynamics: subtree force, moment about O,
                                                                      // inertia; hinge rotations

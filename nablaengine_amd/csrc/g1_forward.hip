@@ -20,6 +20,8 @@
 #include "g1_collide.h"
 #include "g1_tape.h"
 
+#define PROF(k) PROF_MARK(s.prof_acc, s.prof_t, k)
+
 namespace g1k {
 
 // factor the packed matrix in s.L in place (rows in registers on the way, lane = row)
@@ -597,13 +599,20 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
   bool conv = false, zsame = false;
   while (it < iterations) {
     float p;
+    PROF(PH_NINIT);
     if (zsame) {  // no row changed its zone in the last step: H, and so its factor in s.L, are unchanged
       p = chol_resolve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     } else {
       hessian(s, R, lane, con);
+      PROF(PH_HESS);
       factor_L(s, lane);
+      PROF(PH_FACTOR);
       p = chol_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     }
+    PROF(PH_SOLVE);
+#ifdef G1_PROFILE
+    if (lane == 0) s.prof_acc[PH_ITERS] += 1;
+#endif
     if (lane < NV) s.p[lane] = p;
     wsync();
     // exact line search along p on the piecewise-quadratic cost (step.py:2032-2084)
@@ -644,6 +653,7 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
       zprev = z;
       alpha = nx;
     }
+    PROF(PH_LSEARCH);
     // move along p
     if (lane < NV) {
       s.qacc[lane] += alpha * p;
@@ -664,7 +674,9 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
     zsame = ballot(chg) == 0ull;
     wsync();
     const float newcost = wsum(lane_cost(s, R, lane));
+    PROF(PH_UPDATE);
     const float gn = newton_grad(s, R, lane, con);
+    PROF(PH_GRAD);
     const float improvement = kScale * (cost - newcost);
     cost = newcost;
     it++;
@@ -686,8 +698,11 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
     tape_put(rec + REC_QPOS, s.qpos, NQ, REC_QVEL - REC_QPOS, lane);
     tape_put(rec + REC_QVEL, s.qvel, NV, REC_ASTAR - REC_QVEL, lane);
   }
+  PROF(PH_TAPE);
   smooth(s, lane);
+  PROF(PH_SMOOTH);
   collision(s, lane);
+  PROF(PH_COLLIDE);
   if (rec) {  // the contact table (pair | slot << 9), two per word, in contact (= row) order
     const int nc = s.ncon;
     if (lane < MAXCON / 2) {
@@ -767,7 +782,9 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
     for (int t = 0; t < 4; t++) R.aref[t] = 0.f;
   }
   wsync();
+  PROF(PH_ROWS);
   const NewtonOut no = newton(s, R, lane, con, iterations);
+  PROF(PH_NINIT);
   if (lane == 0) s.niter = no.it;
   if (rec) {  // the final zones, and H's factor at them (assembled again when the last step changed a zone)
     if (!no.fresh) {
@@ -794,6 +811,7 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
     }
     wsync();
   }
+  PROF(PH_TAPE);
   // implicitfast: (M + h kv) a_adv = M a*
   {
     for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
@@ -823,6 +841,7 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
     }
   }
   if (lane >= 6 && lane < NV) s.qpos[lane + 1] += kH * s.qvel[lane];
+  PROF(PH_IMPLICIT);
   if (ocon) {  // this substep's contacts: pair, dist, pos, normal (pair -1 past the count)
     float* o = ocon + 8 * lane;
     o[0] = con ? (float)pair : -1.f;
@@ -849,6 +868,10 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
   if (lane < NU) s.ctrl[lane] = ctrl[(size_t)w * NU + lane];
   if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
   if (lane == 0) { s.fric = fric[w]; s.flags = 0; s.niter = 0; }
+#ifdef G1_PROFILE
+  if (lane < NPHASE) s.prof_acc[lane] = 0;
+  if (lane == 0) s.prof_t = __builtin_amdgcn_s_memtime();
+#endif
   wsync();
   Rows R;
   for (int k = 0; k < nsub; k++)
@@ -856,6 +879,10 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
             ocon && k == nsub - 1 ? ocon + (size_t)w * MAXCON * 8 : nullptr);
   if (lane < NQ) oqpos[(size_t)w * NQ + lane] = s.qpos[lane];
   if (lane < NV) { oqvel[(size_t)w * NV + lane] = s.qvel[lane]; owarm[(size_t)w * NV + lane] = s.qacc[lane]; }
+#ifdef G1_PROFILE
+  wsync();
+  if (lane < NPHASE && w < PROF_WORLDS) g_prof[w][lane] = s.prof_acc[lane];
+#endif
   if (lane == 0) {
     info[4 * w] = s.niter;
     info[4 * w + 1] = s.ncon_raw;
@@ -876,4 +903,12 @@ int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel,
   return (int)hipGetLastError();
 }
 size_t forward_lds_bytes() { return sizeof(Sim); }
+int prof_read(unsigned long long* out, int nw) {  // the G1_PROFILE build's per-world phase cycles (nw x NPHASE)
+#ifdef G1_PROFILE
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), sizeof(unsigned long long) * NPHASE * (size_t)nw);
+#else
+  (void)out; (void)nw;
+  return -1;
+#endif
+}
 }  // namespace g1k
