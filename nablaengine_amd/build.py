@@ -11,9 +11,12 @@ LIB = os.path.join(HERE, "libnablaengine_g1.so")
 PROF_LIB = os.path.join(HERE, "libnablaengine_g1_prof.so")
 SOURCES = ["g1_forward.hip", "g1_adjoint.hip", "g1_capi.hip"]
 ARCH = os.environ.get("NABLA_OFFLOAD_ARCH", "gfx950")
-# packed FP32 instructions off (-packed-fp32-ops): the kernels are written for scalar FP32
+# packed FP32 instructions off (-packed-fp32-ops): the kernels are written for scalar FP32. Warnings that mark
+# undefined behaviour the optimizer exploits (a non-void function falling off its end becomes unreachable code, and a
+# kernel then runs into whatever follows) are errors.
 FLAGS = ["-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared", "-Xclang", "-target-feature", "-Xclang",
-         "-packed-fp32-ops", "-ffp-contract=fast", "-Wno-unused-command-line-argument"]
+         "-packed-fp32-ops", "-ffp-contract=fast", "-Wno-unused-command-line-argument", "-Werror=return-type",
+         "-Werror=uninitialized", "-Werror=sometimes-uninitialized", "-Werror=array-bounds"]
 
 
 def build(verbose=False, profile=False):

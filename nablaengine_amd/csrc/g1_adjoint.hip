@@ -446,13 +446,13 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   for (int i = lane; i < NTRI; i += WL) s.L[i] = rec[REC_LQ + i];
   wsync();
   const float aab = lane < NV ? kH * s.vt[lane] : 0.f;
-  const float y = chol_resolve(s.L, aab, lane);
+  const float y = ltl_solve(s.L, aab, lane);
   if (lane < NV) s.y[lane] = y;
   wsync();
   for (int i = lane; i < NTRI; i += WL) s.L[i] = rec[REC_LH + i];
   wsync();
   const float asb = lane < NV ? aab - kH * cKv[lane] * y : 0.f;
-  const float lam = chol_resolve(s.L, asb, lane);
+  const float lam = ltl_solve(s.L, asb, lane);
   if (lane < NV) s.lam[lane] = lam;
   wsync();
   // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body
@@ -696,7 +696,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   wsync();
 }
 
-__global__ __launch_bounds__(64) void k_adjoint(int nw, int nsub, const float* __restrict__ tape,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_adjoint(int nw, int nsub, const float* __restrict__ tape,
                                                 const float* __restrict__ fric, const float* __restrict__ com,
                                                 const float* __restrict__ gq_out, const float* __restrict__ gv_out,
                                                 float* __restrict__ gq_in, float* __restrict__ gv_in,

@@ -147,58 +147,55 @@ __device__ __forceinline__ float rsqrt_nr(float d) {
   return y * (1.5f - 0.5f * d * y * y);
 }
 
-// ------------------------------------------------------------------------------------------------ Cholesky
-// In-place LL^T of the SPD matrix whose row `lane` is a[0..NV-1] (entries j <= lane; above the diagonal ignored),
-// right-looking, pivot column broadcast by v_readlane: afterwards a[j] = L[lane][j] (j < lane), a[lane] = L[lane][lane]
-// and dself = 1 / L[lane][lane]. Lanes >= NV carry garbage that is never read.
-__device__ __forceinline__ void chol_rows(float (&a)[NV], float& dself, int lane) {
+// ------------------------------------------------------------------------------------------------ LTL factorization
+// A = L' L with L lower triangular, eliminated leaf-first (k = NV-1 .. 0), as MuJoCo factors M: with parents before
+// children in the dof order, row k of L is nonzero only at k's ancestor dofs (no fill-in) for a matrix with the
+// tree's sparsity (M, and H = M + J'DJ when no contact couples two robot bodies). Lane j holds column j of the lower
+// triangle in registers (c[m] = A[m][j], m >= j), so row k's entries L[k][j] are lane-local and L[k][m] is one
+// v_readlane away: step k is one pivot and, per ancestor m of k, a broadcast and one FMA on every lane.
+// SPARSE = false visits every m < k (the dense factor of a matrix with cross-branch entries). In place in Lp (packed
+// lower, TRI layout).
+template <bool SPARSE>
+__device__ __forceinline__ void ltl_factor(float* Lp, int lane) {
+  float c[NV];
 #pragma unroll
-  for (int k = 0; k < NV; k++) {
-    float d = fmaxf(rdl(a[k], k), 1e-30f);
-    float inv = rsqrt_nr(d);
-    dself = lane == k ? inv : dself;
-    a[k] = lane == k ? d * inv : a[k] * inv;
+  for (int m = 0; m < NV; m++) c[m] = (m >= lane && lane < NV) ? Lp[tri(m, lane)] : 0.f;
 #pragma unroll
-    for (int j = k + 1; j < NV; j++) a[j] = fmaf(-a[k], rdl(a[k], j), a[j]);
+  for (int k = NV - 1; k >= 0; k--) {
+    const float d = fmaxf(rdl(c[k], k), 1e-30f);
+    const float inv = rsqrt_nr(d);
+    c[k] = lane == k ? d * inv : c[k] * inv;  // L[k][k] on lane k, L[k][j] = A[k][j] / L[k][k] on lane j
+#pragma unroll
+    for (int m = 0; m < k; m++) {
+      if (SPARSE && !((TREE.dofanc[k] >> m) & 1ull)) continue;  // compile-time: m not an ancestor of k
+      c[m] = fmaf(-c[k], rdl(c[k], m), c[m]);  // A[m][j] -= L[k][j] L[k][m]
+    }
   }
+#pragma unroll
+  for (int m = 0; m < NV; m++)
+    if (m >= lane && lane < NV) Lp[tri(m, lane)] = c[m];
 }
 
-// x = A^-1 b with the factor L packed in Lp (LDS, TRI layout; from chol_rows + store_rows); b and x on lane i < NV.
-// Forward substitution reads column k of L (lane i: L[i][k]), backward row k (lane i: L[k][i]); one v_readlane per
-// pivot broadcasts the solved entry.
-__device__ __forceinline__ float chol_solve(const float* Lp, float b, int lane) {
+// x = A^-1 b for A = L' L (ltl_factor), b and x on lane i < NV: L' y = b leaf-first (reads row i of L: lane k takes
+// L[i][k]), then L x = y root-first (lane k takes L[k][j]); one v_readlane per pivot broadcasts the solved entry.
+__device__ __forceinline__ float ltl_solve(const float* Lp, float b, int lane) {
   const int r = lane < NV ? lane : NV - 1;
   const float dself = 1.f / Lp[tri(r, r)];
   float y = b;
 #pragma unroll 7
-  for (int k = 0; k < NV; k++) {
-    const float yk = rdl(y * dself, k);
-    const float lik = lane > k && lane < NV ? Lp[tri(lane, k)] : 0.f;
-    y = lane == k ? yk : (lane > k ? fmaf(-lik, yk, y) : y);
+  for (int i = NV - 1; i >= 0; i--) {
+    const float yi = rdl(y * dself, i);
+    const float lik = lane < i ? Lp[tri(i, lane)] : 0.f;
+    y = lane == i ? yi : (lane < i ? fmaf(-lik, yi, y) : y);
   }
   float x = y;
 #pragma unroll 7
-  for (int k = NV - 1; k >= 0; k--) {
+  for (int k = 0; k < NV; k++) {
     const float xk = rdl(x * dself, k);
-    const float lki = lane < k ? Lp[tri(k, lane)] : 0.f;
-    x = lane == k ? xk : (lane < k ? fmaf(-lki, xk, x) : x);
+    const float lkj = lane > k && lane < NV ? Lp[tri(lane, k)] : 0.f;
+    x = lane == k ? xk : (lane > k ? fmaf(-lkj, xk, x) : x);
   }
   return x;
-}
-__device__ __forceinline__ float chol_resolve(const float* Lp, float b, int lane) { return chol_solve(Lp, b, lane); }
-
-// store the factor rows (register a[], lane = row) packed into Lp
-__device__ __forceinline__ void store_rows(const float (&a)[NV], float* Lp, int lane) {
-#pragma unroll
-  for (int j = 0; j < NV; j++)
-    if (lane < NV && j <= lane) Lp[tri(lane, j)] = a[j];
-}
-
-// load row `lane` of a packed symmetric matrix (lower part j <= lane) into registers
-__device__ __forceinline__ void load_rows(const float* Ap, float (&a)[NV], int lane) {
-  int r = lane < NV ? lane : NV - 1;
-#pragma unroll
-  for (int j = 0; j < NV; j++) a[j] = j <= r ? Ap[tri(r, j)] : 0.f;
 }
 
 }  // namespace g1k

@@ -24,12 +24,11 @@
 
 namespace g1k {
 
-// factor the packed matrix in s.L in place (rows in registers on the way, lane = row)
-__device__ __forceinline__ void factor_L(Sim& s, int lane) {
-  float h[NV], dself = 1.f;
-  load_rows(s.L, h, lane);
-  chol_rows(h, dself, lane);
-  store_rows(h, s.L, lane);
+// factor the packed matrix in s.L in place as L' L; dense when a contact couples two robot bodies (cross-branch
+// entries), else with the tree's sparsity
+__device__ __forceinline__ void factor_L(Sim& s, int lane, bool dense = false) {
+  if (dense) ltl_factor<false>(s.L, lane);
+  else ltl_factor<true>(s.L, lane);
   wsync();
 }
 
@@ -228,7 +227,7 @@ __device__ void smooth(Sim& s, int lane) {
   for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
   wsync();
   factor_L(s, lane);
-  float x = chol_solve(s.L, lane < NV ? s.qsm[lane] : 0.f, lane);
+  float x = ltl_solve(s.L, lane < NV ? s.qsm[lane] : 0.f, lane);
   if (lane < NV) s.qacc0[lane] = x;
   wsync();
 }
@@ -456,8 +455,9 @@ __device__ void refresh(Sim& s, Rows& R, int lane, bool con) {
   R.ljar = ljv - R.laref;
 }
 
-// H = M + J' D J on the rows with x < 0, packed into s.L (lane i writes row i)
-__device__ __forceinline__ void hessian(Sim& s, const Rows& R, int lane, bool con) {
+// H = M + J' D J on the rows with x < 0, packed into s.L (lane i writes row i); returns whether a contact between two
+// robot bodies put entries outside the tree's sparsity
+__device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool con) {
   const int ncon = s.ncon;
   // the contact's 6x6 stiffness K = Phi' C Phi about O, C from the pyramid rows' curvatures in the frame basis
   bool act = false;
@@ -573,6 +573,7 @@ __device__ __forceinline__ void hessian(Sim& s, const Rows& R, int lane, bool co
     wsync();
   }
   wsync();
+  return selfm != 0ull;
 }
 
 
@@ -601,13 +602,13 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
     float p;
     PROF(PH_NINIT);
     if (zsame) {  // no row changed its zone in the last step: H, and so its factor in s.L, are unchanged
-      p = chol_resolve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
+      p = ltl_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     } else {
-      hessian(s, R, lane, con);
+      const bool dense = hessian(s, R, lane, con);
       PROF(PH_HESS);
-      factor_L(s, lane);
+      factor_L(s, lane, dense);
       PROF(PH_FACTOR);
-      p = chol_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
+      p = ltl_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     }
     PROF(PH_SOLVE);
 #ifdef G1_PROFILE
@@ -693,7 +694,7 @@ __device__ __forceinline__ void tape_put(float* dst, const float* src, int n, in
   for (int i = lane; i < end; i += WL) dst[i] = i < n ? src[i] : 0.f;
 }
 
-__device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, float* ocon) {
+__device__ __forceinline__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, float* ocon) {
   if (rec) {
     tape_put(rec + REC_QPOS, s.qpos, NQ, REC_QVEL - REC_QPOS, lane);
     tape_put(rec + REC_QVEL, s.qvel, NV, REC_ASTAR - REC_QVEL, lane);
@@ -788,8 +789,8 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
   if (lane == 0) s.niter = no.it;
   if (rec) {  // the final zones, and H's factor at them (assembled again when the last step changed a zone)
     if (!no.fresh) {
-      hessian(s, R, lane, con);
-      factor_L(s, lane);
+      const bool dense = hessian(s, R, lane, con);
+      factor_L(s, lane, dense);
     }
     tape_put(rec + REC_LH, s.L, NTRI, REC_LQ - REC_LH, lane);
     unsigned cz = 0u;
@@ -819,7 +820,7 @@ __device__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, f
     if (lane < NV) s.L[tri(lane, lane)] += kH * cKv[lane];
     wsync();
     factor_L(s, lane);
-    const float adv = chol_solve(s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
+    const float adv = ltl_solve(s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
     if (lane < NV) s.qvel[lane] += kH * adv;
     if (rec) {
       tape_put(rec + REC_LQ, s.L, NTRI, REC_WORDS - REC_LQ, lane);

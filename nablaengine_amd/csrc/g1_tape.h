@@ -15,8 +15,8 @@ constexpr int REC_QPOS = 48;      // 36: the substep's input qpos
 constexpr int REC_QVEL = 84;      // 35: input qvel
 constexpr int REC_ASTAR = 128;    // 35: Newton's final acceleration a*
 constexpr int REC_AADV = 164;     // 35: implicitfast's a_adv = (M + h kv)^-1 M a*
-constexpr int REC_LH = 200;       // 630: Cholesky factor of H = M + J'DJ at the final zones (packed lower, row-major)
-constexpr int REC_LQ = 832;       // 630: Cholesky factor of M + h kv
+constexpr int REC_LH = 200;       // 630: factor L of H = L' L = M + J'DJ at the final zones (packed lower, row-major)
+constexpr int REC_LQ = 832;       // 630: factor L of M + h kv = L' L
 constexpr int REC_WORDS = 1472;
 constexpr unsigned TAPE_CON_NONE = 0xFFFFu;
 constexpr int FLAG_REFACT = 32;
