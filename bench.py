@@ -28,6 +28,20 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 # interface bytes per world-step (inputs 556 B, outputs 440 B), the design-independent HBM traffic of the forward
 IO_BYTES_FWD = (36 + 35 + 35 + 29 + 1 + 3) * 4 + (36 + 35 + 35) * 4 + 16
+# HBM bytes per forward launch at 4096 worlds, measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (two runs,
+# each scaled by the same counter's reading on a copy of known size, `--copy-mib`); the summary holds the command
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_forward_4096_traffic.md")
+
+
+def measured_traffic(worlds):
+    """Bytes per forward launch from the committed traffic summary (line `traffic_bytes_per_launch: N`), or None
+    when there is none for this world count."""
+    if worlds != 4096 or not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
 
 
 def cpu_baseline(seconds=10.0):
@@ -61,6 +75,9 @@ def main():
     ap.add_argument("--worlds", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--flop-sample", type=int, default=512, help="worlds the flop count is taken on")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="before the timed steps, copy a buffer of this many MiB 3 times (a kernel of known HBM "
+                         "traffic that calibrates rocprofv3's FETCH_SIZE and WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (the worlds are independent; a multi-GPU "
@@ -69,6 +86,13 @@ def main():
     import torch
     from nablaengine_amd import synthetic, torch_ffi
     torch_ffi.init(0)
+    if a.copy_mib:
+        src = torch.ones(a.copy_mib << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     B = a.worlds
     st = synthetic.states(B, config=1)
     args = [torch.from_numpy(st[k]).cuda() for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
@@ -120,7 +144,7 @@ def main():
         "ms_per_step_fwd_vjp": vjp_ms,
         "world_steps_per_s_fwd_vjp": None if vjp_ms is None else B * 1e3 / vjp_ms,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_FP32_TFLOPS, "traffic": None,
+                     "frac": achieved / PEAK_FP32_TFLOPS, "traffic": measured_traffic(B),
                      "note": "FP32 vector (VALU) work, no MFMA: achieved = closed-form algorithmic flops "
                              f"({fl:.3g} per world-step, float64 restatement on {len(sub['qpos'])} of the worlds) x "
                              "worlds / the forward kernel's mean duration (HIP events, its stream); one kernel "
