@@ -165,11 +165,14 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane) {
     const float d = fmaxf(rdl(c[k], k), 1e-30f);
     const float inv = rsqrt_nr(d);
     c[k] = lane == k ? d * inv : c[k] * inv;  // L[k][k] on lane k, L[k][j] = A[k][j] / L[k][k] on lane j
+    // every broadcast of the step first, then the updates: a v_readlane's SGPR is not read by the next instruction
+    float bc[NV];
 #pragma unroll
-    for (int m = 0; m < k; m++) {
-      if (SPARSE && !((TREE.dofanc[k] >> m) & 1ull)) continue;  // compile-time: m not an ancestor of k
-      c[m] = fmaf(-c[k], rdl(c[k], m), c[m]);  // A[m][j] -= L[k][j] L[k][m]
-    }
+    for (int m = 0; m < k; m++)
+      if (!SPARSE || ((TREE.dofanc[k] >> m) & 1ull)) bc[m] = rdl(c[k], m);  // compile-time ancestor test
+#pragma unroll
+    for (int m = 0; m < k; m++)
+      if (!SPARSE || ((TREE.dofanc[k] >> m) & 1ull)) c[m] = fmaf(-c[k], bc[m], c[m]);  // A[m][j] -= L[k][j] L[k][m]
   }
 #pragma unroll
   for (int m = 0; m < NV; m++)
@@ -178,24 +181,27 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane) {
 
 // x = A^-1 b for A = L' L (ltl_factor), b and x on lane i < NV: L' y = b leaf-first (reads row i of L: lane k takes
 // L[i][k]), then L x = y root-first (lane k takes L[k][j]); one v_readlane per pivot broadcasts the solved entry.
+// Each lane keeps its running value scaled by 1 / L[lane][lane], so the value broadcast at step i is already the
+// solved entry, and the entries it is multiplied with are pre-scaled the same way and zeroed on lanes that take no
+// update: a step is one v_readlane and one FMA on the dependency chain. The factor entries are loaded from clamped
+// (always valid) addresses without a lane condition, so the loads are issued ahead of the chain.
 __device__ __forceinline__ float ltl_solve(const float* Lp, float b, int lane) {
   const int r = lane < NV ? lane : NV - 1;
-  const float dself = 1.f / Lp[tri(r, r)];
-  float y = b;
-#pragma unroll 7
-  for (int i = NV - 1; i >= 0; i--) {
-    const float yi = rdl(y * dself, i);
-    const float lik = lane < i ? Lp[tri(i, lane)] : 0.f;
-    y = lane == i ? yi : (lane < i ? fmaf(-lik, yi, y) : y);
+  const float dself = lane < NV ? 1.f / Lp[tri(r, r)] : 0.f;
+  float z = b * dself;  // (b - sum of the solved descendants' terms) / L[lane][lane]
+#pragma unroll
+  for (int i = NV - 1; i >= 1; i--) {
+    const float lik = Lp[tri(i, r < i ? r : i)] * (lane < i ? dself : 0.f);
+    z = fmaf(-lik, rdl(z, i), z);
   }
-  float x = y;
-#pragma unroll 7
-  for (int k = 0; k < NV; k++) {
-    const float xk = rdl(x * dself, k);
-    const float lkj = lane > k && lane < NV ? Lp[tri(lane, k)] : 0.f;
-    x = lane == k ? xk : (lane > k ? fmaf(-lkj, xk, x) : x);
+  // z = y; root-first: x[lane] = (y[lane] - sum_{k < lane} L[lane][k] x[k]) / L[lane][lane]
+  z *= dself;
+#pragma unroll
+  for (int k = 0; k < NV - 1; k++) {
+    const float lkj = Lp[tri(r > k ? r : k, k)] * (lane > k ? dself : 0.f);
+    z = fmaf(-lkj, rdl(z, k), z);
   }
-  return x;
+  return z;
 }
 
 }  // namespace g1k
