@@ -19,7 +19,9 @@ extern "C" {
 int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
                    int* info, float* ocon, float* tape, void* work);
-/* Replaces <fwd>_work_bytes (jax_ffi.py:265): scratch bytes the forward needs for nw worlds (0: none). */
+/* Replaces <fwd>_work_bytes (jax_ffi.py:265): scratch bytes the forward's work buffer takes for nw worlds (the
+ * dispatch order, heaviest worlds first: 8 bytes per world). work = NULL runs the worlds in index order instead; the
+ * results are the same either way. */
 long long dk_fwd_work_bytes(int nw);
 /* Replaces <unit>_upload (jax_ffi.py:214-225): the model constants are compiled into this library, so the call only
  * checks that the current device can run the kernels; consts may be NULL. */
@@ -29,9 +31,9 @@ int dk_fwd_upload(const float* consts, hipStream_t st);
 void dk_fwd_sizes(long long* o);
 
 /* No counterpart in the reference's ABI (its DK_PROFILE builds read g_prof the same way, host.py:13-17): in a build
- * with -DG1_PROFILE, copies the last forward's per-world phase cycles (s_memtime) of the first nw worlds, nw x 13
+ * with -DG1_PROFILE, copies the last forward's per-world phase cycles (s_memtime) of the first nw worlds, nw x 15
  * uint64 (smooth, collision, rows, Newton init, Hessian, factor, solve, line search, update, gradient, implicitfast,
- * tape, Newton iterations); returns -1 in the production build. */
+ * tape, Newton iterations, line-search evaluations, dense factorizations); returns -1 in the production build. */
 int dk_prof_read(unsigned long long* out, int nw);
 
 /* Replaces <variant>_adjoint (jax_ffi.py:228-241) for every (clamp_kv, normal) variant at once: the VJP of one control
@@ -41,6 +43,14 @@ int dk_prof_read(unsigned long long* out, int nw);
 int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                const float* ctrl, float clamp_soft, int clamp_kv, int normal);
+
+/* No counterpart in the reference's ABI (its adjoint entries take no work buffer): dk_adjoint with a work buffer of
+ * dk_adjoint_work_bytes(nw) bytes, in which the worlds are ordered heaviest first (the tape's row counts) before the
+ * launch. Same results as dk_adjoint, which is this entry with work = NULL. */
+int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work);
+long long dk_adjoint_work_bytes(int nw);
 
 /* The reference's per-variant unit names (jax_ffi.py:180,845-846: dk_kv{0,1,2}_n{0..3}), each the entry above with
  * its (clamp_kv, normal) fixed; _upload and _sizes as dk_fwd_upload / dk_fwd_sizes (o[6], o[7] the variant). */

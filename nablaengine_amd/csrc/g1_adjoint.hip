@@ -702,10 +702,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                                                 float* __restrict__ gq_in, float* __restrict__ gv_in,
                                                 float* __restrict__ gctrl, int* __restrict__ info,
                                                 const float* __restrict__ ctrl, float clamp_soft, int clamp_kv,
-                                                int normal) {
+                                                int normal, const int* __restrict__ perm) {
   __shared__ Adj s;
-  const int lane = threadIdx.x, w = blockIdx.x;
-  if (w >= nw) return;
+  const int lane = threadIdx.x;
+  if ((int)blockIdx.x >= nw) return;
+  const int w = perm ? perm[blockIdx.x] : (int)blockIdx.x;  // heaviest worlds first (g1_order.hip)
   const float* wt = tape + (size_t)w * nsub * REC_WORDS;
   if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
   if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = ctrl ? ctrl[(size_t)w * NU + lane] : 0.f; }
@@ -755,12 +756,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane == 0) info[w] = s.flags;
 }
 
+int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
-                   const float* ctrl, float clamp_soft, int clamp_kv, int normal) {
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work) {
   if (nw <= 0) return 0;
+  const int* perm = nullptr;
+  if (work) {  // the dispatch order, heaviest worlds first
+    const int rc = launch_order_adj(st, nw, nsub, tape, work);
+    if (rc) return rc;
+    perm = (const int*)work;
+  }
   hipLaunchKernelGGL(k_adjoint, dim3(nw), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in,
-                     gctrl, info, ctrl, clamp_soft, clamp_kv, normal);
+                     gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm);
   return (int)hipGetLastError();
 }
 size_t adjoint_lds_bytes() { return sizeof(Adj); }

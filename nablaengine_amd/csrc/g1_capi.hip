@@ -6,13 +6,14 @@
 namespace g1k {
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info, float* ocon, float* tape);
+                   int* info, float* ocon, float* tape, void* work);
+size_t order_work_bytes(int nw);
 size_t forward_lds_bytes();
 size_t adjoint_lds_bytes();
 int prof_read(unsigned long long* out, int nw);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
-                   const float* ctrl, float clamp_soft, int clamp_kv, int normal);
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work);
 }  // namespace g1k
 
 namespace {
@@ -32,15 +33,12 @@ extern "C" {
 int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
                    int* info, float* ocon, float* tape, void* work) {
-  (void)work;
   if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0) return (int)hipErrorInvalidValue;
-  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape);
+  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
+                             work);
 }
 
-long long dk_fwd_work_bytes(int nw) {
-  (void)nw;
-  return 0;
-}
+long long dk_fwd_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }
 
 int dk_fwd_upload(const float* consts, hipStream_t st) {
   (void)consts;
@@ -56,14 +54,23 @@ void dk_fwd_sizes(long long* o) {
   o[4] = 35; o[5] = 64; o[6] = -1; o[7] = -1; o[8] = 1;
 }
 
-int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
-               const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
-               const float* ctrl, float clamp_soft, int clamp_kv, int normal) {
+int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work) {
   if (nw < 0 || nsub < 1 || nsub > 32 || clamp_kv < 0 || clamp_kv > 2 || normal < 0 || normal > 3)
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
   return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
-                             clamp_soft, clamp_kv, normal);
+                             clamp_soft, clamp_kv, normal, work);
+}
+
+long long dk_adjoint_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }
+
+int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+               const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+               const float* ctrl, float clamp_soft, int clamp_kv, int normal) {
+  return dk_adjoint_work(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl, clamp_soft,
+                         clamp_kv, normal, nullptr);
 }
 
 #define DK_VARIANT_DEF(KV, N)                                                                                        \

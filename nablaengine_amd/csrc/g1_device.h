@@ -105,7 +105,7 @@ __device__ __forceinline__ void wsync() { __syncthreads(); }
 // (lane 0's clock at phase ends, after a barrier), written to g_prof[world][phase] for the first PROF_WORLDS worlds
 // and read by dk_prof_read. The production build compiles every mark to nothing.
 enum { PH_SMOOTH = 0, PH_COLLIDE, PH_ROWS, PH_NINIT, PH_HESS, PH_FACTOR, PH_SOLVE, PH_LSEARCH, PH_UPDATE, PH_GRAD,
-       PH_IMPLICIT, PH_TAPE, PH_ITERS, NPHASE };
+       PH_IMPLICIT, PH_TAPE, PH_ITERS, PH_LSEVAL, PH_DENSE, NPHASE };
 constexpr int PROF_WORLDS = 16384;
 #ifdef G1_PROFILE
 __device__ inline unsigned long long g_prof[PROF_WORLDS][NPHASE];

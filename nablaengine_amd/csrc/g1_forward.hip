@@ -27,6 +27,9 @@ namespace g1k {
 // factor the packed matrix in s.L in place as L' L; dense when a contact couples two robot bodies (cross-branch
 // entries), else with the tree's sparsity
 __device__ __forceinline__ void factor_L(Sim& s, int lane, bool dense = false) {
+#ifdef G1_PROFILE
+  if (dense && lane == 0) s.prof_acc[PH_DENSE] += 1;
+#endif
   if (dense) ltl_factor<false>(s.L, lane);
   else ltl_factor<true>(s.L, lane);
   wsync();
@@ -642,6 +645,9 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
       }
       if (ballot(!(newton_step && z == zprev)) == 0ull) break;  // the Newton step kept every row on its piece
       if (k == 40) break;
+#ifdef G1_PROFILE
+      if (lane == 0) s.prof_acc[PH_LSEVAL] += 1;
+#endif
       const float2 ff = wsum2(fd, fdd);
       fd = ff.x + a1 + alpha * a2;
       fdd = ff.y + a2;
@@ -859,11 +865,11 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
                                                 int iterations, int nsub, float* __restrict__ oqpos,
                                                 float* __restrict__ oqvel, float* __restrict__ owarm,
                                                 int* __restrict__ info, float* __restrict__ ocon,
-                                                float* __restrict__ tape) {
+                                                float* __restrict__ tape, const int* __restrict__ perm) {
   __shared__ Sim s;
   const int lane = threadIdx.x;
-  const int w = blockIdx.x;
-  if (w >= nw) return;
+  if ((int)blockIdx.x >= nw) return;
+  const int w = perm ? perm[blockIdx.x] : (int)blockIdx.x;  // heaviest worlds first (g1_order.hip)
   if (lane < NQ) s.qpos[lane] = qpos[(size_t)w * NQ + lane];
   if (lane < NV) { s.qvel[lane] = qvel[(size_t)w * NV + lane]; s.qacc[lane] = warm[(size_t)w * NV + lane]; }
   if (lane < NU) s.ctrl[lane] = ctrl[(size_t)w * NU + lane];
@@ -895,12 +901,19 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
 }  // namespace g1k
 
 namespace g1k {
+int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work);
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info, float* ocon, float* tape) {
+                   int* info, float* ocon, float* tape, void* work) {
   if (nw <= 0) return 0;
+  const int* perm = nullptr;
+  if (work) {  // the dispatch order, heaviest worlds first
+    const int rc = launch_order_fwd(st, nw, qpos, work);
+    if (rc) return rc;
+    perm = (const int*)work;
+  }
   hipLaunchKernelGGL(k_forward, dim3(nw), dim3(64), 0, st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub,
-                     oq, ov, ow, info, ocon, tape);
+                     oq, ov, ow, info, ocon, tape, perm);
   return (int)hipGetLastError();
 }
 size_t forward_lds_bytes() { return sizeof(Sim); }

@@ -1,0 +1,142 @@
+// World ordering for the forward and adjoint launches: heaviest worlds first.
+//
+// A launch of B worlds runs them one wave64 each, and the hardware dispatches workgroups in blockIdx order as slots
+// free up. The kernel time is the makespan: a heavy world (many contacts, contacts between two robot bodies) that
+// starts late finishes late. Dispatching worlds in decreasing cost is the longest-processing-time-first schedule.
+// The reference does the same for its split kernels (host.py:236-264 dk_order_world, row-count buckets).
+//
+// The cost is estimated per world before the launch, in the caller's work buffer:
+//   forward  contacts expected at the input state: broadphase candidates of the 502 pairs (the narrowphase's first
+//            test), candidates between two robot bodies weighted more (each makes the Hessian dense);
+//   adjoint  constraint rows summed over the tape's substep headers.
+// Then one workgroup buckets the costs (LDS histogram, descending prefix) into the permutation the main kernel reads
+// as blockIdx.x -> world. Results do not depend on the order: every world's computation is the same wherever and
+// whenever it runs, so the permutation only moves work in time (its order inside a bucket is free).
+#include "g1_device.h"
+#include "g1_collide.h"
+#include "g1_tape.h"
+
+namespace g1k {
+
+constexpr int NBKT = 128;  // cost buckets
+
+// broadphase candidates at the input state: FK of body poses (each body lane walks its chain from the root), geom
+// poses, then the main kernel's bounding test over the pairs
+__global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict__ qpos, int* __restrict__ cost) {
+  __shared__ float q[40];
+  __shared__ float bq[NB][4], bx[NB][4];
+  __shared__ float gx[NGEOM][4], gq[NGEOM][4];
+  const int lane = threadIdx.x, w = blockIdx.x;
+  if (w >= nw) return;
+  if (lane < NQ) q[lane] = qpos[(size_t)w * NQ + lane];
+  wsync();
+  if (lane < NB) {
+    float Q[4], X[3];
+    {
+      const float n = rsqrtf(q[3] * q[3] + q[4] * q[4] + q[5] * q[5] + q[6] * q[6]);
+      for (int k = 0; k < 4; k++) Q[k] = q[3 + k] * n;
+      for (int k = 0; k < 3; k++) X[k] = q[k];
+    }
+    const int depth = cDepth[lane];
+    for (int l = 1; l < depth; l++) {
+      const int k = cTree.path[lane][l];
+      const float qb[4] = {cQuat[4 * k], cQuat[4 * k + 1], cQuat[4 * k + 2], cQuat[4 * k + 3]};
+      const float pb[3] = {cPos[3 * k], cPos[3 * k + 1], cPos[3 * k + 2]};
+      float t[3], q0[4], sn, cs;
+      qrot(Q, pb, t);
+      for (int c = 0; c < 3; c++) X[c] += t[c];
+      qmul(Q, qb, q0);
+      sincosf(0.5f * q[cQadr[k]], &sn, &cs);
+      const float ha[4] = {cs, sn * cAxis[3 * k], sn * cAxis[3 * k + 1], sn * cAxis[3 * k + 2]};
+      qmul(q0, ha, Q);
+    }
+    for (int k = 0; k < 4; k++) bq[lane][k] = lane == 0 ? (k == 0 ? 1.f : 0.f) : Q[k];
+    for (int k = 0; k < 3; k++) bx[lane][k] = lane == 0 ? 0.f : X[k];
+  }
+  wsync();
+  if (lane < NGEOM) {
+    const int b = cGbody[lane];
+    float t[3];
+    const float qb[4] = {bq[b][0], bq[b][1], bq[b][2], bq[b][3]};
+    const float gp[3] = {cGpos[3 * lane], cGpos[3 * lane + 1], cGpos[3 * lane + 2]};
+    const float gqq[4] = {cGquat[4 * lane], cGquat[4 * lane + 1], cGquat[4 * lane + 2], cGquat[4 * lane + 3]};
+    qrot(qb, gp, t);
+    for (int k = 0; k < 3; k++) gx[lane][k] = bx[b][k] + t[k];
+    qmul(qb, gqq, gq[lane]);
+  }
+  wsync();
+  float fn[3];
+  {
+    const float q0[4] = {gq[0][0], gq[0][1], gq[0][2], gq[0][3]};
+    zaxis(q0, fn);
+  }
+  int c = 0;
+  for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {
+    const int pr = lane + WL * k;
+    if (pr < NPAIR) {
+      const unsigned pw = cPairW[pr];
+      const int g1 = pw & 255u, g2 = (pw >> 8) & 255u;
+      const float dif[3] = {gx[g2][0] - gx[g1][0], gx[g2][1] - gx[g1][1], gx[g2][2] - gx[g1][2]};
+      const unsigned cls = (pw >> 21) & 7u;
+      if (cls == 0u || cls == 4u) c += dot3(dif, fn) <= cGrb[g2] * (1.f + 1e-5f) + 1e-6f ? 1 : 0;
+      else {
+        const float rb = cGrb[g1] + cGrb[g2];
+        c += dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f ? 4 : 0;
+      }
+    }
+  }
+  const int tot = wsumi(c);
+  if (lane == 0) cost[w] = tot < NBKT ? tot : NBKT - 1;
+}
+
+// the adjoint's cost from the tape: the constraint rows of every substep (the header word, ncon | nefc << 8 |
+// nlim << 16 | iterations << 24), in units of 8 (the adjoint's work per substep grows with its rows and contacts)
+__global__ __launch_bounds__(256) void k_cost_adj(int nw, int nsub, const float* __restrict__ tape,
+                                                   int* __restrict__ cost) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= nw) return;
+  int c = 0;
+  for (int k = 0; k < nsub; k++) {
+    const unsigned h = __float_as_uint(tape[((size_t)w * nsub + k) * REC_WORDS + REC_HDR]);
+    c += (int)((h >> 8) & 255u);
+  }
+  c >>= 3;
+  cost[w] = c < NBKT ? c : NBKT - 1;
+}
+
+// one workgroup: histogram of the costs, descending prefix, scatter (perm[slot] = world, heaviest first)
+__global__ __launch_bounds__(1024) void k_order(int nw, const int* __restrict__ cost, int* __restrict__ perm) {
+  __shared__ int cnt[NBKT], cur[NBKT];
+  const int t = threadIdx.x;
+  for (int b = t; b < NBKT; b += blockDim.x) cnt[b] = 0;
+  __syncthreads();
+  for (int w = t; w < nw; w += blockDim.x) atomicAdd(&cnt[cost[w]], 1);
+  __syncthreads();
+  if (t == 0) {
+    int acc = 0;
+    for (int b = NBKT - 1; b >= 0; b--) { cur[b] = acc; acc += cnt[b]; }
+  }
+  __syncthreads();
+  for (int w = t; w < nw; w += blockDim.x) perm[atomicAdd(&cur[cost[w]], 1)] = w;
+}
+
+// work buffer: perm (nw int32), cost (nw int32)
+size_t order_work_bytes(int nw) { return nw > 0 ? ((8 * (size_t)nw + 255) & ~(size_t)255) : 0; }
+
+int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work) {
+  int* perm = (int*)work;
+  int* cost = perm + nw;
+  hipLaunchKernelGGL(k_cost_fwd, dim3(nw), dim3(64), 0, st, nw, qpos, cost);
+  hipLaunchKernelGGL(k_order, dim3(1), dim3(1024), 0, st, nw, cost, perm);
+  return (int)hipGetLastError();
+}
+
+int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work) {
+  int* perm = (int*)work;
+  int* cost = perm + nw;
+  hipLaunchKernelGGL(k_cost_adj, dim3((nw + 255) / 256), dim3(256), 0, st, nw, nsub, tape, cost);
+  hipLaunchKernelGGL(k_order, dim3(1), dim3(1024), 0, st, nw, cost, perm);
+  return (int)hipGetLastError();
+}
+
+}  // namespace g1k

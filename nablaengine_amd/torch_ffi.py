@@ -61,6 +61,9 @@ def load_library(path=None):
         lib.dk_fwd_sizes.argtypes, lib.dk_fwd_sizes.restype = [vp], None
         lib.dk_adjoint.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32]
         lib.dk_adjoint.restype = i32
+        lib.dk_adjoint_work.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp]
+        lib.dk_adjoint_work.restype = i32
+        lib.dk_adjoint_work_bytes.argtypes, lib.dk_adjoint_work_bytes.restype = [i32], ctypes.c_longlong
         sizes = (ctypes.c_longlong * 9)()
         lib.dk_fwd_sizes(ctypes.cast(sizes, vp))
         _STATE["sizes"] = [int(x) for x in sizes]
@@ -169,11 +172,13 @@ def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, t
     tp = torch.empty((B if tape else 0, substeps * rw), **kw)
     if B == 0:
         return [q1, v1, w1, info, tp]
+    work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device=qpos.device)
     with _OnDevice(dev):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         _rc(lib.dk_fwd_forward(st, B, *map(_ptr, (qpos, qvel, warm, ctrl, friction, com)), int(iterations),
                                int(substeps), _ptr(q1), _ptr(v1), _ptr(w1), _ptr(info), None,
-                               _ptr(tp) if tape else None, None), "the forward launch")
+                               _ptr(tp) if tape else None, _ptr(work) if work.numel() else None),
+            "the forward launch")
     return [q1, v1, w1, info, tp]
 
 
@@ -201,11 +206,14 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
     info = torch.empty((B,), dtype=torch.int32, device=tape.device)
     if B == 0:
         return [gq, gv, gu, info]
+    lib = _STATE["lib"]
+    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
     with _OnDevice(dev):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        _rc(_STATE["lib"].dk_adjoint(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos),
-                                     _ptr(g_qvel), _ptr(gq), _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl),
-                                     ctypes.c_float(0.0 if clamp_soft is None else clamp_soft), v[0], v[1]),
+        _rc(lib.dk_adjoint_work(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos),
+                                _ptr(g_qvel), _ptr(gq), _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl),
+                                ctypes.c_float(0.0 if clamp_soft is None else clamp_soft), v[0], v[1],
+                                _ptr(work) if work.numel() else None),
             "the adjoint launch")
     return [gq, gv, gu, info]
 

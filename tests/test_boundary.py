@@ -39,7 +39,10 @@ def test_library_exports_every_declared_entry():
     assert list(sizes)[2:6] == [1472, 36, 35, 64]
     lib.dk_kv2_n1_sizes(sizes)
     assert sizes[6] == 2 and sizes[7] == 1
-    assert lib.dk_fwd_work_bytes(4096) == 0
+    lib.dk_fwd_work_bytes.restype = lib.dk_adjoint_work_bytes.restype = ctypes.c_longlong
+    assert lib.dk_fwd_work_bytes(0) == 0 and lib.dk_adjoint_work_bytes(0) == 0
+    # the dispatch order: a permutation and a cost per world (int32)
+    assert lib.dk_fwd_work_bytes(4096) >= 8 * 4096 and lib.dk_adjoint_work_bytes(4096) >= 8 * 4096
 
 
 def test_model_header_matches_json():

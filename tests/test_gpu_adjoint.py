@@ -149,3 +149,39 @@ def test_adjoint_variants_run(ffi):
             assert all(torch.isfinite(x).all() for x in out[:3])
     with pytest.raises(ValueError):
         ffi.backward(r[4], args[4], args[5], _t(cq), _t(cv), clamp_kv=2)
+
+
+def test_dispatch_order_does_not_change_results(ffi):
+    """The C entries with a work buffer dispatch the worlds heaviest first; without one (NULL) in index order. The
+    outputs, the tape and the gradients are bitwise the same both ways (contact-heavy config-4 states, where the
+    order moves the most)."""
+    import ctypes
+    import torch
+    lib = ffi.load_library()
+    B = 1536
+    st = synthetic.states(B, config=4)
+    cq, cv = synthetic.cotangents(B)
+    args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for ordered in (False, True):
+        kw = dict(dtype=torch.float32, device="cuda")
+        q1, v1, w1 = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 35), **kw)
+        info = torch.empty((B, 4), dtype=torch.int32, device="cuda")
+        tape = torch.empty((B, 4 * ffi.rec_words()), **kw)
+        work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+        assert lib.dk_fwd_forward(stream, B, *map(p, args), 10, 4, p(q1), p(v1), p(w1), p(info), None, p(tape),
+                                  p(work) if ordered else None) == 0
+        gq, gv, gu = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 29), **kw)
+        binfo = torch.empty((B,), dtype=torch.int32, device="cuda")
+        work2 = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+        assert lib.dk_adjoint_work(stream, B, 4, p(tape), p(args[4]), p(args[5]), p(_t(cq)), p(_t(cv)), p(gq), p(gv),
+                                   p(gu), p(binfo), None, ctypes.c_float(0.0), 0, 3,
+                                   p(work2) if ordered else None) == 0
+        torch.cuda.synchronize()
+        outs.append((q1, v1, w1, info, tape.view(torch.int32), gq, gv, gu, binfo))
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)
+    perm = work.view(torch.int32)[:B].cpu().numpy()
+    assert np.array_equal(np.sort(perm), np.arange(B))  # a permutation of the worlds
