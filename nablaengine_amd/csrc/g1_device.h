@@ -55,6 +55,14 @@ constexpr float kTol = (float)TOLERANCE;
 
 // ------------------------------------------------------------------------------------------------ lane helpers
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+// The lane index as a value the compiler cannot see through: lane-dependent addresses and masks computed from it stay
+// where they are used. Without this, loop-invariant code motion hoists them out of the solver's loops (dozens of
+// per-lane addresses and lane masks), and the register allocator spills them to scratch, putting a scratch reload on
+// every step of the factor / solve chains.
+__device__ __forceinline__ int opaque_lane(int lane) {
+  asm volatile("" : "+v"(lane));
+  return lane;
+}
 __device__ __forceinline__ float rdl(float x, int k) {  // lane k's x, k uniform
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
 }
@@ -86,6 +94,25 @@ __device__ __forceinline__ float2 wsum2(float a, float b) {
   a += G1_DPP(a, 0x143, 0xc); b += G1_DPP(b, 0x143, 0xc);
   return make_float2(rdl(a, 63), rdl(b, 63));
 }
+// the wave totals of n values at once (a masked sum passes 0 on the lanes outside the set): wsum's DPP steps with
+// the n chains interleaved, so every step's n instructions are independent of each other
+template <int N>
+__device__ __forceinline__ void wsum_n(float* x) {
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x111, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x112, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x114, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x118, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x142, 0xa);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x143, 0xc);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] = rdl(x[e], 63);
+}
 __device__ __forceinline__ int wsumi(int v) {  // small counts: exact in float
   return (int)wsum((float)v);
 }
@@ -105,7 +132,7 @@ __device__ __forceinline__ void wsync() { __syncthreads(); }
 // (lane 0's clock at phase ends, after a barrier), written to g_prof[world][phase] for the first PROF_WORLDS worlds
 // and read by dk_prof_read. The production build compiles every mark to nothing.
 enum { PH_SMOOTH = 0, PH_COLLIDE, PH_ROWS, PH_NINIT, PH_HESS, PH_FACTOR, PH_SOLVE, PH_LSEARCH, PH_UPDATE, PH_GRAD,
-       PH_IMPLICIT, PH_TAPE, PH_ITERS, PH_LSEVAL, PH_DENSE, NPHASE };
+       PH_IMPLICIT, PH_TAPE, PH_ITERS, PH_LSEVAL, PH_DENSE, PH_LSJV, PH_LSMV, PH_HK, PH_HCOMP, PH_HROWS, PH_T0, PH_T1, PH_HWID, NPHASE };
 constexpr int PROF_WORLDS = 16384;
 #ifdef G1_PROFILE
 __device__ inline unsigned long long g_prof[PROF_WORLDS][NPHASE];
@@ -156,7 +183,8 @@ __device__ __forceinline__ float rsqrt_nr(float d) {
 // SPARSE = false visits every m < k (the dense factor of a matrix with cross-branch entries). In place in Lp (packed
 // lower, TRI layout).
 template <bool SPARSE>
-__device__ __forceinline__ void ltl_factor(float* Lp, int lane) {
+__device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
+  const int lane = opaque_lane(lane_);
   float c[NV];
 #pragma unroll
   for (int m = 0; m < NV; m++) c[m] = (m >= lane && lane < NV) ? Lp[tri(m, lane)] : 0.f;
@@ -185,7 +213,8 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane) {
 // solved entry, and the entries it is multiplied with are pre-scaled the same way and zeroed on lanes that take no
 // update: a step is one v_readlane and one FMA on the dependency chain. The factor entries are loaded from clamped
 // (always valid) addresses without a lane condition, so the loads are issued ahead of the chain.
-__device__ __forceinline__ float ltl_solve(const float* Lp, float b, int lane) {
+__device__ __forceinline__ float ltl_solve(const float* Lp, float b, int lane_) {
+  const int lane = opaque_lane(lane_);
   const int r = lane < NV ? lane : NV - 1;
   const float dself = lane < NV ? 1.f / Lp[tri(r, r)] : 0.f;
   float z = b * dself;  // (b - sum of the solved descendants' terms) / L[lane][lane]

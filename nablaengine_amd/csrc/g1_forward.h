@@ -11,6 +11,8 @@ struct __align__(16) Sim {
   float L[NTRI + 2];
   float S[NV][8];             // dof motion subspaces about O: angular (0..2), velocity of O (4..6)
   float Q[NB][4], X[NB][4];   // body poses
+  unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
+  unsigned dsub[WL];                 // bodies moved by dof i (bit b), 0 past the dofs
   float O[4];
   float fric;
   int ncon, ncon_raw, nlim, nefc, flags, niter;
@@ -26,11 +28,16 @@ struct __align__(16) Sim {
       float bw[NB][8];  // body spatial velocity of a dof vector: angular (0..2), velocity of O (4..6)
       union {
         float ft[MAXCON][8];  // contact spatial force about O: torque (0..2), force (4..6); bodies b1 (3), b2 (7)
-        struct { float kc[MAXCON][24]; float kb[NB][24]; float y[NV][8]; } h;  // Hessian scratch
+        struct { float psi[16][8]; float U[NV][16]; } h;  // Hessian: a batch of self-contact rows (<= 16)
       };
     } nt;
   } u;
 };
+
+// 8 worlds per CU: the LDS of one world must stay within 160 KB / 8 (the profile build's counters excepted)
+#ifndef G1_PROFILE
+static_assert(sizeof(Sim) <= 20480, "Sim outgrew the LDS of 8 worlds per CU");
+#endif
 
 // per-lane register state of the constraint rows: lane l holds contact l's rows and dof l's limit row
 struct Rows {

@@ -339,17 +339,26 @@ __constant__ inline Arr<float, 2> cPSolref = to_float(PAIR_SOLREF);
 __constant__ inline Arr<float, 5> cPSolimp = to_float(PAIR_SOLIMP);
 static_assert(JNT_SOLIMP[4] == 2.0 && PAIR_SOLIMP[4] == 2.0, "kbimp assumes the solimp power 2");
 
-// body spatial velocities of the dof vector v (LDS, NV): bw[b] = sum over b's chain of S_d v_d
+// dof t of a chain row of s.chain (4 words of byte indices): the index, clamped to a valid dof past the chain's end
+__device__ __forceinline__ int chain_dof(const unsigned* ch, int t, bool* on) {
+  const unsigned d = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
+  *on = d != 255u;
+  return d != 255u ? (int)d : 0;
+}
+
+// body spatial velocities of the dof vector v (LDS, NV): bw[b] = sum over b's chain of S_d v_d. The chain comes from
+// the LDS table in one load; every step's loads are independent of the others, so they are all in flight at once.
 __device__ __forceinline__ void body_vel(Sim& s, const float* v, int lane) {
   if (lane < NB) {
+    unsigned ch[4];
+    for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
     float w[3] = {0.f, 0.f, 0.f}, u[3] = {0.f, 0.f, 0.f};
-    const int n = cTree.nchain[lane];
+#pragma unroll
     for (int t = 0; t < MAXCHAIN; t++) {
-      if (t < n) {
-        const int d = cTree.chain[lane][t];
-        const float vd = v[d];
-        for (int k = 0; k < 3; k++) { w[k] += s.S[d][k] * vd; u[k] += s.S[d][4 + k] * vd; }
-      }
+      bool on;
+      const int d = chain_dof(ch, t, &on);
+      const float vd = on ? v[d] : 0.f;
+      for (int k = 0; k < 3; k++) { w[k] = fmaf(s.S[d][k], vd, w[k]); u[k] = fmaf(s.S[d][4 + k], vd, u[k]); }
     }
     for (int k = 0; k < 3; k++) { s.u.nt.bw[lane][k] = w[k]; s.u.nt.bw[lane][4 + k] = u[k]; }
   }
@@ -385,16 +394,24 @@ __device__ __forceinline__ void rows_jv(Sim& s, const Rows& R, const float* v, i
   wsync();
 }
 
-// out = M v (M packed in LDS, v in LDS), lane i < NV
-__device__ __forceinline__ float matvec(const Sim& s, const float* v, int lane) {
-  if (lane >= NV) return 0.f;
-  float acc = 0.f, acc2 = 0.f;
-#pragma unroll 5
-  for (int j = 0; j < NV; j++) {
-    const float m = s.M[j <= lane ? tri(lane, j) : tri(j, lane)];
-    if (j & 1) acc2 = fmaf(m, v[j], acc2); else acc = fmaf(m, v[j], acc);
+// out = M v (M packed in LDS, v in LDS), lane i < NV: row i left of the diagonal (M[tri(i, j)], j <= i) and
+// column i below it (M[tri(j, i)], j > i), both read at every j from in-bounds addresses and selected, so all the
+// loads are independent and in flight together
+__device__ __forceinline__ float matvec(const Sim& s, const float* v, int lane_) {
+  const int lane = opaque_lane(lane_);
+  const int i = lane < NV ? lane : NV - 1;
+  const int base = tri(i, 0);
+  float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int j0 = 0; j0 < NV; j0 += 5) {  // 5 columns a step (10 loads in flight)
+#pragma unroll
+    for (int e = 0; e < 5; e++) {
+      const int j = j0 + e;
+      const float a = s.M[base + j], b = s.M[tri(j, 0) + i];
+      acc[e] = fmaf(j <= i ? a : b, v[j], acc[e]);
+    }
   }
-  return acc + acc2;
+  return lane < NV ? ((acc[0] + acc[1]) + (acc[2] + acc[3])) + acc[4] : 0.f;
 }
 
 // ============================================================================================== Newton
@@ -419,15 +436,19 @@ __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
   wsync();
   float g = 0.f;
   if (lane < NV) {
-    const unsigned mask = cTree.dofmask32[lane];
+    const unsigned mask = s.dsub[lane];
     const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]}, v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
     float tau = 0.f;
     const int ncon = s.ncon;
-    for (int c = 0; c < ncon; c++) {
-      const float* o = s.u.nt.ft[c];
-      const int b1 = __float_as_int(o[3]), b2 = __float_as_int(o[7]);
-      const float sg = (float)((int)((mask >> b2) & 1u) - (int)((mask >> b1) & 1u));
-      tau += sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[4] + v[1] * o[5] + v[2] * o[6]);
+    for (int c0 = 0; c0 < ncon; c0 += 4) {  // 4 contacts a step: their loads in flight together
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int c = c0 + e < ncon ? c0 + e : c0;
+        const float* o = s.u.nt.ft[c];
+        const int b1 = __float_as_int(o[3]), b2 = __float_as_int(o[7]);
+        const float sg = c0 + e < ncon ? (float)((int)((mask >> b2) & 1u) - (int)((mask >> b1) & 1u)) : 0.f;
+        tau += sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[4] + v[1] * o[5] + v[2] * o[6]);
+      }
     }
     if (R.lsg != 0.f && R.ljar < 0.f) tau += R.lsg * (-R.lD * R.ljar);
     g = s.Ma[lane] - s.qsm[lane] - tau;
@@ -458,119 +479,164 @@ __device__ void refresh(Sim& s, Rows& R, int lane, bool con) {
   R.ljar = ljv - R.laref;
 }
 
+constexpr int SELF_BATCH = 4;  // contacts between two robot bodies per outer-product batch
+
+// a floor contact's 6x6 stiffness K = Phi' C Phi about O (21 floats: Kaa 6, Kal 9, Kf 6), C from the curvatures d of
+// its pyramid rows in the frame basis; zero where !on
+__device__ __forceinline__ void contact_stiffness(const Rows& R, const float* dd, bool on, float* K) {
+  float d[4];
+  for (int t = 0; t < 4; t++) d[t] = on ? dd[t] : 0.f;
+  float Cnn, Cn1 = 0.f, C11 = 0.f, Cn2 = 0.f, C22 = 0.f;
+  if (R.dim == 3) {
+    Cnn = d[0] + d[1] + d[2] + d[3];
+    Cn1 = R.mu * (d[0] - d[1]); C11 = R.mu * R.mu * (d[0] + d[1]);
+    Cn2 = R.mu * (d[2] - d[3]); C22 = R.mu * R.mu * (d[2] + d[3]);
+  } else Cnn = d[0];
+  const float *n = R.fr, *t1 = R.fr + 3, *t2 = R.fr + 6;
+  float Kf[3][3];
+  for (int a = 0; a < 3; a++)
+    for (int b = 0; b < 3; b++)
+      Kf[a][b] = Cnn * n[a] * n[b] + Cn1 * (n[a] * t1[b] + t1[a] * n[b]) + C11 * t1[a] * t1[b]
+                 + Cn2 * (n[a] * t2[b] + t2[a] * n[b]) + C22 * t2[a] * t2[b];
+  float Kal[3][3], Kaa[3][3];
+  for (int b = 0; b < 3; b++) {  // column b of r^ Kf = r x Kf[:, b]
+    float col[3] = {Kf[0][b], Kf[1][b], Kf[2][b]}, o[3];
+    cross(R.r, col, o);
+    for (int a = 0; a < 3; a++) Kal[a][b] = o[a];
+  }
+  for (int a = 0; a < 3; a++) {  // row a of r^ Kf r^' = r x (row a of Kal)
+    float row[3] = {Kal[a][0], Kal[a][1], Kal[a][2]}, o[3];
+    cross(R.r, row, o);
+    for (int b = 0; b < 3; b++) Kaa[a][b] = o[b];
+  }
+  K[0] = Kaa[0][0]; K[1] = Kaa[1][1]; K[2] = Kaa[2][2]; K[3] = Kaa[0][1]; K[4] = Kaa[0][2]; K[5] = Kaa[1][2];
+  for (int a = 0; a < 3; a++) for (int b = 0; b < 3; b++) K[6 + 3 * a + b] = Kal[a][b];
+  K[15] = Kf[0][0]; K[16] = Kf[1][1]; K[17] = Kf[2][2]; K[18] = Kf[0][1]; K[19] = Kf[0][2]; K[20] = Kf[1][2];
+}
+
 // H = M + J' D J on the rows with x < 0, packed into s.L (lane i writes row i); returns whether a contact between two
-// robot bodies put entries outside the tree's sparsity
+// robot bodies put entries outside the tree's sparsity.
+//   Floor contacts: J'CJ of a contact on body B is S_i' K S_j on every pair of dofs moving B, with K = Phi' C Phi its
+//   6x6 stiffness about O. The contacts are summed per body by wave reductions (one pass per distinct body, usually
+//   the two feet); dof i accumulates (n, f) = (sum of K over the bodies it moves) S_i, and H[i][j] = S_j . (n, f) on
+//   i's ancestor dofs j (the composite stiffness of i's subtree, as CRBA composites inertia).
+//   Contacts between two robot bodies: J'CJ = sum over the active pyramid edges t of u_t u_t', u_t = sqrt(D) J' e_t,
+//   u_t[d] = sigma_d S_d . (r x e_t, e_t) with sigma_d = (dof d moves body 2) - (dof d moves body 1); added as outer
+//   products, SELF_BATCH contacts (4 edges each) a batch.
 __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool con) {
-  const int ncon = s.ncon;
-  // the contact's 6x6 stiffness K = Phi' C Phi about O, C from the pyramid rows' curvatures in the frame basis
-  bool act = false;
-  if (con) {
-    float d[4];
+  float d[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) d[t] = (t < R.nr && R.jar[t] < 0.f) ? R.D : 0.f;
-    float Cnn, Cn1 = 0.f, C11 = 0.f, Cn2 = 0.f, C22 = 0.f;
-    if (R.dim == 3) {
-      Cnn = d[0] + d[1] + d[2] + d[3];
-      Cn1 = R.mu * (d[0] - d[1]); C11 = R.mu * R.mu * (d[0] + d[1]);
-      Cn2 = R.mu * (d[2] - d[3]); C22 = R.mu * R.mu * (d[2] + d[3]);
-    } else Cnn = d[0];
-    act = Cnn != 0.f;
-    const float *n = R.fr, *t1 = R.fr + 3, *t2 = R.fr + 6;
-    float Kf[3][3];
-    for (int a = 0; a < 3; a++)
-      for (int b = 0; b < 3; b++)
-        Kf[a][b] = Cnn * n[a] * n[b] + Cn1 * (n[a] * t1[b] + t1[a] * n[b]) + C11 * t1[a] * t1[b]
-                   + Cn2 * (n[a] * t2[b] + t2[a] * n[b]) + C22 * t2[a] * t2[b];
-    float Kal[3][3], Kaa[3][3];
-    for (int b = 0; b < 3; b++) {  // column b of r^ Kf = r x Kf[:, b]
-      float col[3] = {Kf[0][b], Kf[1][b], Kf[2][b]}, o[3];
-      cross(R.r, col, o);
-      for (int a = 0; a < 3; a++) Kal[a][b] = o[a];
-    }
-    for (int a = 0; a < 3; a++) {  // row a of r^ Kf r^' = r x (row a of Kal)
-      float row[3] = {Kal[a][0], Kal[a][1], Kal[a][2]}, o[3];
-      cross(R.r, row, o);
-      for (int b = 0; b < 3; b++) Kaa[a][b] = o[b];
-    }
-    float* k = s.u.nt.h.kc[lane];
-    k[0] = Kaa[0][0]; k[1] = Kaa[1][1]; k[2] = Kaa[2][2]; k[3] = Kaa[0][1]; k[4] = Kaa[0][2]; k[5] = Kaa[1][2];
-    for (int a = 0; a < 3; a++) for (int b = 0; b < 3; b++) k[6 + 3 * a + b] = Kal[a][b];
-    k[15] = Kf[0][0]; k[16] = Kf[1][1]; k[17] = Kf[2][2]; k[18] = Kf[0][1]; k[19] = Kf[0][2]; k[20] = Kf[1][2];
-    k[21] = __int_as_float(R.b1); k[22] = __int_as_float(R.b2);
-  }
-  const unsigned long long actm = ballot(act);
+  for (int t = 0; t < 4; t++) d[t] = (con && t < R.nr && R.jar[t] < 0.f) ? R.D : 0.f;
+  const bool act = (d[0] + d[1]) + (d[2] + d[3]) != 0.f;
+  const bool floorc = act && R.b1 == 0;
   const unsigned long long selfm = ballot(act && R.b1 != 0);
-  wsync();
-  // composite stiffness of each body's subtree: sum of the contacts whose bodies lie in it (once per body in it)
-  if (lane >= 1 && lane < NB) {
-    float kb[21];
-    for (int e = 0; e < 21; e++) kb[e] = 0.f;
-    const unsigned sub = cTree.submask[lane];
-    for (unsigned long long m = actm; m; m &= m - 1ull) {
-      const int c = __builtin_ctzll(m);
-      const float* k = s.u.nt.h.kc[c];
-      const int b1 = __float_as_int(k[21]), b2 = __float_as_int(k[22]);
-      const float mult = (float)((int)((sub >> b1) & 1u) + (int)((sub >> b2) & 1u));
-      for (int e = 0; e < 21; e++) kb[e] += mult * k[e];
+  PROF(PH_HK);
+  const unsigned dm = s.dsub[lane];
+  const int il = lane < NV ? lane : 0;
+  const float w[3] = {s.S[il][0], s.S[il][1], s.S[il][2]}, v[3] = {s.S[il][4], s.S[il][5], s.S[il][6]};
+  float n[3] = {0.f, 0.f, 0.f}, f[3] = {0.f, 0.f, 0.f};
+  for (unsigned long long rem = ballot(floorc); rem;) {  // one distinct contact body B a pass
+    const int B = rdli(R.b2, __builtin_ctzll(rem));
+    const bool in = floorc && R.b2 == B;
+    rem &= ~ballot(in);
+    float k[21];
+    contact_stiffness(R, d, in, k);
+    wsum_n<21>(k);
+    if ((dm >> B) & 1u) {  // n += Kaa w + Kal v, f += Kal' w + Kll v
+      n[0] += k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
+      n[1] += k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
+      n[2] += k[4] * w[0] + k[5] * w[1] + k[2] * w[2] + k[12] * v[0] + k[13] * v[1] + k[14] * v[2];
+      f[0] += k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
+      f[1] += k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
+      f[2] += k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
     }
-    for (int e = 0; e < 21; e++) s.u.nt.h.kb[lane][e] = kb[e];
   }
-  wsync();
-  // rows of H: M, then S_j . (Kc_body(i) S_i) on the ancestor dofs j of i
+  PROF(PH_HCOMP);
+  // rows of H: M, then S_j . (n, f) on the ancestor dofs j of i
   for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
   if (lane < NV) {
     const int bi = lane < 6 ? 1 : lane - 4;
-    const float* k = s.u.nt.h.kb[bi];
-    const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]}, v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
-    float n[3], f[3];
-    // n = Kaa w + Kal v, f = Kal' w + Kll v
-    n[0] = k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
-    n[1] = k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
-    n[2] = k[4] * w[0] + k[5] * w[1] + k[2] * w[2] + k[12] * v[0] + k[13] * v[1] + k[14] * v[2];
-    f[0] = k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
-    f[1] = k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
-    f[2] = k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
-    const int nch = cTree.nchain[bi];
-#pragma unroll 2
-    for (int t = 0; t < nch; t++) {  // the chain of dof i's body: its ancestor dofs (and the root's j <= i)
-      const int j = cTree.chain[bi][t];
-      if (j <= lane)
-        s.L[tri(lane, j)] += s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0]
-                             + s.S[j][5] * f[1] + s.S[j][6] * f[2];
+    // the chain of dof i's body: its ancestor dofs (and the root's j <= i). Every load first (S rows, M entries:
+    // independent of the stores into L), then the stores of the chain's entries
+    unsigned ch[4];
+    for (int k = 0; k < 4; k++) ch[k] = s.chain[bi][k];
+#pragma unroll
+    for (int t0 = 0; t0 < MAXCHAIN; t0 += 8) {  // 8 entries a batch
+      float hv[8];
+      int ha[8];
+      bool hon[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int j = chain_dof(ch, t0 + e, &hon[e]);
+        hon[e] = hon[e] && j <= lane;
+        ha[e] = tri(lane, j <= lane ? j : lane);
+        hv[e] = s.M[ha[e]] + (s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0]
+                              + s.S[j][5] * f[1] + s.S[j][6] * f[2]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        if (hon[e]) s.L[ha[e]] = hv[e];
     }
     if (R.lsg != 0.f && R.ljar < 0.f) s.L[tri(lane, lane)] += R.lD;
   }
-  // contacts between two robot bodies: the cross-chain terms -(p2_i p1_j + p1_i p2_j) S_i' K S_j
-  for (unsigned long long m = selfm; m; m &= m - 1ull) {
-    const int c = __builtin_ctzll(m);
-    const float* k = s.u.nt.h.kc[c];
-    const int b1 = __float_as_int(k[21]), b2 = __float_as_int(k[22]);
-    if (lane < NV) {
-      const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]},
-                  v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
-      float* y = s.u.nt.h.y[lane];
-      y[0] = k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
-      y[1] = k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
-      y[2] = k[4] * w[0] + k[5] * w[1] + k[2] * w[2] + k[12] * v[0] + k[13] * v[1] + k[14] * v[2];
-      y[4] = k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
-      y[5] = k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
-      y[6] = k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
-      const unsigned dm = cTree.dofmask32[lane];
-      y[3] = (float)((dm >> b1) & 1u);
-      y[7] = (float)((dm >> b2) & 1u);
+  PROF(PH_HROWS);
+  for (unsigned long long m = selfm; m;) {  // contacts between two robot bodies, SELF_BATCH a batch
+    unsigned long long bm = 0ull;
+    for (int q = 0; q < SELF_BATCH && m; q++) { bm |= m & (~m + 1ull); m &= m - 1ull; }
+    if (lane < 4 * SELF_BATCH)
+      for (int k = 0; k < 8; k++) s.u.nt.h.psi[lane][k] = 0.f;
+    if ((bm >> lane) & 1ull) {  // this contact's 4 edge rows: sqrt(D) (r x e_t, e_t), e_t = n +- mu t1, n +- mu t2
+      const int q = prefix_count(bm, lane);
+      const float sd = sqrtf(R.D);
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        float e[3];
+        const float sg = (t & 1) ? -R.mu : R.mu;
+        const float* ta = R.fr + 3 * (1 + (t >> 1));
+        for (int k = 0; k < 3; k++) e[k] = R.dim == 3 ? R.fr[k] + sg * ta[k] : (t == 0 ? R.fr[k] : 0.f);
+        const float sc = d[t] != 0.f ? sd : 0.f;
+        float re[3];
+        cross(R.r, e, re);
+        float* o = s.u.nt.h.psi[4 * q + t];
+        for (int k = 0; k < 3; k++) { o[k] = sc * re[k]; o[3 + k] = sc * e[k]; }
+        o[6] = __int_as_float(R.b1);
+        o[7] = __int_as_float(R.b2);
+      }
     }
     wsync();
-    if (lane < NV) {
-      const unsigned dm = cTree.dofmask32[lane];
-      const float p1 = (float)((dm >> b1) & 1u), p2 = (float)((dm >> b2) & 1u);
-      const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]},
-                  v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
-#pragma unroll 2
-      for (int j = 0; j <= lane; j++) {
-        const float* y = s.u.nt.h.y[j];
-        const float coef = p2 * y[3] + p1 * y[7];
-        s.L[tri(lane, j)] -= coef * (w[0] * y[0] + w[1] * y[1] + w[2] * y[2] + v[0] * y[4] + v[1] * y[5]
-                                     + v[2] * y[6]);
+    if (lane < NV) {  // U[i][r] = sigma_r(i) S_i . psi_r
+#pragma unroll
+      for (int r = 0; r < 4 * SELF_BATCH; r++) {
+        const float* o = s.u.nt.h.psi[r];
+        const int b1 = __float_as_int(o[6]), b2 = __float_as_int(o[7]);
+        const float sg = (float)((int)((dm >> b2) & 1u) - (int)((dm >> b1) & 1u));
+        s.u.nt.h.U[lane][r] = sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[3] + v[1] * o[4] + v[2] * o[5]);
+      }
+    }
+    wsync();
+    if (lane < NV) {  // H[i][j] += sum_r U[i][r] U[j][r] for j <= i, 5 columns a step: their loads together
+      float ui[4 * SELF_BATCH];
+      for (int r = 0; r < 4 * SELF_BATCH; r++) ui[r] = s.u.nt.h.U[lane][r];
+#pragma unroll
+      for (int j0 = 0; j0 < NV; j0 += 5) {
+        float hv[5];
+        int ha[5];
+#pragma unroll
+        for (int e = 0; e < 5; e++) {
+          const int j = j0 + e;
+          float h0 = 0.f, h1 = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4 * SELF_BATCH; r += 2) {
+            h0 = fmaf(ui[r], s.u.nt.h.U[j][r], h0);
+            h1 = fmaf(ui[r + 1], s.u.nt.h.U[j][r + 1], h1);
+          }
+          ha[e] = tri(lane, j <= lane ? j : lane);
+          hv[e] = s.L[ha[e]] + (h0 + h1);
+        }
+#pragma unroll
+        for (int e = 0; e < 5; e++)
+          if (j0 + e <= lane) s.L[ha[e]] = hv[e];
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     wsync();
@@ -602,6 +668,9 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
   int it = 0;
   bool conv = false, zsame = false;
   while (it < iterations) {
+    // a compiler barrier: LDS values are loaded where they are used inside the iteration, not hoisted out of the loop
+    // into registers held across all of it
+    asm volatile("" ::: "memory");
     float p;
     PROF(PH_NINIT);
     if (zsame) {  // no row changed its zone in the last step: H, and so its factor in s.L, are unchanged
@@ -622,10 +691,12 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
     // exact line search along p on the piecewise-quadratic cost (step.py:2032-2084)
     float jv[4], ljv;
     rows_jv(s, R, s.p, lane, con, jv, &ljv);
+    PROF(PH_LSJV);
     const float mp = matvec(s, s.p, lane);
     if (lane < NV) s.Mp[lane] = mp;
     const float2 aa = wsum2(lane < NV ? (s.Ma[lane] - s.qsm[lane]) * p : 0.f, lane < NV ? p * mp : 0.f);
     const float a1 = aa.x, a2 = aa.y;
+    PROF(PH_LSMV);
     float alpha = 0.f, lo = 0.f, hi = 1e30f, d0 = 0.f;
     unsigned zprev = 0u;
     bool newton_step = false;
@@ -700,7 +771,12 @@ __device__ __forceinline__ void tape_put(float* dst, const float* src, int n, in
   for (int i = lane; i < end; i += WL) dst[i] = i < n ? src[i] : 0.f;
 }
 
-__device__ __forceinline__ void substep(Sim& s, Rows& R, int lane, int iterations, float* rec, float* ocon) {
+// One call per substep, not inlined: the substep's registers are allocated on their own (inlined into the kernel's
+// substep loop, the allocator spills inside the Newton loop); the call saves and restores its callee-saved registers
+// once per substep.
+__device__ __attribute__((noinline)) void substep(Sim& s, int lane_, int iterations, float* rec, float* ocon) {
+  const int lane = opaque_lane(lane_);  // nothing lane-dependent is hoisted out of the substep loop
+  Rows R;
   if (rec) {
     tape_put(rec + REC_QPOS, s.qpos, NQ, REC_QVEL - REC_QPOS, lane);
     tape_put(rec + REC_QVEL, s.qvel, NV, REC_ASTAR - REC_QVEL, lane);
@@ -859,7 +935,7 @@ __device__ __forceinline__ void substep(Sim& s, Rows& R, int lane, int iteration
 }
 
 // one world per wave64 (one workgroup of 64 lanes)
-__global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict__ qpos, const float* __restrict__ qvel,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_forward(int nw, const float* __restrict__ qpos, const float* __restrict__ qvel,
                                                 const float* __restrict__ warm, const float* __restrict__ ctrl,
                                                 const float* __restrict__ fric, const float* __restrict__ com,
                                                 int iterations, int nsub, float* __restrict__ oqpos,
@@ -875,18 +951,33 @@ __global__ __launch_bounds__(64) void k_forward(int nw, const float* __restrict_
   if (lane < NU) s.ctrl[lane] = ctrl[(size_t)w * NU + lane];
   if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
   if (lane == 0) { s.fric = fric[w]; s.flags = 0; s.niter = 0; }
+  s.dsub[lane] = lane < NV ? cTree.dofmask32[lane] : 0u;
+  if (lane < NB) {  // the chain table: the dofs moving body `lane`, ascending, as bytes
+    const int n = cTree.nchain[lane];
+    for (int k = 0; k < MAXCHAIN / 4; k++) {
+      unsigned wd = 0u;
+      for (int e = 0; e < 4; e++) wd |= (4 * k + e < n ? (unsigned)cTree.chain[lane][4 * k + e] : 255u) << (8 * e);
+      s.chain[lane][k] = wd;
+    }
+  }
 #ifdef G1_PROFILE
   if (lane < NPHASE) s.prof_acc[lane] = 0;
-  if (lane == 0) s.prof_t = __builtin_amdgcn_s_memtime();
+  if (lane == 0) {
+    s.prof_t = __builtin_amdgcn_s_memtime();
+    s.prof_acc[PH_T0] = __builtin_amdgcn_s_memrealtime();  // the world's start and end on the 100 MHz clock, and where
+    s.prof_acc[PH_HWID] = (unsigned long long)__builtin_amdgcn_s_getreg(0xF804)  // HW_ID: wave, SIMD, CU, SE
+                          | (unsigned long long)__builtin_amdgcn_s_getreg(0xF814) << 32;  // XCC_ID
+  }
 #endif
   wsync();
-  Rows R;
   for (int k = 0; k < nsub; k++)
-    substep(s, R, lane, iterations, tape ? tape + ((size_t)w * nsub + k) * REC_WORDS : nullptr,
+    substep(s, lane, iterations, tape ? tape + ((size_t)w * nsub + k) * REC_WORDS : nullptr,
             ocon && k == nsub - 1 ? ocon + (size_t)w * MAXCON * 8 : nullptr);
   if (lane < NQ) oqpos[(size_t)w * NQ + lane] = s.qpos[lane];
   if (lane < NV) { oqvel[(size_t)w * NV + lane] = s.qvel[lane]; owarm[(size_t)w * NV + lane] = s.qacc[lane]; }
 #ifdef G1_PROFILE
+  wsync();
+  if (lane == 0) s.prof_acc[PH_T1] = __builtin_amdgcn_s_memrealtime();
   wsync();
   if (lane < NPHASE && w < PROF_WORLDS) g_prof[w][lane] = s.prof_acc[lane];
 #endif

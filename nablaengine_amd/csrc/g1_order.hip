@@ -6,8 +6,8 @@
 // The reference does the same for its split kernels (host.py:236-264 dk_order_world, row-count buckets).
 //
 // The cost is estimated per world before the launch, in the caller's work buffer:
-//   forward  contacts expected at the input state: broadphase candidates of the 502 pairs (the narrowphase's first
-//            test), candidates between two robot bodies weighted more (each makes the Hessian dense);
+//   forward  contacts at the input state (the main kernel's broadphase and narrowphase): their constraint rows, and a
+//            weight per contact between two robot bodies (each makes the Newton Hessian dense);
 //   adjoint  constraint rows summed over the tape's substep headers.
 // Then one workgroup buckets the costs (LDS histogram, descending prefix) into the permutation the main kernel reads
 // as blockIdx.x -> world. Results do not depend on the order: every world's computation is the same wherever and
@@ -20,12 +20,16 @@ namespace g1k {
 
 constexpr int NBKT = 128;  // cost buckets
 
-// broadphase candidates at the input state: FK of body poses (each body lane walks its chain from the root), geom
-// poses, then the main kernel's bounding test over the pairs
+// contacts at the input state: FK of body poses (each body lane walks its chain from the root), geom poses, the main
+// kernel's broadphase and narrowphase (the same code); the cost counts the contacts' constraint rows (4 per pyramid
+// contact, 1 per frictionless one) plus a weight per contact between two robot bodies (each makes the Newton Hessian
+// dense and adds its outer products)
+constexpr int COST_SELF = 12;
 __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict__ qpos, int* __restrict__ cost) {
   __shared__ float q[40];
   __shared__ float bq[NB][4], bx[NB][4];
   __shared__ float gx[NGEOM][4], gq[NGEOM][4];
+  __shared__ unsigned short cand[NPAIR + 2];
   const int lane = threadIdx.x, w = blockIdx.x;
   if (w >= nw) return;
   if (lane < NQ) q[lane] = qpos[(size_t)w * NQ + lane];
@@ -70,22 +74,40 @@ __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict
     const float q0[4] = {gq[0][0], gq[0][1], gq[0][2], gq[0][3]};
     zaxis(q0, fn);
   }
-  int c = 0;
+  int ncand = 0;
   for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {
     const int pr = lane + WL * k;
+    bool keep = false;
     if (pr < NPAIR) {
       const unsigned pw = cPairW[pr];
       const int g1 = pw & 255u, g2 = (pw >> 8) & 255u;
       const float dif[3] = {gx[g2][0] - gx[g1][0], gx[g2][1] - gx[g1][1], gx[g2][2] - gx[g1][2]};
       const unsigned cls = (pw >> 21) & 7u;
-      if (cls == 0u || cls == 4u) c += dot3(dif, fn) <= cGrb[g2] * (1.f + 1e-5f) + 1e-6f ? 1 : 0;
+      if (cls == 0u || cls == 4u) keep = dot3(dif, fn) <= cGrb[g2] * (1.f + 1e-5f) + 1e-6f;
       else {
         const float rb = cGrb[g1] + cGrb[g2];
-        c += dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f ? 4 : 0;
+        keep = dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f;
       }
     }
+    const unsigned long long bal = ballot(keep);
+    if (keep) cand[ncand + prefix_count(bal, lane)] = (unsigned short)pr;
+    ncand += __popcll(bal);
   }
-  const int tot = wsumi(c);
+  wsync();
+  int c = 0;
+  for (int c0 = 0; c0 < ncand; c0 += WL) {
+    if (c0 + lane < ncand) {
+      const int pr = cand[c0 + lane];
+      Cand o;
+      collide_pair(gx, gq, pr, o);
+      const unsigned pw = cPairW[pr];
+      const unsigned cls = (pw >> 21) & 7u;
+      const int n = (int)o.has[0] + (int)o.has[1];
+      const int rows = ((pw >> 16) & 15u) == 3u ? 4 : 1;
+      c += n * (cls == 0u || cls == 4u ? rows : rows + COST_SELF);
+    }
+  }
+  const int tot = wsumi(c) / 2;
   if (lane == 0) cost[w] = tot < NBKT ? tot : NBKT - 1;
 }
 
