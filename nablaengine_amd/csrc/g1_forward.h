@@ -4,10 +4,12 @@
 
 namespace g1k {
 
+constexpr int MSTRIDE = 36;
+
 struct __align__(16) Sim {
   float qpos[40], qvel[36], qacc[36], ctrl[32], com[4];
   float qsm[36], qacc0[36], Ma[36], grad[36], p[36], Mp[36];
-  float M[NTRI + 2];
+  float M[NV][MSTRIDE];  // the mass matrix, full and symmetric, row-major (rows 16-byte aligned; column 35 unused)
   float L[NTRI + 2];
   float S[NV][8];             // dof motion subspaces about O: angular (0..2), velocity of O (4..6)
   float Q[NB][4], X[NB][4];   // body poses
@@ -38,6 +40,13 @@ struct __align__(16) Sim {
 #ifndef G1_PROFILE
 static_assert(sizeof(Sim) <= 20480, "Sim outgrew the LDS of 8 worlds per CU");
 #endif
+
+// dof t of a chain row of Sim::chain (4 words of byte indices): the index, clamped to a valid dof past the chain's end
+__device__ __forceinline__ int chain_dof(const unsigned* ch, int t, bool* on) {
+  const unsigned d = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
+  *on = d != 255u;
+  return d != 255u ? (int)d : 0;
+}
 
 // per-lane register state of the constraint rows: lane l holds contact l's rows and dof l's limit row
 struct Rows {

@@ -65,6 +65,26 @@ __device__ __forceinline__ void apply_inertia(const float* J, const float* w, co
   for (int k = 0; k < 3; k++) f[k] = J[9] * v[k] - hw[k];
 }
 
+// the packed lower triangle of M + dg diag(kv) into s.L for the factorization: zeros, then each dof lane's chain
+// entries (M has the tree's sparsity: its nonzeros in row i are on the chain of dof i's body)
+__device__ __forceinline__ void m_to_L(Sim& s, int lane, float dg) {
+  for (int e = lane; e < NTRI + 2; e += WL) s.L[e] = 0.f;
+  if (lane < NV) {
+    const int bi = lane < 6 ? 1 : lane - 4;
+    unsigned ch[4];
+    for (int k = 0; k < 4; k++) ch[k] = s.chain[bi][k];
+    const float dd = dg * cKv[lane];
+#pragma unroll
+    for (int t = 0; t < MAXCHAIN; t++) {
+      bool on;
+      const int j = chain_dof(ch, t, &on);
+      const float m = s.M[lane][j] + (j == lane ? dd : 0.f);
+      if (on && j <= lane) s.L[tri(lane, j)] = m;
+    }
+  }
+  wsync();
+}
+
 __device__ void smooth(Sim& s, int lane) {
   if (lane >= 2 && lane < NB) {  // hinge rotations, one lane per body
     float sn, cs;
@@ -186,6 +206,7 @@ __device__ void smooth(Sim& s, int lane) {
   }
   wsync();
   // bias forces (qfrc_bias) projected on the dofs, CRBA row of dof `lane`, actuators
+  for (int e = lane; e < NV * MSTRIDE; e += WL) (&s.M[0][0])[e] = 0.f;
   float bias = 0.f;
   if (lane < NV) {
     const int bi = lane < 6 ? 1 : lane - 4;
@@ -198,16 +219,18 @@ __device__ void smooth(Sim& s, int lane) {
     float Jb[10], n[3], f[3];
     for (int k = 0; k < 10; k++) Jb[k] = s.u.sm.Ic[bi][k];
     apply_inertia(Jb, w, v, n, f);
-    const uint64_t anc = cTree.dofanc[lane];
-#pragma unroll 2
-    for (int j = 0; j <= lane; j++) {
-      float mij = 0.f;
-      if ((anc >> j) & 1ull) {
-        mij = s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
-              + s.S[j][6] * f[2];
-        if (j == lane) mij += cArm[lane];
-      }
-      s.M[tri(lane, j)] = mij;
+    // M[i][j] = S_j . I_c(body i) S_i on the chain of dof i's body (its ancestor dofs j <= i), both halves; the
+    // rest of M is zero (zero-filled above, earlier in this wave's LDS order)
+    unsigned ch[4];
+    for (int k = 0; k < 4; k++) ch[k] = s.chain[bi][k];
+    const float arm = cArm[lane];
+#pragma unroll
+    for (int t = 0; t < MAXCHAIN; t++) {
+      bool on;
+      const int j = chain_dof(ch, t, &on);
+      const float mij = s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
+                        + s.S[j][6] * f[2] + (j == lane ? arm : 0.f);
+      if (on && j <= lane) { s.M[lane][j] = mij; s.M[j][lane] = mij; }
     }
     float act = 0.f;
     if (lane >= 6) {
@@ -227,8 +250,7 @@ __device__ void smooth(Sim& s, int lane) {
   }
   wsync();
   // qacc_smooth = M^-1 qfrc_smooth
-  for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
-  wsync();
+  m_to_L(s, lane, 0.f);
   factor_L(s, lane);
   float x = ltl_solve(s.L, lane < NV ? s.qsm[lane] : 0.f, lane);
   if (lane < NV) s.qacc0[lane] = x;
@@ -339,13 +361,6 @@ __constant__ inline Arr<float, 2> cPSolref = to_float(PAIR_SOLREF);
 __constant__ inline Arr<float, 5> cPSolimp = to_float(PAIR_SOLIMP);
 static_assert(JNT_SOLIMP[4] == 2.0 && PAIR_SOLIMP[4] == 2.0, "kbimp assumes the solimp power 2");
 
-// dof t of a chain row of s.chain (4 words of byte indices): the index, clamped to a valid dof past the chain's end
-__device__ __forceinline__ int chain_dof(const unsigned* ch, int t, bool* on) {
-  const unsigned d = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
-  *on = d != 255u;
-  return d != 255u ? (int)d : 0;
-}
-
 // body spatial velocities of the dof vector v (LDS, NV): bw[b] = sum over b's chain of S_d v_d. The chain comes from
 // the LDS table in one load; every step's loads are independent of the others, so they are all in flight at once.
 __device__ __forceinline__ void body_vel(Sim& s, const float* v, int lane) {
@@ -394,24 +409,26 @@ __device__ __forceinline__ void rows_jv(Sim& s, const Rows& R, const float* v, i
   wsync();
 }
 
-// out = M v (M packed in LDS, v in LDS), lane i < NV: row i left of the diagonal (M[tri(i, j)], j <= i) and
-// column i below it (M[tri(j, i)], j > i), both read at every j from in-bounds addresses and selected, so all the
-// loads are independent and in flight together
+// out = M v (M full in LDS, v in LDS: both 16-byte aligned), lane i < NV: row i as 8 four-float loads and 3 scalars,
+// v's entries as broadcast loads; every load independent of the others
 __device__ __forceinline__ float matvec(const Sim& s, const float* v, int lane_) {
   const int lane = opaque_lane(lane_);
   const int i = lane < NV ? lane : NV - 1;
-  const int base = tri(i, 0);
-  float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-  for (int j0 = 0; j0 < NV; j0 += 5) {  // 5 columns a step (10 loads in flight)
+  const float4* row = reinterpret_cast<const float4*>(s.M[i]);
+  const float4* vv = reinterpret_cast<const float4*>(v);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 5; e++) {
-      const int j = j0 + e;
-      const float a = s.M[base + j], b = s.M[tri(j, 0) + i];
-      acc[e] = fmaf(j <= i ? a : b, v[j], acc[e]);
-    }
+  for (int c = 0; c < 8; c++) {
+    const float4 m = row[c], x = vv[c];
+    acc[0] = fmaf(m.x, x.x, acc[0]);
+    acc[1] = fmaf(m.y, x.y, acc[1]);
+    acc[2] = fmaf(m.z, x.z, acc[2]);
+    acc[3] = fmaf(m.w, x.w, acc[3]);
   }
-  return lane < NV ? ((acc[0] + acc[1]) + (acc[2] + acc[3])) + acc[4] : 0.f;
+  acc[0] = fmaf(s.M[i][32], v[32], acc[0]);
+  acc[1] = fmaf(s.M[i][33], v[33], acc[1]);
+  acc[2] = fmaf(s.M[i][34], v[34], acc[2]);
+  return lane < NV ? (acc[0] + acc[1]) + (acc[2] + acc[3]) : 0.f;
 }
 
 // ============================================================================================== Newton
@@ -552,8 +569,8 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
     }
   }
   PROF(PH_HCOMP);
-  // rows of H: M, then S_j . (n, f) on the ancestor dofs j of i
-  for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
+  // rows of H: zero, then M[i][j] + S_j . (n, f) on the ancestor dofs j of i (M's nonzeros are on these chains)
+  for (int e = lane; e < NTRI + 2; e += WL) s.L[e] = 0.f;
   if (lane < NV) {
     const int bi = lane < 6 ? 1 : lane - 4;
     // the chain of dof i's body: its ancestor dofs (and the root's j <= i). Every load first (S rows, M entries:
@@ -570,8 +587,8 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
         const int j = chain_dof(ch, t0 + e, &hon[e]);
         hon[e] = hon[e] && j <= lane;
         ha[e] = tri(lane, j <= lane ? j : lane);
-        hv[e] = s.M[ha[e]] + (s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0]
-                              + s.S[j][5] * f[1] + s.S[j][6] * f[2]);
+        hv[e] = s.M[lane][j] + (s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0]
+                                + s.S[j][5] * f[1] + s.S[j][6] * f[2]);
       }
 #pragma unroll
       for (int e = 0; e < 8; e++)
@@ -897,10 +914,7 @@ __device__ __attribute__((noinline)) void substep(Sim& s, int lane_, int iterati
   PROF(PH_TAPE);
   // implicitfast: (M + h kv) a_adv = M a*
   {
-    for (int e = lane; e < NTRI; e += WL) s.L[e] = s.M[e];
-    wsync();
-    if (lane < NV) s.L[tri(lane, lane)] += kH * cKv[lane];
-    wsync();
+    m_to_L(s, lane, kH);
     factor_L(s, lane);
     const float adv = ltl_solve(s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
     if (lane < NV) s.qvel[lane] += kH * adv;
