@@ -211,23 +211,37 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
 // L[i][k]), then L x = y root-first (lane k takes L[k][j]); one v_readlane per pivot broadcasts the solved entry.
 // Each lane keeps its running value scaled by 1 / L[lane][lane], so the value broadcast at step i is already the
 // solved entry, and the entries it is multiplied with are pre-scaled the same way and zeroed on lanes that take no
-// update: a step is one v_readlane and one FMA on the dependency chain. The factor entries are loaded from clamped
-// (always valid) addresses without a lane condition, so the loads are issued ahead of the chain.
+// update: a step is one v_readlane and one FMA on the dependency chain. The factor entries come from one base address
+// per pass plus the step's immediate offset (no address arithmetic per step, and every load independent of the
+// chain); the lanes that take no update read an entry of L too (always inside it) and select 0 instead.
 __device__ __forceinline__ float ltl_solve(const float* Lp, float b, int lane_) {
   const int lane = opaque_lane(lane_);
   const int r = lane < NV ? lane : NV - 1;
   const float dself = lane < NV ? 1.f / Lp[tri(r, r)] : 0.f;
   float z = b * dself;  // (b - sum of the solved descendants' terms) / L[lane][lane]
+  // pass 1, step i: lanes r < i take L[i][r] = col[tri(i, 0)] (every lane's address inside L)
+  const float* col = Lp + r;
+  float lv[NV];
+#pragma unroll
+  for (int i = NV - 1; i >= 1; i--) lv[i] = col[tri(i, 0)];
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the chain
 #pragma unroll
   for (int i = NV - 1; i >= 1; i--) {
-    const float lik = Lp[tri(i, r < i ? r : i)] * (lane < i ? dself : 0.f);
+    const float l = lv[i] * dself;
+    const float lik = lane < i ? l : 0.f;
     z = fmaf(-lik, rdl(z, i), z);
   }
   // z = y; root-first: x[lane] = (y[lane] - sum_{k < lane} L[lane][k] x[k]) / L[lane][lane]
+  // pass 2, step k: lanes r > k take L[r][k] = row[k] (every lane's address inside L)
   z *= dself;
+  const float* row = Lp + tri(r, 0);
+#pragma unroll
+  for (int k = 0; k < NV - 1; k++) lv[k] = row[k];
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int k = 0; k < NV - 1; k++) {
-    const float lkj = Lp[tri(r > k ? r : k, k)] * (lane > k ? dself : 0.f);
+    const float l = lv[k] * dself;
+    const float lkj = lane > k ? l : 0.f;
     z = fmaf(-lkj, rdl(z, k), z);
   }
   return z;
