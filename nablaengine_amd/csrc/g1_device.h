@@ -185,9 +185,15 @@ __device__ __forceinline__ float rsqrt_nr(float d) {
 template <bool SPARSE>
 __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
   const int lane = opaque_lane(lane_);
+  // column j = lane of the lower triangle: A[m][j] = col[tri(m, 0)] for m >= j; every lane's address inside the
+  // matrix (lanes past the column select 0), all the loads issued before the elimination
+  const float* col = Lp + (lane < NV ? lane : NV - 1);
   float c[NV];
 #pragma unroll
-  for (int m = 0; m < NV; m++) c[m] = (m >= lane && lane < NV) ? Lp[tri(m, lane)] : 0.f;
+  for (int m = 0; m < NV; m++) c[m] = col[tri(m, 0)];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int m = 0; m < NV; m++) c[m] = m >= lane ? c[m] : 0.f;
 #pragma unroll
   for (int k = NV - 1; k >= 0; k--) {
     const float d = fmaxf(rdl(c[k], k), 1e-30f);
