@@ -496,7 +496,8 @@ __device__ void refresh(Sim& s, Rows& R, int lane, bool con) {
   R.ljar = ljv - R.laref;
 }
 
-constexpr int SELF_BATCH = 4;  // contacts between two robot bodies per outer-product batch
+constexpr int SELF_BATCH = 4;  // contacts between two robot bodies per outer-product batch (4 edge rows each)
+typedef float mfma4 __attribute__((ext_vector_type(4)));
 
 // a floor contact's 6x6 stiffness K = Phi' C Phi about O (21 floats: Kaa 6, Kal 9, Kf 6), C from the curvatures d of
 // its pyramid rows in the frame basis; zero where !on
@@ -538,8 +539,8 @@ __device__ __forceinline__ void contact_stiffness(const Rows& R, const float* dd
 //   the two feet); dof i accumulates (n, f) = (sum of K over the bodies it moves) S_i, and H[i][j] = S_j . (n, f) on
 //   i's ancestor dofs j (the composite stiffness of i's subtree, as CRBA composites inertia).
 //   Contacts between two robot bodies: J'CJ = sum over the active pyramid edges t of u_t u_t', u_t = sqrt(D) J' e_t,
-//   u_t[d] = sigma_d S_d . (r x e_t, e_t) with sigma_d = (dof d moves body 2) - (dof d moves body 1); added as outer
-//   products, SELF_BATCH contacts (4 edges each) a batch.
+//   u_t[d] = sigma_d S_d . (r x e_t, e_t) with sigma_d = (dof d moves body 2) - (dof d moves body 1); added as
+//   U U' on the matrix cores (fp32 MFMA), SELF_BATCH contacts (4 edges each) a batch.
 __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool con) {
   float d[4];
 #pragma unroll
@@ -621,39 +622,38 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
       }
     }
     wsync();
-    if (lane < NV) {  // U[i][r] = sigma_r(i) S_i . psi_r
+    if (lane < 48) {  // U[i][r] = sigma_r(i) S_i . psi_r; rows past the dofs zero
 #pragma unroll
       for (int r = 0; r < 4 * SELF_BATCH; r++) {
         const float* o = s.u.nt.h.psi[r];
         const int b1 = __float_as_int(o[6]), b2 = __float_as_int(o[7]);
         const float sg = (float)((int)((dm >> b2) & 1u) - (int)((dm >> b1) & 1u));
-        s.u.nt.h.U[lane][r] = sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[3] + v[1] * o[4] + v[2] * o[5]);
+        s.u.nt.h.U[lane][r] =
+            lane < NV ? sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[3] + v[1] * o[4] + v[2] * o[5]) : 0.f;
       }
     }
     wsync();
-    if (lane < NV) {  // H[i][j] += sum_r U[i][r] U[j][r] for j <= i, 5 columns a step: their loads together
-      float ui[4 * SELF_BATCH];
-      for (int r = 0; r < 4 * SELF_BATCH; r++) ui[r] = s.u.nt.h.U[lane][r];
+    {  // H += U U' on the matrix cores: 16 x 16 tiles (ti, tj <= ti) of the 48-row padding, k = 16 rows in steps of 4
+      // (v_mfma_f32_16x16x4f32: lane l gives A[l % 16][l / 16] and B[l / 16][l % 16], holds C[4 (l / 16) + e][l % 16])
+      const int lr = lane & 15, lk = lane >> 4;
+      float op[3][4];
 #pragma unroll
-      for (int j0 = 0; j0 < NV; j0 += 5) {
-        float hv[5];
-        int ha[5];
+      for (int t = 0; t < 3; t++)
 #pragma unroll
-        for (int e = 0; e < 5; e++) {
-          const int j = j0 + e;
-          float h0 = 0.f, h1 = 0.f;
+        for (int kk = 0; kk < 4; kk++) op[t][kk] = s.u.nt.h.U[16 * t + lr][4 * kk + lk];
 #pragma unroll
-          for (int r = 0; r < 4 * SELF_BATCH; r += 2) {
-            h0 = fmaf(ui[r], s.u.nt.h.U[j][r], h0);
-            h1 = fmaf(ui[r + 1], s.u.nt.h.U[j][r + 1], h1);
+      for (int ti = 0; ti < 3; ti++) {
+#pragma unroll
+        for (int tj = 0; tj <= ti; tj++) {
+          mfma4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kk = 0; kk < 4; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(op[ti][kk], op[tj][kk], acc, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int i = 16 * ti + 4 * lk + e, j = 16 * tj + lr;
+            if (i < NV && j <= i) s.L[tri(i, j)] += acc[e];
           }
-          ha[e] = tri(lane, j <= lane ? j : lane);
-          hv[e] = s.L[ha[e]] + (h0 + h1);
         }
-#pragma unroll
-        for (int e = 0; e < 5; e++)
-          if (j0 + e <= lane) s.L[ha[e]] = hv[e];
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
     wsync();
