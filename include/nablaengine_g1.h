@@ -31,11 +31,12 @@ int dk_fwd_upload(const float* consts, hipStream_t st);
 void dk_fwd_sizes(long long* o);
 
 /* No counterpart in the reference's ABI (its DK_PROFILE builds read g_prof the same way, host.py:13-17): in a build
- * with -DG1_PROFILE, copies the last forward's per-world phase cycles (s_memtime) of the first nw worlds, nw x 23
+ * with -DG1_PROFILE, copies the last forward's per-world phase cycles (s_memtime) of the first nw worlds, nw x 27
  * uint64 (smooth, collision, rows, Newton init, Hessian, factor, solve, line search, update, gradient, implicitfast,
  * tape, Newton iterations, line-search evaluations, dense factorizations, then the cycles of parts of the line
  * search (row velocities J p; M p) and of the Hessian (contact stiffnesses, subtree sums, rows), then the world's start
- * and end (s_memrealtime, 100 MHz) and where it ran (HW_ID | XCC_ID << 32)); returns -1 in the production build. */
+ * and end (s_memrealtime, 100 MHz) and where it ran (HW_ID | XCC_ID << 32), then the cycles of parts of the smooth
+ * dynamics (forward kinematics, body forces, subtree sums, CRBA and bias)); returns -1 in the production build. */
 int dk_prof_read(unsigned long long* out, int nw);
 
 /* Replaces <variant>_adjoint (jax_ffi.py:228-241) for every (clamp_kv, normal) variant at once: the VJP of one control

@@ -132,7 +132,7 @@ __device__ __forceinline__ void wsync() { __syncthreads(); }
 // (lane 0's clock at phase ends, after a barrier), written to g_prof[world][phase] for the first PROF_WORLDS worlds
 // and read by dk_prof_read. The production build compiles every mark to nothing.
 enum { PH_SMOOTH = 0, PH_COLLIDE, PH_ROWS, PH_NINIT, PH_HESS, PH_FACTOR, PH_SOLVE, PH_LSEARCH, PH_UPDATE, PH_GRAD,
-       PH_IMPLICIT, PH_TAPE, PH_ITERS, PH_LSEVAL, PH_DENSE, PH_LSJV, PH_LSMV, PH_HK, PH_HCOMP, PH_HROWS, PH_T0, PH_T1, PH_HWID, NPHASE };
+       PH_IMPLICIT, PH_TAPE, PH_ITERS, PH_LSEVAL, PH_DENSE, PH_LSJV, PH_LSMV, PH_HK, PH_HCOMP, PH_HROWS, PH_T0, PH_T1, PH_HWID, PH_SFK, PH_SBF, PH_SSUB, PH_SCRBA, NPHASE };
 constexpr int PROF_WORLDS = 16384;
 #ifdef G1_PROFILE
 __device__ inline unsigned long long g_prof[PROF_WORLDS][NPHASE];

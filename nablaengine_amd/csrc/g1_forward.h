@@ -23,8 +23,8 @@ struct __align__(16) Sim {
   unsigned long long prof_t, prof_acc[NPHASE];
 #endif
   union {
-    struct { float F[NB][4], T[NB][4], Ic[NB][12], ha[NB][4]; } sm;  // smooth dynamics: subtree force, moment about O,
-                                                                     // inertia; hinge rotations
+    struct { float F[NB][4], T[NB][4], Ic[NB][12], hl[NB][12]; } sm;  // smooth dynamics: subtree force, moment about O,
+                                                                     // inertia; bodies' local transforms
     struct { float gx[NGEOM][4], gq[NGEOM][4]; float stage[MAXCON][16]; unsigned short cand[NPAIR + 2]; } col;
     struct {
       float bw[NB][8];  // body spatial velocity of a dof vector: angular (0..2), velocity of O (4..6)

@@ -86,17 +86,23 @@ __device__ __forceinline__ void m_to_L(Sim& s, int lane, float dg) {
 }
 
 __device__ void smooth(Sim& s, int lane) {
-  if (lane >= 2 && lane < NB) {  // hinge rotations, one lane per body
+  // each hinge body's local transform, one lane per body: q_l = quat (x) hinge rotation, the body's offset in its
+  // parent's frame p_b, and the hinge axis in the parent's frame a_l = quat a (the hinge rotation keeps its own axis)
+  if (lane >= 2 && lane < NB) {
     float sn, cs;
     sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
-    s.u.sm.ha[lane][0] = cs;
-    s.u.sm.ha[lane][1] = sn * cAxis[3 * lane];
-    s.u.sm.ha[lane][2] = sn * cAxis[3 * lane + 1];
-    s.u.sm.ha[lane][3] = sn * cAxis[3 * lane + 2];
+    const float qb[4] = {cQuat[4 * lane], cQuat[4 * lane + 1], cQuat[4 * lane + 2], cQuat[4 * lane + 3]};
+    const float ax[3] = {cAxis[3 * lane], cAxis[3 * lane + 1], cAxis[3 * lane + 2]};
+    const float ha[4] = {cs, sn * ax[0], sn * ax[1], sn * ax[2]};
+    float* h = s.u.sm.hl[lane];
+    qmul(qb, ha, h);
+    for (int c = 0; c < 3; c++) h[4 + c] = cPos[3 * lane + c];
+    qrot(qb, ax, h + 8);
   }
   wsync();
   // FK: each body lane walks its own chain from the root: pose, velocity, and the bias acceleration (qacc = 0;
-  // gravity as the root's -g) (source.py:186-235 fwd_body)
+  // gravity as the root's -g) (source.py:186-235 fwd_body). The chain's bodies come from the LDS chain table (the
+  // hinge dofs past the root's 6, body = dof - 4), their local transforms from the table above.
   float Q[4], X[3], W[3], V[3], AL[3], A[3];
   {
     float n = rsqrtf(s.qpos[3] * s.qpos[3] + s.qpos[4] * s.qpos[4] + s.qpos[5] * s.qpos[5] + s.qpos[6] * s.qpos[6]);
@@ -105,32 +111,33 @@ __device__ void smooth(Sim& s, int lane) {
     qrot(Q, s.qvel + 3, W);
   }
   const int b = lane < NB ? lane : 0;
-  const int depth = cDepth[b];
+  unsigned ch[4];
+  for (int k = 0; k < 4; k++) ch[k] = s.chain[b][k];
 #pragma unroll
   for (int l = 1; l < MAXDEPTH; l++) {
-    if (l < depth) {
-      const int k = cTree.path[b][l];
-      float q0[4], t[3], aw[3], r[3], awd[3], u[3], wr[3], u2[3];
-      const float qb[4] = {cQuat[4 * k], cQuat[4 * k + 1], cQuat[4 * k + 2], cQuat[4 * k + 3]};
-      const float pb[3] = {cPos[3 * k], cPos[3 * k + 1], cPos[3 * k + 2]};
-      const float ax[3] = {cAxis[3 * k], cAxis[3 * k + 1], cAxis[3 * k + 2]};
-      const float ha[4] = {s.u.sm.ha[k][0], s.u.sm.ha[k][1], s.u.sm.ha[k][2], s.u.sm.ha[k][3]};
-      qmul(Q, qb, q0);
-      qrot(Q, pb, t);  // r = X_child - X_parent
-      for (int c = 0; c < 3; c++) r[c] = t[c];
-      qmul(q0, ha, Q);
-      qrot(Q, ax, aw);
-      const float qd = s.qvel[k + 4];
+    bool on;
+    const int d = chain_dof(ch, 5 + l, &on);  // the hinge dof of the body at depth l + 1 on b's chain
+    if (on) {
+      const int k = d - 4;
+      const float* h = s.u.sm.hl[k];
+      const float ql[4] = {h[0], h[1], h[2], h[3]}, pb[3] = {h[4], h[5], h[6]}, al[3] = {h[8], h[9], h[10]};
+      float t[3], aw[3], awd[3], u[3], wr[3], u2[3], q1[4];
+      qrot(Q, pb, t);  // X_child - X_parent
+      qrot(Q, al, aw);
+      qmul(Q, ql, q1);
+      for (int c = 0; c < 4; c++) Q[c] = q1[c];
+      const float qd = s.qvel[d];
       for (int c = 0; c < 3; c++) awd[c] = aw[c] * qd;
       // from the parent's W, AL (in registers): A, V, AL, then W
-      cross(AL, r, u);
-      cross(W, r, wr);
+      cross(AL, t, u);
+      cross(W, t, wr);
       cross(W, wr, u2);
       for (int c = 0; c < 3; c++) { A[c] += u[c] + u2[c]; V[c] += wr[c]; X[c] += t[c]; }
       cross(W, awd, u);
       for (int c = 0; c < 3; c++) { AL[c] += u[c]; W[c] += awd[c]; }
     }
   }
+  PROF(PH_SFK);
   if (lane < NB) {
     for (int k = 0; k < 4; k++) s.Q[lane][k] = lane == 0 ? (k == 0 ? 1.f : 0.f) : Q[k];
     for (int k = 0; k < 3; k++) s.X[lane][k] = lane == 0 ? 0.f : X[k];
@@ -184,6 +191,7 @@ __device__ void smooth(Sim& s, int lane) {
     J[6] = m * cc3[0]; J[7] = m * cc3[1]; J[8] = m * cc3[2]; J[9] = m;
   }
   wsync();
+  PROF(PH_SBF);
   // subtree sums by masks (lane = body): force, moment about O, spatial inertia
   float Fs[3] = {0.f, 0.f, 0.f}, Ts[3] = {0.f, 0.f, 0.f}, Js[10];
   for (int k = 0; k < 10; k++) Js[k] = 0.f;
@@ -198,6 +206,7 @@ __device__ void smooth(Sim& s, int lane) {
     for (int k = 0; k < 3; k++) { s.u.sm.F[lane][k] = Fs[k]; s.u.sm.T[lane][k] = Ts[k]; }
     for (int k = 0; k < 10; k++) s.u.sm.Ic[lane][k] = Js[k];
   }
+  PROF(PH_SSUB);
   // motion subspaces
   if (lane < NV) {
     float w[3], v[3];
@@ -249,6 +258,7 @@ __device__ void smooth(Sim& s, int lane) {
     if (lane == 0) { s.clampm[0] = (unsigned)cm; s.clampm[1] = (unsigned)(cm >> 32); }
   }
   wsync();
+  PROF(PH_SCRBA);
   // qacc_smooth = M^-1 qfrc_smooth
   m_to_L(s, lane, 0.f);
   factor_L(s, lane);
