@@ -67,27 +67,37 @@ __device__ __forceinline__ void st_sv(float* p, const Sv& x) {
 
 enum { TW_V = 0, TW_L, TW_Y, TW_AW, TW_A2, TW_A1, NTW };  // per-body twists
 enum { FB_F1 = 0, FB_P, FB_X1, FB_F2, FB_P2, FB_EG, FB_OL, FB_OA, FB_OV, NFB };  // per-body force vectors
-constexpr int CRES = 48;  // per-contact result words
+__device__ __forceinline__ Sv ld_sv6(const float* p) {  // a spatial vector packed as 6 floats (8-byte aligned)
+  Sv r;
+  for (int k = 0; k < 3; k++) { r.w[k] = p[k]; r.v[k] = p[3 + k]; }
+  return r;
+}
+__device__ __forceinline__ void st_sv6(float* p, const Sv& x) {
+  for (int k = 0; k < 3; k++) { p[k] = x.w[k]; p[3 + k] = x.v[k]; }
+}
 
 struct __align__(16) Adj {
   float qpos[40], qvel[36], astar[36], aadv[36], at[36];
   float qb[36], vb[36], vt[36], qn[36], y[36], lam[36], ub[32], ctrl[32], com[4];
-  float L[NTRI + 2];
   float S[NV][8];
-  float Q[NB][4], X[NB][4], ha[NB][4];
+  float Q[NB][4], X[NB][4];
+  float hl[NB][12];                  // each hinge body's local transform: q_l, p_b, a_l (as the forward's FK)
+  unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
   float O[4];
   float fric;
   float Ib[NB][12];
-  float tw[NB][NTW][8];
+  float tw[NB][NTW][6];              // per-body twists (6 floats each)
   float gx[NGEOM][4], gq[NGEOM][4];
   union {
-    float cres[MAXCON][CRES];
-    float fb[NB][NFB][8];
+    float L[NTRI + 2];         // the taped factor of the solves
+    float fb[NB][NFB][6];      // then the per-body force vectors (6 floats each)
   };
   int ncon, flags;
   unsigned clampm[2], limzone[2], limrow[2], czone[8];
   unsigned short con[MAXCON];
 };
+// 8 worlds per CU: the LDS of one world must stay within 160 KB / 8
+static_assert(sizeof(Adj) <= 20480, "Adj outgrew the LDS of 8 worlds per CU");
 
 // impedance and its derivative in the distance (kbimp's curve, solimp power 2; 0 where the curve is clamped)
 __device__ __forceinline__ void imp_d(const float* solimp, float pos, float* imp, float* dimp) {
@@ -322,14 +332,17 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   }
   if (lane == 0) s.ncon = min((int)(__float_as_uint(rec[REC_HDR]) & 255u), MAXCON);
   wsync();
-  // poses
+  // poses: each hinge body's local transform (lane = body), then each body lane walks its chain (the chain table)
   if (lane >= 2 && lane < NB) {
     float sn, cs;
     sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
-    s.ha[lane][0] = cs;
-    s.ha[lane][1] = sn * cAxis[3 * lane];
-    s.ha[lane][2] = sn * cAxis[3 * lane + 1];
-    s.ha[lane][3] = sn * cAxis[3 * lane + 2];
+    const float qb[4] = {cQuat[4 * lane], cQuat[4 * lane + 1], cQuat[4 * lane + 2], cQuat[4 * lane + 3]};
+    const float ax[3] = {cAxis[3 * lane], cAxis[3 * lane + 1], cAxis[3 * lane + 2]};
+    const float ha[4] = {cs, sn * ax[0], sn * ax[1], sn * ax[2]};
+    float* h = s.hl[lane];
+    qmul(qb, ha, h);
+    for (int c = 0; c < 3; c++) h[4 + c] = cPos[3 * lane + c];
+    qrot(qb, ax, h + 8);
   }
   if (lane < 3) s.O[lane] = s.qpos[lane];
   wsync();
@@ -339,18 +352,19 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     for (int k = 0; k < 4; k++) Q[k] = s.qpos[3 + k] * n;
     for (int k = 0; k < 3; k++) X[k] = s.qpos[k];
     const int b = lane < NB ? lane : 0;
-    const int depth = cDepth[b];
+    unsigned ch[4];
+    for (int k = 0; k < 4; k++) ch[k] = s.chain[b][k];
 #pragma unroll
     for (int l = 1; l < MAXDEPTH; l++) {
-      if (l < depth) {
-        const int k = cTree.path[b][l];
-        const float qb[4] = {cQuat[4 * k], cQuat[4 * k + 1], cQuat[4 * k + 2], cQuat[4 * k + 3]};
-        const float pb[3] = {cPos[3 * k], cPos[3 * k + 1], cPos[3 * k + 2]};
-        const float ha[4] = {s.ha[k][0], s.ha[k][1], s.ha[k][2], s.ha[k][3]};
-        float q0[4], t[3];
-        qmul(Q, qb, q0);
+      bool on;
+      const int d = chain_dof(ch, 5 + l, &on);  // the hinge dof of the body at depth l + 1 on b's chain
+      if (on) {
+        const float* h = s.hl[d - 4];
+        const float ql[4] = {h[0], h[1], h[2], h[3]}, pb[3] = {h[4], h[5], h[6]};
+        float t[3], q1[4];
         qrot(Q, pb, t);
-        qmul(q0, ha, Q);
+        qmul(Q, ql, q1);
+        for (int c = 0; c < 4; c++) Q[c] = q1[c];
         for (int c = 0; c < 3; c++) X[c] += t[c];
       }
     }
@@ -458,10 +472,12 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body
   if (lane >= 1 && lane < NB) {
     Sv V = sv0(), Lm = sv0(), Y = sv0(), Aw = sv0(), A2 = sv0(), Ac = sv0();
-    const int n = cTree.nchain[lane];
+    unsigned ch[4];
+    for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
     for (int t = 0; t < MAXCHAIN; t++) {
-      if (t < n) {
-        const int d = cTree.chain[lane][t];
+      bool on;
+      const int d = chain_dof(ch, t, &on);
+      if (on) {
         const Sv Sd = ld_sv(s.S[d]);
         const float vd = s.qvel[d];
         V = sv_add(V, Sd, vd);
@@ -478,15 +494,15 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     }
     Sv A1 = sv_add(Aw, Ac);
     for (int k = 0; k < 3; k++) A1.v[k] -= kGrav[k];
-    st_sv(s.tw[lane][TW_V], V);
-    st_sv(s.tw[lane][TW_L], Lm);
-    st_sv(s.tw[lane][TW_Y], Y);
-    st_sv(s.tw[lane][TW_AW], Aw);
-    st_sv(s.tw[lane][TW_A2], A2);
-    st_sv(s.tw[lane][TW_A1], A1);
+    st_sv6(s.tw[lane][TW_V], V);
+    st_sv6(s.tw[lane][TW_L], Lm);
+    st_sv6(s.tw[lane][TW_Y], Y);
+    st_sv6(s.tw[lane][TW_AW], Aw);
+    st_sv6(s.tw[lane][TW_A2], A2);
+    st_sv6(s.tw[lane][TW_A1], A1);
   }
   if (lane == 0)
-    for (int t = 0; t < NTW; t++) st_sv(s.tw[0][t], sv0());
+    for (int t = 0; t < NTW; t++) st_sv6(s.tw[0][t], sv0());
   wsync();
   // limit rows (their dof's lane): through the distance only (J constant)
   float lgq = 0.f, lgv = 0.f;
@@ -509,15 +525,17 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   }
   // contacts (lane = contact of the tape's table): replay, row terms, geometry VJP -> wrenches
   const int ncon = s.ncon;
+  Sv cOmL = sv0(), cOmA = sv0(), cW1 = sv0(), cW2 = sv0();  // this lane's contact: row sums, the sides' wrenches
+  float cbb = 0.f;
+  int cb1 = 0, cb2 = 0;
+  bool cact = false;
   if (lane < ncon) {
-    float* o = s.cres[lane];
-    for (int e = 0; e < CRES; e++) o[e] = 0.f;
     const unsigned zc = (s.czone[lane >> 3] >> (4 * (lane & 7))) & 15u;
     const int pr = min((int)(s.con[lane] & 511u), NPAIR - 1), slot = s.con[lane] >> 9;
     const unsigned w = cPairW[pr];
     const int b1 = cGbody[w & 255u], b2 = cGbody[(w >> 8) & 255u], dim = (w >> 16) & 15u;
-    o[46] = __int_as_float(b1);
-    o[47] = __int_as_float(b2);
+    cb1 = b1;
+    cb2 = b2;
     if (zc) {
       Cand cd;
       collide_pair(s.gx, s.gq, pr, cd);
@@ -538,9 +556,9 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
         const float D = 1.f / fmaxf(iw * (1.f - imp) / imp, 1e-15f), dD = dimp / (iw * (1.f - imp) * (1.f - imp));
         float rr[3];
         for (int q = 0; q < 3; q++) rr[q] = pos[q] - s.O[q];
-        const Sv Lc = sv_add(ld_sv(s.tw[b2][TW_L]), ld_sv(s.tw[b1][TW_L]), -1.f);
-        const Sv Ac = sv_add(ld_sv(s.tw[b2][TW_AW]), ld_sv(s.tw[b1][TW_AW]), -1.f);
-        const Sv Vc = sv_add(ld_sv(s.tw[b2][TW_V]), ld_sv(s.tw[b1][TW_V]), -1.f);
+        const Sv Lc = sv_add(ld_sv6(s.tw[b2][TW_L]), ld_sv6(s.tw[b1][TW_L]), -1.f);
+        const Sv Ac = sv_add(ld_sv6(s.tw[b2][TW_AW]), ld_sv6(s.tw[b1][TW_AW]), -1.f);
+        const Sv Vc = sv_add(ld_sv6(s.tw[b2][TW_V]), ld_sv6(s.tw[b1][TW_V]), -1.f);
         float dbar = 0.f, rb[3] = {0.f, 0.f, 0.f}, frb[9];
         for (int q = 0; q < 9; q++) frb[q] = 0.f;
         Sv OmL = sv0(), OmA = sv0();
@@ -572,10 +590,10 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
         }
         const Sv OmV = sv_add(sv0(), OmA, b);
         // the bodies' twist changes at the contact (side b2 +, b1 -)
-        const Sv e1 = sv_add(sv_add(cross_mf(ld_sv(s.tw[b1][TW_L]), OmL), cross_mf(ld_sv(s.tw[b1][TW_AW]), OmA)),
-                             cross_mf(ld_sv(s.tw[b1][TW_V]), OmV));
-        const Sv e2 = sv_add(sv_add(cross_mf(ld_sv(s.tw[b2][TW_L]), OmL), cross_mf(ld_sv(s.tw[b2][TW_AW]), OmA)),
-                             cross_mf(ld_sv(s.tw[b2][TW_V]), OmV));
+        const Sv e1 = sv_add(sv_add(cross_mf(ld_sv6(s.tw[b1][TW_L]), OmL), cross_mf(ld_sv6(s.tw[b1][TW_AW]), OmA)),
+                             cross_mf(ld_sv6(s.tw[b1][TW_V]), OmV));
+        const Sv e2 = sv_add(sv_add(cross_mf(ld_sv6(s.tw[b2][TW_L]), OmL), cross_mf(ld_sv6(s.tw[b2][TW_AW]), OmA)),
+                             cross_mf(ld_sv6(s.tw[b2][TW_V]), OmV));
         float x1b[3], t1b[3], x2b[3], t2b[3];
         contact_geom_vjp(s, pr, slot, fr, dbar, rb, frb, normal, x1b, t1b, x2b, t2b);
         const int g1 = w & 255u, g2 = (w >> 8) & 255u;
@@ -589,49 +607,56 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
           cross(xo, x2b, m);
           for (int q = 0; q < 3; q++) { G2.w[q] = t2b[q] + m[q]; G2.v[q] = x2b[q]; }
         }
-        st_sv(o + 0, OmL);
-        st_sv(o + 8, OmA);
-        st_sv(o + 16, sv_add(G1, e1, -1.f));  // the b1 side's wrench (its twists enter with -)
-        st_sv(o + 24, sv_add(G2, e2));        // the b2 side's wrench
-        o[32] = b;
+        cOmL = OmL;
+        cOmA = OmA;
+        cW1 = sv_add(G1, e1, -1.f);  // the b1 side's wrench (its twists enter with -)
+        cW2 = sv_add(G2, e2);        // the b2 side's wrench
+        cbb = b;
+        cact = true;
       }
     }
   }
-  wsync();
-  // per body: the contacts' wrenches (contact order), then the RNE force vectors
+  // per body: the contacts' wrenches and row sums, summed over the contact lanes once per distinct contact body
+  // (masked wave sums, a fixed order); body lane B keeps its totals
   Sv EG = sv0(), OL = sv0(), OA = sv0(), OV = sv0();
-  if (lane >= 1 && lane < NB) {
-    for (int c = 0; c < ncon; c++) {
-      const float* o = s.cres[c];
-      const int b1 = __float_as_int(o[46]), b2 = __float_as_int(o[47]);
-      const float bb = o[32];
-      const float s2 = b2 == lane ? 1.f : 0.f, s1 = b1 == lane ? 1.f : 0.f;
-      if (s1 == 0.f && s2 == 0.f) continue;
-      const Sv OmL = ld_sv(o), OmA = ld_sv(o + 8);
-      EG = sv_add(EG, ld_sv(o + 24), s2);
-      EG = sv_add(EG, ld_sv(o + 16), s1);
-      OL = sv_add(OL, OmL, s2 - s1);
-      OA = sv_add(OA, OmA, s2 - s1);
-      OV = sv_add(OV, OmA, (s2 - s1) * bb);
+  for (unsigned m = wor(cact ? (1u << cb1) | (1u << cb2) : 0u) & ~1u; m; m &= m - 1u) {
+    const int B = __builtin_ctz(m);
+    const bool on2 = cact && cb2 == B, on1 = cact && cb1 == B;
+    const float sd = on2 ? 1.f : (on1 ? -1.f : 0.f);
+    float x[24];
+    for (int k = 0; k < 3; k++) {
+      x[k] = on2 ? cW2.w[k] : (on1 ? cW1.w[k] : 0.f);
+      x[3 + k] = on2 ? cW2.v[k] : (on1 ? cW1.v[k] : 0.f);
+      x[6 + k] = sd * cOmL.w[k];
+      x[9 + k] = sd * cOmL.v[k];
+      x[12 + k] = sd * cOmA.w[k];
+      x[15 + k] = sd * cOmA.v[k];
+      x[18 + k] = sd * cbb * cOmA.w[k];
+      x[21 + k] = sd * cbb * cOmA.v[k];
     }
+    wsum_n<24>(x);
+    if (lane == B)
+      for (int k = 0; k < 3; k++) {
+        EG.w[k] = x[k]; EG.v[k] = x[3 + k]; OL.w[k] = x[6 + k]; OL.v[k] = x[9 + k];
+        OA.w[k] = x[12 + k]; OA.v[k] = x[15 + k]; OV.w[k] = x[18 + k]; OV.v[k] = x[21 + k];
+      }
   }
-  wsync();
   if (lane >= 1 && lane < NB) {
     const float* I = s.Ib[lane];
-    const Sv V = ld_sv(s.tw[lane][TW_V]), Lm = ld_sv(s.tw[lane][TW_L]);
+    const Sv V = ld_sv6(s.tw[lane][TW_V]), Lm = ld_sv6(s.tw[lane][TW_L]);
     const Sv IV = inertia_apply(I, V), IL = inertia_apply(I, Lm);
-    const Sv F1 = sv_add(inertia_apply(I, ld_sv(s.tw[lane][TW_A1])), cross_mf(V, IV));
+    const Sv F1 = sv_add(inertia_apply(I, ld_sv6(s.tw[lane][TW_A1])), cross_mf(V, IV));
     const Sv Qs = cross_mf(V, IL), Rs = cross_mf(Lm, IV), Ts = inertia_apply(I, cross_mm(V, Lm));
     const Sv X1 = sv_add(sv_add(Rs, Ts), Qs, -1.f);
-    st_sv(s.fb[lane][FB_F1], F1);
-    st_sv(s.fb[lane][FB_P], IL);
-    st_sv(s.fb[lane][FB_X1], X1);
-    st_sv(s.fb[lane][FB_F2], inertia_apply(I, ld_sv(s.tw[lane][TW_A2])));
-    st_sv(s.fb[lane][FB_P2], inertia_apply(I, ld_sv(s.tw[lane][TW_Y])));
-    st_sv(s.fb[lane][FB_EG], EG);
-    st_sv(s.fb[lane][FB_OL], OL);
-    st_sv(s.fb[lane][FB_OA], OA);
-    st_sv(s.fb[lane][FB_OV], OV);
+    st_sv6(s.fb[lane][FB_F1], F1);
+    st_sv6(s.fb[lane][FB_P], IL);
+    st_sv6(s.fb[lane][FB_X1], X1);
+    st_sv6(s.fb[lane][FB_F2], inertia_apply(I, ld_sv6(s.tw[lane][TW_A2])));
+    st_sv6(s.fb[lane][FB_P2], inertia_apply(I, ld_sv6(s.tw[lane][TW_Y])));
+    st_sv6(s.fb[lane][FB_EG], EG);
+    st_sv6(s.fb[lane][FB_OL], OL);
+    st_sv6(s.fb[lane][FB_OA], OA);
+    st_sv6(s.fb[lane][FB_OV], OV);
   }
   wsync();
   // per dof: subtree sums and the joint's outside terms
@@ -642,15 +667,15 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     Sv F1 = sv0(), P = sv0(), X1 = sv0(), F2 = sv0(), P2 = sv0(), EGs = sv0(), OLs = sv0(), OAs = sv0(), OVs = sv0();
     for (int b = 1; b < NB; b++) {
       if (!((sub >> b) & 1u)) continue;
-      F1 = sv_add(F1, ld_sv(s.fb[b][FB_F1]));
-      P = sv_add(P, ld_sv(s.fb[b][FB_P]));
-      X1 = sv_add(X1, ld_sv(s.fb[b][FB_X1]));
-      F2 = sv_add(F2, ld_sv(s.fb[b][FB_F2]));
-      P2 = sv_add(P2, ld_sv(s.fb[b][FB_P2]));
-      EGs = sv_add(EGs, ld_sv(s.fb[b][FB_EG]));
-      OLs = sv_add(OLs, ld_sv(s.fb[b][FB_OL]));
-      OAs = sv_add(OAs, ld_sv(s.fb[b][FB_OA]));
-      OVs = sv_add(OVs, ld_sv(s.fb[b][FB_OV]));
+      F1 = sv_add(F1, ld_sv6(s.fb[b][FB_F1]));
+      P = sv_add(P, ld_sv6(s.fb[b][FB_P]));
+      X1 = sv_add(X1, ld_sv6(s.fb[b][FB_X1]));
+      F2 = sv_add(F2, ld_sv6(s.fb[b][FB_F2]));
+      P2 = sv_add(P2, ld_sv6(s.fb[b][FB_P2]));
+      EGs = sv_add(EGs, ld_sv6(s.fb[b][FB_EG]));
+      OLs = sv_add(OLs, ld_sv6(s.fb[b][FB_OL]));
+      OAs = sv_add(OAs, ld_sv6(s.fb[b][FB_OA]));
+      OVs = sv_add(OVs, ld_sv6(s.fb[b][FB_OV]));
     }
     Sv Vo = sv0(), Lo = sv0(), Yo = sv0(), Awo = sv0(), A1o = sv0(), A2o = sv0();
     for (int k = 0; k < 3; k++) A1o.v[k] = -kGrav[k];
@@ -661,14 +686,14 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
       }
     } else if (j >= 6) {
       const int p = cParent[bj];
-      Vo = ld_sv(s.tw[p][TW_V]); Lo = ld_sv(s.tw[p][TW_L]); Yo = ld_sv(s.tw[p][TW_Y]);
-      Awo = ld_sv(s.tw[p][TW_AW]); A1o = ld_sv(s.tw[p][TW_A1]); A2o = ld_sv(s.tw[p][TW_A2]);
+      Vo = ld_sv6(s.tw[p][TW_V]); Lo = ld_sv6(s.tw[p][TW_L]); Yo = ld_sv6(s.tw[p][TW_Y]);
+      Awo = ld_sv6(s.tw[p][TW_AW]); A1o = ld_sv6(s.tw[p][TW_A1]); A2o = ld_sv6(s.tw[p][TW_A2]);
     }
     const Sv Sj = ld_sv(s.S[j]);
     const Sv sig = cross_mm(Sj, Vo), alp = cross_mm(Sj, A1o), ell = cross_mm(Sj, Lo);
     const float dq1 = -sv_dot(ell, F1) - sv_dot(alp, P) + sv_dot(cross_mm(sig, Vo), P) + sv_dot(sig, X1);
     Sv rho = sv0();
-    if (j >= 3) rho = sv_add(sig, cross_mm(Sj, ld_sv(s.tw[bj][TW_V])));
+    if (j >= 3) rho = sv_add(sig, cross_mm(Sj, ld_sv6(s.tw[bj][TW_V])));
     const float dv1 = -sv_dot(Sj, X1) - sv_dot(rho, P);
     const float dq2 = -sv_dot(cross_mm(Sj, Yo), F2) - sv_dot(cross_mm(Sj, A2o), P2);
     const float dqc = sv_dot(Sj, EGs) - sv_dot(Sj, sv_add(sv_add(cross_mf(Lo, OLs), cross_mf(Awo, OAs)),
@@ -711,6 +736,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
   if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = ctrl ? ctrl[(size_t)w * NU + lane] : 0.f; }
   if (lane == 0) { s.fric = fric[w]; s.flags = 0; }
+  chain_table(s.chain, lane);
   // the output cotangents in the tangent space at the output state (its root quaternion: the last substep's
   // integration replayed from the record)
   if (lane < NV) s.vb[lane] = gv_out[(size_t)w * NV + lane];

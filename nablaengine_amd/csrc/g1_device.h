@@ -113,6 +113,18 @@ __device__ __forceinline__ void wsum_n(float* x) {
 #pragma unroll
   for (int e = 0; e < N; e++) x[e] = rdl(x[e], 63);
 }
+// bitwise OR over the wave's 64 lanes (wsum's DPP steps with OR; lanes without a source OR in 0)
+__device__ __forceinline__ unsigned wor(unsigned v) {
+#define G1_DPPI(x, ctrl, rmask) (unsigned)__builtin_amdgcn_update_dpp(0, (int)(x), (ctrl), (rmask), 0xf, false)
+  v |= G1_DPPI(v, 0x111, 0xf);
+  v |= G1_DPPI(v, 0x112, 0xf);
+  v |= G1_DPPI(v, 0x114, 0xf);
+  v |= G1_DPPI(v, 0x118, 0xf);
+  v |= G1_DPPI(v, 0x142, 0xa);
+  v |= G1_DPPI(v, 0x143, 0xc);
+#undef G1_DPPI
+  return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
+}
 __device__ __forceinline__ int wsumi(int v) {  // small counts: exact in float
   return (int)wsum((float)v);
 }
@@ -142,6 +154,25 @@ __device__ inline unsigned long long g_prof[PROF_WORLDS][NPHASE];
 #define PROF_DECL
 #define PROF_MARK(acc, t, k) do { } while (0)
 #endif
+
+// The chain table of a world (in LDS, built at kernel start by chain_table): per body, the dofs moving it in
+// ascending order, one byte each in 4 words, 255 past the chain's end. chain_dof reads entry t of a row: the dof,
+// clamped to a valid one past the end (with *on false).
+__device__ __forceinline__ int chain_dof(const unsigned* ch, int t, bool* on) {
+  const unsigned d = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
+  *on = d != 255u;
+  return d != 255u ? (int)d : 0;
+}
+__device__ __forceinline__ void chain_table(unsigned (*chain)[MAXCHAIN / 4], int lane) {
+  if (lane < NB) {
+    const int n = cTree.nchain[lane];
+    for (int k = 0; k < MAXCHAIN / 4; k++) {
+      unsigned wd = 0u;
+      for (int e = 0; e < 4; e++) wd |= (4 * k + e < n ? (unsigned)cTree.chain[lane][4 * k + e] : 255u) << (8 * e);
+      chain[lane][k] = wd;
+    }
+  }
+}
 
 // ------------------------------------------------------------------------------------------------ 3D helpers
 __device__ __forceinline__ void qmul(const float* a, const float* b, float* o) {

@@ -42,13 +42,6 @@ struct __align__(16) Sim {
 static_assert(sizeof(Sim) <= 20480, "Sim outgrew the LDS of 8 worlds per CU");
 #endif
 
-// dof t of a chain row of Sim::chain (4 words of byte indices): the index, clamped to a valid dof past the chain's end
-__device__ __forceinline__ int chain_dof(const unsigned* ch, int t, bool* on) {
-  const unsigned d = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
-  *on = d != 255u;
-  return d != 255u ? (int)d : 0;
-}
-
 // per-lane register state of the constraint rows: lane l holds contact l's rows and dof l's limit row
 struct Rows {
   float r[3], fr[9], mu, D;  // contact point - O; frame rows n, t1, t2; friction; the rows' D

@@ -976,14 +976,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
   if (lane == 0) { s.fric = fric[w]; s.flags = 0; s.niter = 0; }
   s.dsub[lane] = lane < NV ? cTree.dofmask32[lane] : 0u;
-  if (lane < NB) {  // the chain table: the dofs moving body `lane`, ascending, as bytes
-    const int n = cTree.nchain[lane];
-    for (int k = 0; k < MAXCHAIN / 4; k++) {
-      unsigned wd = 0u;
-      for (int e = 0; e < 4; e++) wd |= (4 * k + e < n ? (unsigned)cTree.chain[lane][4 * k + e] : 255u) << (8 * e);
-      s.chain[lane][k] = wd;
-    }
-  }
+  chain_table(s.chain, lane);
 #ifdef G1_PROFILE
   if (lane < NPHASE) s.prof_acc[lane] = 0;
   if (lane == 0) {
