@@ -446,37 +446,34 @@ struct NewtonOut { int it; bool conv, fresh; };  // fresh: s.L holds H's factor 
 
 // gradient at the current jar: grad = M a - qfrc_smooth - J' f, f = -D x on the rows with x < 0; returns |grad|
 __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
-  if (con) {  // the contact's frame force in world coordinates and its moment about O
+  // J' f: the contact's frame force f = -D x (rows with x < 0) as a world force F and its moment T about O, summed per
+  // distinct contact body by masked wave sums (body 2 +, body 1 -); dof i adds S_i . (T, F) of the bodies it moves
+  float T[3] = {0.f, 0.f, 0.f}, F[3] = {0.f, 0.f, 0.f};
+  bool act = false;
+  if (con) {
     float f[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) f[t] = (t < R.nr && R.jar[t] < 0.f) ? -R.D * R.jar[t] : 0.f;
     float fn, f1 = 0.f, f2 = 0.f;
     if (R.dim == 3) { fn = f[0] + f[1] + f[2] + f[3]; f1 = R.mu * (f[0] - f[1]); f2 = R.mu * (f[2] - f[3]); }
     else fn = f[0];
-    float F[3], T[3];
     for (int k = 0; k < 3; k++) F[k] = fn * R.fr[k] + f1 * R.fr[3 + k] + f2 * R.fr[6 + k];
     cross(R.r, F, T);
-    float* o = s.u.nt.ft[lane];
-    o[0] = T[0]; o[1] = T[1]; o[2] = T[2]; o[3] = __int_as_float(R.b1);
-    o[4] = F[0]; o[5] = F[1]; o[6] = F[2]; o[7] = __int_as_float(R.b2);
+    act = fn != 0.f;
   }
-  wsync();
+  const unsigned dm = s.dsub[lane];
+  const int il = lane < NV ? lane : 0;
+  const float w[3] = {s.S[il][0], s.S[il][1], s.S[il][2]}, v[3] = {s.S[il][4], s.S[il][5], s.S[il][6]};
+  float tau = 0.f;
+  for (unsigned m = wor(act ? (1u << R.b1) | (1u << R.b2) : 0u) & ~1u; m; m &= m - 1u) {
+    const int B = __builtin_ctz(m);
+    const float sd = (act && R.b2 == B) ? 1.f : ((act && R.b1 == B) ? -1.f : 0.f);
+    float x[6] = {sd * T[0], sd * T[1], sd * T[2], sd * F[0], sd * F[1], sd * F[2]};
+    wsum_n<6>(x);
+    if ((dm >> B) & 1u) tau += w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
+  }
   float g = 0.f;
   if (lane < NV) {
-    const unsigned mask = s.dsub[lane];
-    const float w[3] = {s.S[lane][0], s.S[lane][1], s.S[lane][2]}, v[3] = {s.S[lane][4], s.S[lane][5], s.S[lane][6]};
-    float tau = 0.f;
-    const int ncon = s.ncon;
-    for (int c0 = 0; c0 < ncon; c0 += 4) {  // 4 contacts a step: their loads in flight together
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int c = c0 + e < ncon ? c0 + e : c0;
-        const float* o = s.u.nt.ft[c];
-        const int b1 = __float_as_int(o[3]), b2 = __float_as_int(o[7]);
-        const float sg = c0 + e < ncon ? (float)((int)((mask >> b2) & 1u) - (int)((mask >> b1) & 1u)) : 0.f;
-        tau += sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[4] + v[1] * o[5] + v[2] * o[6]);
-      }
-    }
     if (R.lsg != 0.f && R.ljar < 0.f) tau += R.lsg * (-R.lD * R.ljar);
     g = s.Ma[lane] - s.qsm[lane] - tau;
     s.grad[lane] = g;
