@@ -199,12 +199,6 @@ __device__ __forceinline__ void cross(const float* a, const float* b, float* o) 
 }
 __device__ __forceinline__ float dot3(const float* a, const float* b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2]; }
 
-// 1 / sqrt(d): the hardware estimate (v_rsq_f32) refined by one Newton-Raphson step y (3 - d y^2) / 2
-__device__ __forceinline__ float rsqrt_nr(float d) {
-  float y = __builtin_amdgcn_rsqf(d);
-  return y * (1.5f - 0.5f * d * y * y);
-}
-
 // ------------------------------------------------------------------------------------------------ LTL factorization
 // A = L' L with L lower triangular, eliminated leaf-first (k = NV-1 .. 0), as MuJoCo factors M: with parents before
 // children in the dof order, row k of L is nonzero only at k's ancestor dofs (no fill-in) for a matrix with the
@@ -212,7 +206,9 @@ __device__ __forceinline__ float rsqrt_nr(float d) {
 // triangle in registers (c[m] = A[m][j], m >= j), so row k's entries L[k][j] are lane-local and L[k][m] is one
 // v_readlane away: step k is one pivot and, per ancestor m of k, a broadcast and one FMA on every lane.
 // SPARSE = false visits every m < k (the dense factor of a matrix with cross-branch entries). In place in Lp (packed
-// lower, TRI layout).
+// lower, TRI layout). Lane j's registers c[m] for m < j hold other entries of the matrix (loaded from in-bounds
+// addresses, not zeroed): they are updated from one another only, never broadcast (a broadcast reads lane m's c[k],
+// k > m) and never stored, so the valid entries do not depend on them.
 template <bool SPARSE>
 __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
   const int lane = opaque_lane(lane_);
@@ -222,14 +218,11 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
   float c[NV];
 #pragma unroll
   for (int m = 0; m < NV; m++) c[m] = col[tri(m, 0)];
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int m = 0; m < NV; m++) c[m] = m >= lane ? c[m] : 0.f;
 #pragma unroll
   for (int k = NV - 1; k >= 0; k--) {
     const float d = fmaxf(rdl(c[k], k), 1e-30f);
-    const float inv = rsqrt_nr(d);
-    c[k] = lane == k ? d * inv : c[k] * inv;  // L[k][k] on lane k, L[k][j] = A[k][j] / L[k][k] on lane j
+    // L[k][j] = A[k][j] / sqrt(d) on lane j; on lane k itself d / sqrt(d) = L[k][k] (the hardware 1/sqrt, 1 ulp)
+    c[k] *= __builtin_amdgcn_rsqf(d);
     // every broadcast of the step first, then the updates: a v_readlane's SGPR is not read by the next instruction
     float bc[NV];
 #pragma unroll
