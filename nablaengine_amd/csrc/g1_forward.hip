@@ -718,42 +718,65 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
     PROF(PH_LSJV);
     const float mp = matvec(s, s.p, lane);
     if (lane < NV) s.Mp[lane] = mp;
-    const float2 aa = wsum2(lane < NV ? (s.Ma[lane] - s.qsm[lane]) * p : 0.f, lane < NV ? p * mp : 0.f);
-    const float a1 = aa.x, a2 = aa.y;
-    PROF(PH_LSMV);
-    float alpha = 0.f, lo = 0.f, hi = 1e30f, d0 = 0.f;
-    unsigned zprev = 0u;
-    bool newton_step = false;
-    for (int k = 0; k <= 40; k++) {
-      float fd = 0.f, fdd = 0.f;
-      unsigned z = 0u;
+    // per row: x(alpha) = jar + alpha jv; rows past the kept ones start at +1e30 (never in the quadratic zone)
+    float xr[5], vr[5], dr[5];
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        if (t < R.nr) {
-          const float x = R.jar[t] + alpha * jv[t];
-          if (x < 0.f) { fd += R.D * x * jv[t]; fdd += R.D * jv[t] * jv[t]; z |= 1u << t; }
-        }
+    for (int t = 0; t < 4; t++) {
+      xr[t] = t < R.nr ? R.jar[t] : 1e30f;
+      vr[t] = t < R.nr ? jv[t] : 0.f;
+      dr[t] = R.D;
+    }
+    xr[4] = R.lsg != 0.f ? R.ljar : 1e30f;
+    vr[4] = R.lsg != 0.f ? ljv : 0.f;
+    dr[4] = R.lD;
+    // the slope and curvature of the rows' cost at alpha (the quadratic-zone rows), and the zone pattern
+    auto rows_at = [&](float alpha, float* fd, float* fdd, unsigned* z) {
+      float a = 0.f, b = 0.f;
+      unsigned zz = 0u;
+#pragma unroll
+      for (int t = 0; t < 5; t++) {
+        const float x = fmaf(alpha, vr[t], xr[t]);
+        const bool q = x < 0.f;
+        const float dv = q ? dr[t] * vr[t] : 0.f;
+        a = fmaf(dv, x, a);
+        b = fmaf(dv, vr[t], b);
+        zz |= q ? 1u << t : 0u;
       }
-      if (R.lsg != 0.f) {
-        const float x = R.ljar + alpha * ljv;
-        if (x < 0.f) { fd += R.lD * x * ljv; fdd += R.lD * ljv * ljv; z |= 16u; }
-      }
-      if (ballot(!(newton_step && z == zprev)) == 0ull) break;  // the Newton step kept every row on its piece
-      if (k == 40) break;
+      *fd = a; *fdd = b; *z = zz;
+    };
+    // the Gauss term's coefficients a1 = (M a - f) . p, a2 = p . M p and the rows at alpha = 0: one reduction
+    float fd0, fdd0;
+    unsigned zprev;
+    rows_at(0.f, &fd0, &fdd0, &zprev);
+    float r4[4] = {lane < NV ? (s.Ma[lane] - s.qsm[lane]) * p : 0.f, lane < NV ? p * mp : 0.f, fd0, fdd0};
+    wsum_n<4>(r4);
+    const float a1 = r4[0], a2 = r4[1];
+    PROF(PH_LSMV);
+    // exact 1-D Newton with bracketing on the piecewise-quadratic cost (step.py:2032-2084)
+    float alpha = 0.f, lo = 0.f, hi = 1e30f;
+    const float d0 = r4[2] + a1;
+    if (d0 < 0.f) {
+      float fd = d0, fdd = r4[3] + a2;
+      for (int k = 1; k <= 40; k++) {
+        if (fabsf(fd) <= 1e-7f * fabsf(d0)) break;
+        if (fd < 0.f) lo = alpha; else hi = alpha;
+        float nx = fmaf(-fd, __builtin_amdgcn_rcpf(fdd), alpha);
+        const bool newton_step = nx > lo && nx < hi;
+        if (!newton_step) nx = hi < 1e29f ? 0.5f * (lo + hi) : 2.f * fmaxf(alpha, 1e-6f);
+        alpha = nx;
+        float f1, f2;
+        unsigned z;
+        rows_at(alpha, &f1, &f2, &z);
+        if (ballot(!(newton_step && z == zprev)) == 0ull) break;  // the Newton step kept every row on its piece
+        if (k == 40) break;
 #ifdef G1_PROFILE
-      if (lane == 0) s.prof_acc[PH_LSEVAL] += 1;
+        if (lane == 0) s.prof_acc[PH_LSEVAL] += 1;
 #endif
-      const float2 ff = wsum2(fd, fdd);
-      fd = ff.x + a1 + alpha * a2;
-      fdd = ff.y + a2;
-      if (k == 0) { d0 = fd; if (d0 >= 0.f) break; }
-      if (fabsf(fd) <= 1e-7f * fabsf(d0)) break;
-      if (fd < 0.f) lo = alpha; else hi = alpha;
-      float nx = alpha - fd / fdd;
-      newton_step = nx > lo && nx < hi;
-      if (!newton_step) nx = hi < 1e29f ? 0.5f * (lo + hi) : 2.f * fmaxf(alpha, 1e-6f);
-      zprev = z;
-      alpha = nx;
+        const float2 ff = wsum2(f1, f2);
+        fd = ff.x + fmaf(alpha, a2, a1);
+        fdd = ff.y + a2;
+        zprev = z;
+      }
     }
     PROF(PH_LSEARCH);
     // move along p
