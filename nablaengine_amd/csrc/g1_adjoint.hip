@@ -634,7 +634,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
       x[18 + k] = sd * cbb * cOmA.w[k];
       x[21 + k] = sd * cbb * cOmA.v[k];
     }
-    wsum_n<24>(x);
+    wsum_nw<24>(x, ncon);  // contact lanes only
     if (lane == B)
       for (int k = 0; k < 3; k++) {
         EG.w[k] = x[k]; EG.v[k] = x[3 + k]; OL.w[k] = x[6 + k]; OL.v[k] = x[9 + k];

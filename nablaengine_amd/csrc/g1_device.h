@@ -125,6 +125,35 @@ __device__ __forceinline__ unsigned wor(unsigned v) {
 #undef G1_DPPI
   return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
 }
+// wsum_n over the first `width` lanes only (the other lanes' values are not read): 4 DPP steps for 16 lanes, 5 for
+// 32, 6 for 64; width uniform. The same fixed order on every call with the same width.
+template <int N>
+__device__ __forceinline__ void wsum_nw(float* x, int width) {
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x111, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x112, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x114, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x118, 0xf);
+  if (width <= 16) {
+#pragma unroll
+    for (int e = 0; e < N; e++) x[e] = rdl(x[e], 15);
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x142, 0xa);
+  if (width <= 32) {
+#pragma unroll
+    for (int e = 0; e < N; e++) x[e] = rdl(x[e], 31);
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x143, 0xc);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] = rdl(x[e], 63);
+}
 __device__ __forceinline__ int wsumi(int v) {  // small counts: exact in float
   return (int)wsum((float)v);
 }

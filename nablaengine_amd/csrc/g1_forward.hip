@@ -469,7 +469,7 @@ __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
     const int B = __builtin_ctz(m);
     const float sd = (act && R.b2 == B) ? 1.f : ((act && R.b1 == B) ? -1.f : 0.f);
     float x[6] = {sd * T[0], sd * T[1], sd * T[2], sd * F[0], sd * F[1], sd * F[2]};
-    wsum_n<6>(x);
+    wsum_nw<6>(x, s.ncon);  // contact lanes only
     if ((dm >> B) & 1u) tau += w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
   }
   float g = 0.f;
@@ -560,13 +560,16 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
   const int il = lane < NV ? lane : 0;
   const float w[3] = {s.S[il][0], s.S[il][1], s.S[il][2]}, v[3] = {s.S[il][4], s.S[il][5], s.S[il][6]};
   float n[3] = {0.f, 0.f, 0.f}, f[3] = {0.f, 0.f, 0.f};
+  float K[21];
+  contact_stiffness(R, d, floorc, K);
   for (unsigned long long rem = ballot(floorc); rem;) {  // one distinct contact body B a pass
     const int B = rdli(R.b2, __builtin_ctzll(rem));
     const bool in = floorc && R.b2 == B;
     rem &= ~ballot(in);
     float k[21];
-    contact_stiffness(R, d, in, k);
-    wsum_n<21>(k);
+#pragma unroll
+    for (int e = 0; e < 21; e++) k[e] = in ? K[e] : 0.f;
+    wsum_nw<21>(k, s.ncon);  // contact lanes only
     if ((dm >> B) & 1u) {  // n += Kaa w + Kal v, f += Kal' w + Kll v
       n[0] += k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
       n[1] += k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
