@@ -1,17 +1,23 @@
-"""Benchmark of the MI355X G1 control step (BASELINE.json metric): ms per 20 ms control step at 4096 worlds and
-world-steps/s, forward (and forward+VJP where the library has the adjoint), on one GPU.
+"""Benchmark of the MI355X G1 control step (BASELINE.json metric): ms per 20 ms control step and world-steps/s, forward
+and forward+VJP, at 4096 worlds (and 16384), on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu] [--no-16k]
 
 A step is one control step (4 substeps of 5 ms, Newton 10 iterations) of B worlds of BASELINE config 1 (seeded
-synthetic states, inputs resident in HBM before the timed region). K steps are timed back to back between two
-synchronizations; rank 0 prints one JSON line. `roofline` is the dominant kernel's (the forward): algorithmic flops
-per launch (the float64 CPU restatement's closed-form phase counts on the same inputs, counted once before timing)
-divided by the kernel's average duration from HIP events on the stream it is launched on; peak is MI355X's FP32
-(157.3 TFLOP/s). `cpu_baseline` is the float64 CPU restatement ("port", one thread) on 64 config-0 worlds, repeated
-for about 10 s.
+synthetic states, inputs resident in HBM before the timed region), exactly what torch_ffi.forward runs: the dispatch
+order pre-pass and the forward kernel. K steps are timed back to back between two synchronizations with HIP events on
+the launch stream; rank 0 prints one JSON line. Forward+VJP is the taped forward plus the adjoint (torch_ffi.forward
+(tape=True) + torch_ffi.backward), timed the same way.
+
+`roofline` is the dominant kernel's, k_forward: algorithmic flops per launch (the float64 CPU restatement's
+closed-form phase counts on the same inputs, counted once before timing, per world-step x B) divided by k_forward's
+mean duration, timed live here with HIP events around K back-to-back launches of the forward alone (the order
+computed once before, dk_fwd_forward_ordered); peak is MI355X's FP32 (157.3 TFLOP/s). `traffic` is k_forward's HBM
+bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (the committed summary). `cpu_baseline` is the float64 CPU
+restatement ("port", one thread) on 64 config-0 worlds for about 10 s.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -28,13 +34,14 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 # interface bytes per world-step (inputs 556 B, outputs 440 B), the design-independent HBM traffic of the forward
 IO_BYTES_FWD = (36 + 35 + 35 + 29 + 1 + 3) * 4 + (36 + 35 + 35) * 4 + 16
-# HBM bytes per forward launch at 4096 worlds, measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (two runs,
+# HBM bytes per k_forward launch at 4096 worlds, measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (two runs,
 # each scaled by the same counter's reading on a copy of known size, `--copy-mib`); the summary holds the command
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_forward_4096_traffic.md")
+KEYS = ("qpos", "qvel", "warm", "ctrl", "friction", "com")
 
 
 def measured_traffic(worlds):
-    """Bytes per forward launch from the committed traffic summary (line `traffic_bytes_per_launch: N`), or None
+    """Bytes per k_forward launch from the committed traffic summary (line `traffic_bytes_per_launch: N`), or None
     when there is none for this world count."""
     if worlds != 4096 or not os.path.exists(TRAFFIC_FILE):
         return None
@@ -67,6 +74,58 @@ def algorithmic_flops(st):
     return float(np.mean(r[4]))
 
 
+def timed(fn, steps, warmup, stream):
+    """Mean ms per call of fn over `steps` back-to-back calls (HIP events on `stream`), after `warmup` calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def measure(B, steps, warmup, kernel=False):
+    """(forward ms, fwd+VJP ms, k_forward ms or None, info of the last forward) at B worlds of config 1."""
+    import torch
+    from nablaengine_amd import synthetic, torch_ffi
+    st = synthetic.states(B, config=1)
+    args = [torch.from_numpy(st[k]).cuda() for k in KEYS]
+    stream = torch.cuda.current_stream()
+    out = {}
+
+    def fwd():
+        out["r"] = torch_ffi.forward(*args)
+    ms = timed(fwd, steps, warmup, stream)
+    info = out["r"][3].cpu().numpy()
+    gq, gv = (torch.from_numpy(x).cuda() for x in synthetic.cotangents(B))
+
+    def vjp():
+        r = torch_ffi.forward(*args, tape=True)
+        torch_ffi.backward(r[4], args[4], args[5], gq, gv)
+    vjp_ms = timed(vjp, steps, warmup, stream)
+    kms = None
+    if kernel:  # k_forward alone: the order once, then the ordered launches back to back
+        lib = torch_ffi.load_library()
+        st_ = ctypes.c_void_p(stream.cuda_stream)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+        kw = dict(dtype=torch.float32, device="cuda")
+        q1, v1, w1 = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 35), **kw)
+        inf = torch.empty((B, 4), dtype=torch.int32, device="cuda")
+        work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+        assert lib.dk_fwd_order(st_, B, p(args[0]), p(work)) == 0
+
+        def kern():
+            assert lib.dk_fwd_forward_ordered(st_, B, *map(p, args), 10, 4, p(q1), p(v1), p(w1), p(inf), None, None,
+                                              p(work)) == 0
+        kms = timed(kern, steps, warmup, stream)
+    return ms, vjp_ms, kms, info
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,6 +133,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--worlds", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-16k", action="store_true", help="skip the 16384-world forward and fwd+VJP lines")
     ap.add_argument("--flop-sample", type=int, default=512, help="worlds the flop count is taken on")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="before the timed steps, copy a buffer of this many MiB 3 times (a kernel of known HBM "
@@ -94,67 +154,40 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     B = a.worlds
+    ms, vjp_ms, kms, info = measure(B, a.steps, a.warmup, kernel=True)
+    big = None
+    if not a.no_16k and B != 16384:
+        bms, bvjp, _, binfo = measure(16384, max(a.steps // 4, 3), max(a.warmup // 4, 2))
+        big = {"worlds": 16384, "ms_per_step": bms, "ms_per_step_fwd_vjp": bvjp,
+               "world_steps_per_s": 16384e3 / bms, "world_steps_per_s_fwd_vjp": 16384e3 / bvjp}
     st = synthetic.states(B, config=1)
-    args = [torch.from_numpy(st[k]).cuda() for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
-    stream = torch.cuda.current_stream()
-    for _ in range(a.warmup):
-        torch_ffi.forward(*args)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        out = torch_ffi.forward(*args)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / a.steps
-    ms = e0.elapsed_time(e1) / a.steps
-    info = out[3].cpu().numpy()
-    # fwd+VJP
-    vjp_ms = None
-    try:
-        gq, gv = synthetic.cotangents(B)
-        gq, gv = torch.from_numpy(gq).cuda(), torch.from_numpy(gv).cuda()
-        r = torch_ffi.forward(*args, tape=True)
-        torch_ffi.backward(r[4], args[4], args[5], gq, gv)
-        torch.cuda.synchronize()
-        for _ in range(a.warmup):
-            r = torch_ffi.forward(*args, tape=True)
-            torch_ffi.backward(r[4], args[4], args[5], gq, gv)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(a.steps):
-            r = torch_ffi.forward(*args, tape=True)
-            torch_ffi.backward(r[4], args[4], args[5], gq, gv)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        vjp_ms = e0.elapsed_time(e1) / a.steps
-    except RuntimeError:
-        vjp_ms = None
     sub = {k: v[: a.flop_sample] for k, v in st.items()}
     fl = algorithmic_flops(sub)
-    achieved = fl * B / (ms * 1e-3) / 1e12
+    achieved = fl * B / (kms * 1e-3) / 1e12
     res = {
         "metric": METRIC, "value": B * 1e3 / ms, "unit": "world-steps/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (BASELINE config 1: seeded standing states, random ctrl; model g1_train.mjb)",
         "config": {"workload": f"G1 control step forward, {B} worlds, 4 x 5 ms substeps, Newton 10 it, implicitfast",
                    "worlds": B, "substeps": 4, "iterations": 10},
-        "ms_per_step_host_wall": wall,
         "ms_per_step_fwd_vjp": vjp_ms,
-        "world_steps_per_s_fwd_vjp": None if vjp_ms is None else B * 1e3 / vjp_ms,
+        "world_steps_per_s_fwd_vjp": B * 1e3 / vjp_ms,
+        "ms_k_forward": kms,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_FP32_TFLOPS, "traffic": measured_traffic(B),
-                     "note": "FP32 vector (VALU) work, no MFMA: achieved = closed-form algorithmic flops "
-                             f"({fl:.3g} per world-step, float64 restatement on {len(sub['qpos'])} of the worlds) x "
-                             "worlds / the forward kernel's mean duration (HIP events, its stream); one kernel "
-                             "launch per step"},
-        "roofline_hbm": {"achieved": IO_BYTES_FWD * B / (ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": IO_BYTES_FWD * B / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                     "note": "FP32 vector (VALU) work, no MFMA in the Newton path's bulk: achieved = closed-form "
+                             f"algorithmic flops ({fl:.3g} per world-step, float64 restatement on {len(sub['qpos'])} "
+                             "of the worlds) x worlds / k_forward's mean duration (HIP events around back-to-back "
+                             "launches of the forward kernel alone, its stream); the step also runs the dispatch-order "
+                             "pre-pass (ms_per_step - ms_k_forward)"},
+        "roofline_hbm": {"achieved": IO_BYTES_FWD * B / (kms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": IO_BYTES_FWD * B / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                          "note": f"interface bytes {IO_BYTES_FWD} per world-step"},
         "capacity": {"contacts_max": int(info[:, 1].max()), "rows_max": int(info[:, 2].max()),
                      "overflow_worlds": int(((info[:, 3] & 20) != 0).sum())},
     }
+    if big:
+        res["worlds_16384"] = big
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res))

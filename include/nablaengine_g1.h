@@ -19,6 +19,14 @@ extern "C" {
 int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
                    int* info, float* ocon, float* tape, void* work);
+/* No counterpart in the reference's ABI (its order is internal to dk_forward_split, host.py:310-330): the dispatch
+ * order of dk_fwd_forward on its own, written into work (dk_fwd_work_bytes(nw) bytes) from the input qpos; and the
+ * forward launched with an order already in work (no recomputation), for callers that reuse one order across steps
+ * (the worlds' costs change slowly) and for timing the forward kernel alone. Results are the same in any order. */
+int dk_fwd_order(hipStream_t st, int nw, const float* qpos, void* work);
+int dk_fwd_forward_ordered(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm,
+                           const float* ctrl, const float* fric, const float* com, int iterations, int nsub, float* oq,
+                           float* ov, float* ow, int* info, float* ocon, float* tape, const void* work);
 /* Replaces <fwd>_work_bytes (jax_ffi.py:265): scratch bytes the forward's work buffer takes for nw worlds (the
  * dispatch order, heaviest worlds first: 8 bytes per world). work = NULL runs the worlds in index order instead; the
  * results are the same either way. */

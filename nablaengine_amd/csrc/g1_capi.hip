@@ -6,7 +6,8 @@
 namespace g1k {
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info, float* ocon, float* tape, void* work);
+                   int* info, float* ocon, float* tape, void* work, int order);
+int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work);
 size_t order_work_bytes(int nw);
 size_t forward_lds_bytes();
 size_t adjoint_lds_bytes();
@@ -35,7 +36,20 @@ int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel,
                    int* info, float* ocon, float* tape, void* work) {
   if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0) return (int)hipErrorInvalidValue;
   return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
-                             work);
+                             work, 1);
+}
+
+int dk_fwd_order(hipStream_t st, int nw, const float* qpos, void* work) {
+  if (nw < 0 || (nw > 0 && !work)) return (int)hipErrorInvalidValue;
+  return nw > 0 ? g1k::launch_order_fwd(st, nw, qpos, work) : 0;
+}
+
+int dk_fwd_forward_ordered(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm,
+                           const float* ctrl, const float* fric, const float* com, int iterations, int nsub, float* oq,
+                           float* ov, float* ow, int* info, float* ocon, float* tape, const void* work) {
+  if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0 || (nw > 0 && !work)) return (int)hipErrorInvalidValue;
+  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
+                             const_cast<void*>(work), 2);
 }
 
 long long dk_fwd_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }

@@ -1033,14 +1033,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 namespace g1k {
 int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work);
+// order: 0 index order (work unused), 1 compute the order into work first, 2 the order already in work
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info, float* ocon, float* tape, void* work) {
+                   int* info, float* ocon, float* tape, void* work, int order) {
   if (nw <= 0) return 0;
   const int* perm = nullptr;
-  if (work) {  // the dispatch order, heaviest worlds first
-    const int rc = launch_order_fwd(st, nw, qpos, work);
-    if (rc) return rc;
+  if (work && order) {  // the dispatch order, heaviest worlds first
+    if (order == 1) {
+      const int rc = launch_order_fwd(st, nw, qpos, work);
+      if (rc) return rc;
+    }
     perm = (const int*)work;
   }
   hipLaunchKernelGGL(k_forward, dim3(nw), dim3(64), 0, st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub,

@@ -56,6 +56,9 @@ def load_library(path=None):
         vp, i32, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
         lib.dk_fwd_forward.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 7
         lib.dk_fwd_forward.restype = i32
+        lib.dk_fwd_forward_ordered.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 7
+        lib.dk_fwd_forward_ordered.restype = i32
+        lib.dk_fwd_order.argtypes, lib.dk_fwd_order.restype = [vp, i32, vp, vp], i32
         lib.dk_fwd_work_bytes.argtypes, lib.dk_fwd_work_bytes.restype = [i32], ctypes.c_longlong
         lib.dk_fwd_upload.argtypes, lib.dk_fwd_upload.restype = [vp, vp], i32
         lib.dk_fwd_sizes.argtypes, lib.dk_fwd_sizes.restype = [vp], None
