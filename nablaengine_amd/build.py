@@ -13,9 +13,11 @@ SOURCES = ["g1_forward.hip", "g1_adjoint.hip", "g1_order.hip", "g1_capi.hip"]
 ARCH = os.environ.get("NABLA_OFFLOAD_ARCH", "gfx950")
 # packed FP32 instructions off (-packed-fp32-ops): the kernels are written for scalar FP32. Warnings that mark
 # undefined behaviour the optimizer exploits (a non-void function falling off its end becomes unreachable code, and a
-# kernel then runs into whatever follows) are errors.
+# kernel then runs into whatever follows) are errors. Machine LICM off: the kernels hold one world per wave at the
+# 256-VGPR limit, and values it hoists out of the substep and Newton loops are spilled to scratch inside them.
 FLAGS = ["-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared", "-Xclang", "-target-feature", "-Xclang",
-         "-packed-fp32-ops", "-ffp-contract=fast", "-Wno-unused-command-line-argument", "-Werror=return-type",
+         "-packed-fp32-ops", "-ffp-contract=fast", "-mllvm", "-disable-machine-licm",
+         "-Wno-unused-command-line-argument", "-Werror=return-type",
          "-Werror=uninitialized", "-Werror=sometimes-uninitialized", "-Werror=array-bounds"]
 
 

@@ -821,10 +821,11 @@ __device__ __forceinline__ void tape_put(float* dst, const float* src, int n, in
   for (int i = lane; i < end; i += WL) dst[i] = i < n ? src[i] : 0.f;
 }
 
-// One call per substep, not inlined: the substep's registers are allocated on their own (inlined into the kernel's
-// substep loop, the allocator spills inside the Newton loop); the call saves and restores its callee-saved registers
-// once per substep.
-__device__ __attribute__((noinline)) void substep(Sim& s, int lane_, int iterations, float* rec, float* ocon) {
+// Inlined into the kernel's substep loop. The library is built with machine LICM off (-mllvm -disable-machine-licm):
+// with it on, uniform values derived from the constant tables (the contact impedance parameters) are hoisted out of
+// the substep loop into registers held across the Newton loop, and spilled there; a call per substep instead would
+// save and restore about 112 callee-saved VGPRs through scratch each time (0.5 GB of HBM traffic per launch).
+__device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float* rec, float* ocon) {
   const int lane = opaque_lane(lane_);  // nothing lane-dependent is hoisted out of the substep loop
   Rows R;
   if (rec) {
