@@ -31,6 +31,19 @@ int dk_fwd_forward_ordered(hipStream_t st, int nw, const float* qpos, const floa
  * dispatch order, heaviest worlds first: 8 bytes per world). work = NULL runs the worlds in index order instead; the
  * results are the same either way. */
 long long dk_fwd_work_bytes(int nw);
+/* Replaces <fwd>_kinematics (jax_ffi.py:281-285; g1_engine/kinematics.py:1-45): the kinematics outputs of nw states
+ * (MJX kinematics + com_pos + com_vel). in: qpos (nw, 36), qvel (nw, 35), com (nw, 3); out: qn (nw, 36) qpos with the
+ * root quaternion normalized, xpos (nw, 31, 3), xquat (nw, 31, 4) body frames (world body 0 included), cvel (nw, 31, 6)
+ * [angular; linear] twists at subtree_com[1], sc (nw, 31, 3) subtree COMs. torch_ffi runs it on a step's output state
+ * for step(..., kinematics=True). */
+int dk_fwd_kinematics(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com, float* qn,
+                      float* xpos, float* xquat, float* cvel, float* sc);
+/* Replaces <fwd>_kinematics_vjp (jax_ffi.py:286-292): the VJP of dk_fwd_kinematics at (qpos, qvel, com): the outputs'
+ * cotangents gqn, gxpos, gxquat, gcvel, gsc (shapes as the outputs) -> gq (nw, 36), gv (nw, 35); gq_in / gv_in
+ * (NULL, or cotangents of the same state, e.g. a step's outputs') are added to the result last. com gets none. */
+int dk_fwd_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com,
+                          const float* gqn, const float* gxpos, const float* gxquat, const float* gcvel,
+                          const float* gsc, const float* gq_in, const float* gv_in, float* gq, float* gv);
 /* Replaces <unit>_upload (jax_ffi.py:214-225): the model constants are compiled into this library, so the call only
  * checks that the current device can run the kernels; consts may be NULL. */
 int dk_fwd_upload(const float* consts, hipStream_t st);

@@ -12,6 +12,11 @@ size_t order_work_bytes(int nw);
 size_t forward_lds_bytes();
 size_t adjoint_lds_bytes();
 int prof_read(unsigned long long* out, int nw);
+int launch_kinematics(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com, float* qn,
+                      float* xpos, float* xquat, float* cvel, float* sc);
+int launch_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com,
+                          const float* gqn, const float* gxpos, const float* gxquat, const float* gcvel,
+                          const float* gsc, const float* gq_in, const float* gv_in, float* gq, float* gv);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work);
@@ -50,6 +55,19 @@ int dk_fwd_forward_ordered(hipStream_t st, int nw, const float* qpos, const floa
   if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0 || (nw > 0 && !work)) return (int)hipErrorInvalidValue;
   return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
                              const_cast<void*>(work), 2);
+}
+
+int dk_fwd_kinematics(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com, float* qn,
+                      float* xpos, float* xquat, float* cvel, float* sc) {
+  if (nw < 0) return (int)hipErrorInvalidValue;
+  return g1k::launch_kinematics(st, nw, qpos, qvel, com, qn, xpos, xquat, cvel, sc);
+}
+
+int dk_fwd_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com,
+                          const float* gqn, const float* gxpos, const float* gxquat, const float* gcvel,
+                          const float* gsc, const float* gq_in, const float* gv_in, float* gq, float* gv) {
+  if (nw < 0) return (int)hipErrorInvalidValue;
+  return g1k::launch_kinematics_vjp(st, nw, qpos, qvel, com, gqn, gxpos, gxquat, gcvel, gsc, gq_in, gv_in, gq, gv);
 }
 
 long long dk_fwd_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }

@@ -2,11 +2,17 @@
 ``nablaengine.torch_ffi``, ``src/nablaengine/torch_ffi.py``).
 
   step(qpos, qvel, warm, ctrl, friction, com, *, iterations=10, substeps=4, clamp_kv=0, normal=3, clamp_soft=None,
-       grad_decay=1.0, kinematics=False) -> (qpos', qvel', warm')
-  forward(qpos, qvel, warm, ctrl, friction, com, *, iterations=10, substeps=4, tape=False)
-       -> (qpos', qvel', warm', info[, tape])
-  backward(tape, friction, com, g_qpos, g_qvel, *, substeps=4, clamp_kv=0, normal=3, ctrl=None, clamp_soft=None)
-       -> (g_qpos, g_qvel, g_ctrl, info)
+       grad_decay=1.0, kinematics=False) -> (qpos', qvel', warm'[, qpos_n, xpos, xquat, cvel, subtree_com])
+  kinematics(qpos, qvel, com) -> (qpos_n, xpos, xquat, cvel, subtree_com)
+  forward(qpos, qvel, warm, ctrl, friction, com, *, iterations=10, substeps=4, tape=False, kinematics=False)
+       -> (qpos', qvel', warm', info[, tape][, the kinematics outputs])
+  backward(tape, friction, com, g_qpos, g_qvel, *, substeps=4, clamp_kv=0, normal=3, ctrl=None, clamp_soft=None,
+           kinematics=None) -> (g_qpos, g_qvel, g_ctrl, info)
+
+The kinematics outputs (reference g1_engine/kinematics.py:1-45, MJX kinematics + com_pos + com_vel) of a state:
+qpos_n (B, 36) qpos with the root quaternion normalized, xpos (B, 31, 3), xquat (B, 31, 4) the body frames, cvel
+(B, 31, 6) [angular; linear] twists at subtree_com[:, 1], subtree_com (B, 31, 3). step(..., kinematics=True) gives
+those of its output state, bitwise kinematics(qpos', qvel', com); their cotangents join the step's in its backward.
 
 Arguments: float32 tensors on one ROCm device, contiguous, leading dimension B (the worlds): qpos (B, 36), qvel (B, 35),
 warm (B, 35), ctrl (B, 29), friction (B,), com (B, 3). Other dtypes, devices or shapes raise TypeError; nothing is
@@ -67,6 +73,8 @@ def load_library(path=None):
         lib.dk_adjoint_work.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp]
         lib.dk_adjoint_work.restype = i32
         lib.dk_adjoint_work_bytes.argtypes, lib.dk_adjoint_work_bytes.restype = [i32], ctypes.c_longlong
+        lib.dk_fwd_kinematics.argtypes, lib.dk_fwd_kinematics.restype = [vp, i32] + [vp] * 8, i32
+        lib.dk_fwd_kinematics_vjp.argtypes, lib.dk_fwd_kinematics_vjp.restype = [vp, i32] + [vp] * 12, i32
         sizes = (ctypes.c_longlong * 9)()
         lib.dk_fwd_sizes(ctypes.cast(sizes, vp))
         _STATE["sizes"] = [int(x) for x in sizes]
@@ -152,7 +160,16 @@ class _OnDevice:
             torch.cuda.set_device(self.prev)
 
 
-def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape):
+def _kin_shapes(B):
+    return (B, NQ), (B, NBODY, 3), (B, NBODY, 4), (B, NBODY, 6), (B, NBODY, 3)
+
+
+def _kin_empty(B, device):
+    import torch
+    return [torch.empty(s, dtype=torch.float32, device=device) for s in _kin_shapes(B)]
+
+
+def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics=False):
     import torch
     if not isinstance(qpos, torch.Tensor):
         raise _err(f"qpos must be a torch.Tensor, got {type(qpos).__name__}")
@@ -173,8 +190,9 @@ def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, t
     info = torch.empty((B, 4), dtype=torch.int32, device=qpos.device)
     rw = _STATE["sizes"][2]
     tp = torch.empty((B if tape else 0, substeps * rw), **kw)
+    kin = _kin_empty(B, qpos.device) if kinematics else []
     if B == 0:
-        return [q1, v1, w1, info, tp]
+        return [q1, v1, w1, info, tp] + kin
     work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device=qpos.device)
     with _OnDevice(dev):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
@@ -182,10 +200,13 @@ def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, t
                                int(substeps), _ptr(q1), _ptr(v1), _ptr(w1), _ptr(info), None,
                                _ptr(tp) if tape else None, _ptr(work) if work.numel() else None),
             "the forward launch")
-    return [q1, v1, w1, info, tp]
+        if kinematics:  # the output state's kinematics (reference torch_ffi.py:488-489)
+            _rc(lib.dk_fwd_kinematics(st, B, _ptr(q1), _ptr(v1), _ptr(com), *map(_ptr, kin)), "the kinematics launch")
+    return [q1, v1, w1, info, tp] + kin
 
 
-def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal, clamp_soft):
+def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal, clamp_soft, kin_state=(),
+                   kin_cot=()):
     import torch
     if not isinstance(tape, torch.Tensor) or tape.device.type != "cuda":
         raise _err("tape must be a GPU torch.Tensor")
@@ -210,9 +231,21 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
     if B == 0:
         return [gq, gv, gu, info]
     lib = _STATE["lib"]
+    if kin_state:
+        q1, v1 = kin_state
+        _check("qpos'", q1, (B, NQ), dev)
+        _check("qvel'", v1, (B, NV), dev)
+        for name, x, shape in zip(("g_qpos_n", "g_xpos", "g_xquat", "g_cvel", "g_subtree_com"), kin_cot,
+                                  _kin_shapes(B)):
+            _check(name, x, shape, dev)
     work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
     with _OnDevice(dev):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        if kin_state:  # the kinematics outputs' cotangents pulled back onto (qpos', qvel'), theirs added last
+            cq, cv = torch.empty((B, NQ), **kw), torch.empty((B, NV), **kw)
+            _rc(lib.dk_fwd_kinematics_vjp(st, B, _ptr(q1), _ptr(v1), _ptr(com), *map(_ptr, kin_cot), _ptr(g_qpos),
+                                          _ptr(g_qvel), _ptr(cq), _ptr(cv)), "the kinematics VJP launch")
+            g_qpos, g_qvel = cq, cv
         _rc(lib.dk_adjoint_work(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos),
                                 _ptr(g_qvel), _ptr(gq), _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl),
                                 ctypes.c_float(0.0 if clamp_soft is None else clamp_soft), v[0], v[1],
@@ -221,34 +254,101 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
     return [gq, gv, gu, info]
 
 
+def _kinematics_impl(qpos, qvel, com):
+    import torch
+    if not isinstance(qpos, torch.Tensor) or qpos.device.type != "cuda":
+        raise _err("qpos must be a GPU torch.Tensor")
+    dev = qpos.device.index
+    B = qpos.shape[0] if qpos.dim() == 2 else -1
+    for name, x, shape in (("qpos", qpos, (B, NQ)), ("qvel", qvel, (B, NV)), ("com", com, (B, 3))):
+        _check(name, x, shape, dev)
+    if dev not in _READY:
+        init(dev)
+    out = _kin_empty(B, qpos.device)
+    if B:
+        with _OnDevice(dev):
+            st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+            _rc(_STATE["lib"].dk_fwd_kinematics(st, B, _ptr(qpos), _ptr(qvel), _ptr(com), *map(_ptr, out)),
+                "the kinematics launch")
+    return out
+
+
+def _kinematics_backward_impl(qpos, qvel, com, *cot):
+    import torch
+    dev = qpos.device.index
+    B = qpos.shape[0]
+    for name, x, shape in (("qpos", qpos, (B, NQ)), ("qvel", qvel, (B, NV)), ("com", com, (B, 3))):
+        _check(name, x, shape, dev)
+    for name, x, shape in zip(("g_qpos_n", "g_xpos", "g_xquat", "g_cvel", "g_subtree_com"), cot, _kin_shapes(B)):
+        _check(name, x, shape, dev)
+    kw = dict(dtype=torch.float32, device=qpos.device)
+    gq, gv = torch.empty((B, NQ), **kw), torch.empty((B, NV), **kw)
+    if B:
+        with _OnDevice(dev):
+            st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+            _rc(_STATE["lib"].dk_fwd_kinematics_vjp(st, B, _ptr(qpos), _ptr(qvel), _ptr(com), *map(_ptr, cot), None,
+                                                    None, _ptr(gq), _ptr(gv)), "the kinematics VJP launch")
+    return [gq, gv]
+
+
 def _make_step_fn():
     import torch
 
     class _Step(torch.autograd.Function):
-        """reference torch_ffi.py:747-779: the tape as the residual; gradients for qpos, qvel and ctrl only."""
+        """reference torch_ffi.py:747-779: the tape as the residual; gradients for qpos, qvel and ctrl only; with
+        kinematics the output state's kinematics outputs too, their cotangents pulled back onto (qpos', qvel') first."""
 
         @staticmethod
         def forward(ctx, qpos, qvel, warm, ctrl, friction, com, iterations, substeps, clamp_kv, normal, clamp_soft,
-                    grad_decay):
-            q1, v1, w1, info, tp = _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, True)
+                    grad_decay, kin):
+            r = _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, True, kin)
+            q1, v1, w1, info, tp = r[:5]
             ctx.save_for_backward(tp, friction, com, ctrl, q1, v1)
-            ctx.opts = (substeps, clamp_kv, normal, clamp_soft, grad_decay)
+            ctx.opts = (substeps, clamp_kv, normal, clamp_soft, grad_decay, kin)
             ctx.mark_non_differentiable(w1)
-            return q1, v1, w1
+            return (q1, v1, w1) + tuple(r[5:])
 
         @staticmethod
-        def backward(ctx, g_q1, g_v1, g_w1):
+        def backward(ctx, g_q1, g_v1, g_w1, *g_kin):
             tp, friction, com, ctrl, q1, v1 = ctx.saved_tensors
-            substeps, clamp_kv, normal, clamp_soft, grad_decay = ctx.opts
+            substeps, clamp_kv, normal, clamp_soft, grad_decay, kin = ctx.opts
             g_q1 = torch.zeros_like(q1) if g_q1 is None else g_q1.contiguous()
             g_v1 = torch.zeros_like(v1) if g_v1 is None else g_v1.contiguous()
+            ks, kc = (), ()
+            if kin and any(g is not None for g in g_kin):
+                ks = (q1, v1)
+                kc = tuple(torch.zeros(sh, dtype=torch.float32, device=q1.device) if g is None else g.contiguous()
+                           for g, sh in zip(g_kin, _kin_shapes(q1.shape[0])))
             gq, gv, gu, _ = _backward_impl(tp, friction, com, g_q1, g_v1, ctrl if clamp_kv == 2 else None, substeps,
-                                           clamp_kv, normal, clamp_soft)
+                                           clamp_kv, normal, clamp_soft, ks, kc)
             if grad_decay != 1.0:  # the state cotangent through this step times it, ctrl's not (float32 product)
                 gq, gv = gq * grad_decay, gv * grad_decay
-            return gq, gv, None, gu, None, None, None, None, None, None, None, None
+            return gq, gv, None, gu, None, None, None, None, None, None, None, None, None
 
     return _Step
+
+
+def _make_kin_fn():
+    import torch
+
+    class _Kin(torch.autograd.Function):
+        """reference torch_ffi.py:787-804: gradients for qpos and qvel, none for com."""
+
+        @staticmethod
+        def forward(ctx, qpos, qvel, com):
+            out = _kinematics_impl(qpos, qvel, com)
+            ctx.save_for_backward(qpos, qvel, com)
+            return tuple(out)
+
+        @staticmethod
+        def backward(ctx, *g):
+            qpos, qvel, com = ctx.saved_tensors
+            g = [torch.zeros(sh, dtype=torch.float32, device=qpos.device) if x is None else x.contiguous()
+                 for x, sh in zip(g, _kin_shapes(qpos.shape[0]))]
+            gq, gv = _kinematics_backward_impl(qpos, qvel, com, *g)
+            return gq, gv, None
+
+    return _Kin
 
 
 _FNS = {}
@@ -262,13 +362,12 @@ def _fn(name, make):
 
 def step(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, clamp_kv=CLAMP_KV,
          normal=NORMAL, clamp_soft=None, grad_decay=GRAD_DECAY, kinematics=False):
-    """One control step: (qpos', qvel', warm') (reference torch_ffi.py:817-835). Differentiable in qpos, qvel and ctrl
+    """One control step: (qpos', qvel', warm'); kinematics=True: (qpos', qvel', warm', qpos_n, xpos, xquat, cvel,
+    subtree_com), the output state's kinematics (reference torch_ffi.py:817-835). Differentiable in qpos, qvel and ctrl
     when any input requires grad (the forward then also writes the tape); warm' is not differentiable."""
     import torch
     if int(clamp_kv) not in (0, 1, 2) or int(normal) not in (0, 1, 2, 3):
         raise _err("clamp_kv in {0, 1, 2}, normal in 0..3", ValueError)
-    if kinematics:
-        raise _err("kinematics=True: the kinematics outputs are not in this build", ValueError)
     soft = _soft(clamp_kv, clamp_soft)
     gd = float(grad_decay)
     if not math.isfinite(gd):
@@ -276,27 +375,43 @@ def step(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, subste
     args = (qpos, qvel, warm, ctrl, friction, com)
     if torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in args):
         return _fn("step", _make_step_fn).apply(*args, int(iterations), int(substeps), int(clamp_kv), int(normal),
-                                                soft, gd)
-    r = _forward_impl(*args, int(iterations), int(substeps), False)
-    return tuple(r[:3])
+                                                soft, gd, bool(kinematics))
+    r = _forward_impl(*args, int(iterations), int(substeps), False, bool(kinematics))
+    return tuple(r[:3]) + tuple(r[5:])
 
 
-def forward(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, tape=False):
-    """One control step without autograd: (qpos', qvel', warm', info (B, 4) int32[, tape]) (reference
-    torch_ffi.py:845-851)."""
-    r = _forward_impl(qpos, qvel, warm, ctrl, friction, com, int(iterations), int(substeps), bool(tape))
-    return tuple(r[:4]) + ((r[4],) if tape else ())
+def kinematics(qpos, qvel, com):
+    """Differentiable kinematics outputs of states (qpos, qvel, com): (qpos_n, xpos, xquat, cvel, subtree_com)
+    (reference torch_ffi.py:838-842); gradients for qpos and qvel, none for com. kinematics(q', v', com) of a step's
+    output is bitwise step(..., kinematics=True)'s."""
+    import torch
+    if torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in (qpos, qvel, com)):
+        return _fn("kin", _make_kin_fn).apply(qpos, qvel, com)
+    return tuple(_kinematics_impl(qpos, qvel, com))
+
+
+def forward(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, tape=False,
+            kinematics=False):
+    """One control step without autograd: (qpos', qvel', warm', info (B, 4) int32[, tape][, the kinematics outputs])
+    (reference torch_ffi.py:845-851)."""
+    r = _forward_impl(qpos, qvel, warm, ctrl, friction, com, int(iterations), int(substeps), bool(tape),
+                      bool(kinematics))
+    return tuple(r[:4]) + ((r[4],) if tape else ()) + tuple(r[5:])
 
 
 def backward(tape, friction, com, g_qpos, g_qvel, *, substeps=SUBSTEPS, clamp_kv=CLAMP_KV, normal=NORMAL, ctrl=None,
-             clamp_soft=None):
+             clamp_soft=None, kinematics=None):
     """The adjoint of one control step from its tape: (g_qpos (B, 36), g_qvel (B, 35), g_ctrl (B, 29), info (B,))
-    (reference torch_ffi.py:854-865)."""
+    (reference torch_ffi.py:854-865); kinematics: None or (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel,
+    g_subtree_com), the cotangents of the output state's kinematics outputs, pulled back and added first."""
     soft = _soft(clamp_kv, clamp_soft)
     if soft is not None and ctrl is None:
         raise _err("clamp_kv=2 (the soft clamp) needs the step's ctrl", ValueError)
+    ks, kc = ((), ()) if kinematics is None else (tuple(kinematics[:2]), tuple(kinematics[2:]))
+    if kinematics is not None and len(kc) != 5:
+        raise _err("kinematics = (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com)", ValueError)
     return tuple(_backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl if soft is not None else None, int(substeps),
-                                int(clamp_kv), int(normal), soft))
+                                int(clamp_kv), int(normal), soft, ks, kc))
 
 
 def _make_scale_fn():

@@ -11,6 +11,12 @@ Parity status of each function (how it is pinned; the tests that pin it are name
   ``tests/test_oracle.py``.
 - ``contacts``: pinned by the step truth and by closed forms (sphere-plane depth, segment distance).
 - ``integrate_pos``, ``qpos_tangent``: closed forms (quaternion norm, round trip) in ``tests/test_oracle.py``.
+- ``kinematics``: the body poses against ``smooth``'s (pinned by the step truth) and the root's pose against qpos; cvel
+  against central differences of the poses along qvel (the twist is the poses' time derivative) and the kinetic
+  energy of the bodies computed from cvel against ``0.5 v' M v``; subtree_com through the gravity torques of
+  ``smooth`` (each joint's torque from the weight of its subtree at its subtree COM) in
+  ``tests/test_oracle_kinematics.py``.
+- ``kinematics_vjp``: central differences of ``kinematics`` (float64, h = 1e-6), brute force.
 """
 
 import ctypes
@@ -46,6 +52,7 @@ def lib():
                               ctypes.c_double, ctypes.c_int, dp, dp, ctypes.c_int, ctypes.c_int, ctypes.c_double, dp, dp,
                               dp]
         L.g1o_contacts.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp]
+        L.g1o_kinematics.argtypes = [ctypes.c_int] + [dp] * 8
         _lib = L
     return _lib
 
@@ -178,3 +185,37 @@ def qpos_tangent(qpos, g_qpos):
         dqk = 0.5 * quat_mul(q, np.broadcast_to(e, q.shape))
         out[..., 3 + k] = np.sum(g[..., 3:7] * dqk, -1)
     return out
+
+
+KIN_SHAPES = ((NQ,), (NB, 3), (NB, 4), (NB, 6), (NB, 3))  # qpos_n, xpos, xquat, cvel, subtree_com per world
+
+
+def kinematics(qpos, qvel, com):
+    """Kinematics outputs of states (B, 36), (B, 35), (B, 3): (qpos_n (B, 36), xpos (B, 31, 3), xquat (B, 31, 4),
+    cvel (B, 31, 6), subtree_com (B, 31, 3)), float64 (MJX kinematics + com_pos + com_vel semantics,
+    g1_engine/kinematics.py:1-45)."""
+    qpos = np.ascontiguousarray(np.asarray(qpos, np.float64).reshape(-1, NQ))
+    B = qpos.shape[0]
+    qvel, com = _c(qvel, (B, NV)), _c(com, (B, 3))
+    out = [np.empty((B,) + s) for s in KIN_SHAPES]
+    lib().g1o_kinematics(B, _p(qpos), _p(qvel), _p(com), *map(_p, out))
+    return tuple(out)
+
+
+def kinematics_vjp(qpos, qvel, com, cot, h=1e-6):
+    """VJP of ``kinematics`` by central differences (float64): cotangents cot = (g_qpos_n, g_xpos, g_xquat, g_cvel,
+    g_subtree_com) of one batch -> (g_qpos (B, 36), g_qvel (B, 35)); qpos's quaternion entries are perturbed
+    independently (the map normalizes them), as a VJP through MJX's normalization differentiates."""
+    qpos, qvel, com = _c(qpos, (-1, NQ)), _c(qvel, (-1, NV)), _c(com, (-1, 3))
+    B = qpos.shape[0]
+    cot = [np.asarray(c, np.float64).reshape((B,) + s) for c, s in zip(cot, KIN_SHAPES)]
+    gq, gv = np.zeros((B, NQ)), np.zeros((B, NV))
+    for which, g, n in ((0, gq, NQ), (1, gv, NV)):
+        for j in range(n):
+            x = [qpos.copy(), qvel.copy()]
+            x[which][:, j] += h
+            up = kinematics(x[0], x[1], com)
+            x[which][:, j] -= 2 * h
+            dn = kinematics(x[0], x[1], com)
+            g[:, j] = sum(((a - b) * c).reshape(B, -1).sum(1) for a, b, c in zip(up, dn, cot)) / (2 * h)
+    return gq, gv

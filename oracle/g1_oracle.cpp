@@ -1245,6 +1245,65 @@ int g1o_smooth(const double* qpos, const double* qvel, const double* ctrl, const
   return 0;
 }
 
+// Kinematics outputs of nw states (g1_engine/kinematics.py:1-45: MuJoCo MJX's kinematics + com_pos + com_vel, mujoco
+// 3.17 smooth.py), float64:
+//   qn    qpos with the free joint's quaternion normalized (smooth.py 49, 67-70);
+//   xpos, xquat (nw, NB, 3 / 4)  the body frames, world body 0 at the origin with the identity quaternion; the root
+//         from qpos; a hinge body from its parent as fwd_body composes it (hinge at the body origin, angle qpos);
+//   sc    (nw, NB, 3) subtree COMs: sum of m_b xipos_b over the subtree / its mass, xipos_b = xpos_b + R_b ipos_b
+//         (ipos of the torso + com); the world body's is body 1's (smooth.py 150-165);
+//   cvel  (nw, NB, 6) [angular; linear] twist of each body at the point sc[1] (body 0: zeros): angular W_b (world),
+//         linear V_b + W_b x (sc[1] - xpos_b), V_b the velocity of the body origin (smooth.py 415-457).
+int g1o_kinematics(int nw, const double* qpos, const double* qvel, const double* com, double* qn, double* xpos,
+                   double* xquat, double* cvel, double* sc) {
+  World* s = new World;
+  const double zero[NV] = {0};
+  for (int w = 0; w < nw; w++) {
+    std::memcpy(s->qpos, qpos + (size_t)w * NQ, sizeof(double) * NQ);
+    std::memcpy(s->qvel, qvel + (size_t)w * NV, sizeof(double) * NV);
+    std::memcpy(s->com, com + (size_t)w * 3, sizeof(double) * 3);
+    for (int b = 1; b < NB; b++) fwd_body(*s, b, zero);  // parents before children in the body order
+    double* o = qn + (size_t)w * NQ;
+    std::memcpy(o, s->qpos, sizeof(double) * NQ);
+    for (int k = 0; k < 4; k++) o[3 + k] = s->Q[1][k];
+    double* xp = xpos + (size_t)w * NB * 3;
+    double* xq = xquat + (size_t)w * NB * 4;
+    for (int k = 0; k < 3; k++) xp[k] = 0.0;
+    xq[0] = 1.0; xq[1] = xq[2] = xq[3] = 0.0;
+    for (int b = 1; b < NB; b++) {
+      for (int k = 0; k < 3; k++) xp[3 * b + k] = s->X[b][k];
+      for (int k = 0; k < 4; k++) xq[4 * b + k] = s->Q[b][k];
+    }
+    double ms[NB] = {0}, ws[NB][3] = {{0}};  // subtree mass and sum of m xipos, leaf to root
+    for (int b = NB - 1; b >= 1; b--) {
+      double ip[3], r[3];
+      body_ipos(*s, b, ip);
+      qrot(s->Q[b], ip, r);
+      ms[b] += BODY_MASS[b];
+      for (int k = 0; k < 3; k++) ws[b][k] += BODY_MASS[b] * (s->X[b][k] + r[k]);
+      const int p = BODY_PARENT[b];
+      if (p >= 1) {
+        ms[p] += ms[b];
+        for (int k = 0; k < 3; k++) ws[p][k] += ws[b][k];
+      }
+    }
+    double* c = sc + (size_t)w * NB * 3;
+    for (int b = 1; b < NB; b++)
+      for (int k = 0; k < 3; k++) c[3 * b + k] = ws[b][k] / ms[b];
+    for (int k = 0; k < 3; k++) c[k] = c[3 + k];
+    double* cv = cvel + (size_t)w * NB * 6;
+    for (int k = 0; k < 6; k++) cv[k] = 0.0;
+    for (int b = 1; b < NB; b++) {
+      double r[3], u[3];
+      for (int k = 0; k < 3; k++) r[k] = c[3 + k] - s->X[b][k];
+      cross(s->W[b], r, u);
+      for (int k = 0; k < 3; k++) { cv[6 * b + k] = s->W[b][k]; cv[6 * b + 3 + k] = s->V[b][k] + u[k]; }
+    }
+  }
+  delete s;
+  return 0;
+}
+
 // Contacts of one state (tests): returns the count kept (<= 64); per contact (pair, slot, dist, pos[3], frame[9]) as
 // 15 doubles in out.
 int g1o_contacts(const double* qpos, const double* qvel, const double* ctrl, const double* com, double fric,
