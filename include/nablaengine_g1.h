@@ -15,7 +15,8 @@ extern "C" {
  * out: oq (nw, 36), ov (nw, 35), ow (nw, 35) = the last substep's qacc, info (nw, 4) = (Newton iterations of the last
  * substep, contacts found, constraint rows, flags: 4 contacts beyond 64 dropped, 16 rows beyond 192 dropped);
  * ocon (nw, 64, 8) or NULL: the last substep's contacts (pair, dist, pos[3], normal[3]; pair -1 past the count);
- * tape (nw, nsub * DK_REC_WORDS) or NULL: the adjoint's record; work: dk_fwd_work_bytes(nw) bytes or NULL when 0. */
+ * tape (nw, nsub * DK_REC_WORDS) or NULL: the adjoint's record (its flags word as the reference's: 4 / 16
+ * overflow, 1 << 8 refactored at the final zones, 1 << 9 not converged, 1 << 10 near-singular self contact); work: dk_fwd_work_bytes(nw) bytes or NULL when 0. */
 int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
                    int* info, float* ocon, float* tape, void* work);
@@ -44,6 +45,16 @@ int dk_fwd_kinematics(hipStream_t st, int nw, const float* qpos, const float* qv
 int dk_fwd_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com,
                           const float* gqn, const float* gxpos, const float* gxquat, const float* gcvel,
                           const float* gsc, const float* gq_in, const float* gv_in, float* gq, float* gv);
+/* Replace dk_torch_diag_fwd / dk_torch_diag_bwd (torch_ffi.py:85-156, 146-155): the diagnostic counters, 18 uint64 in
+ * d (the caller's device array; order of torch_ffi.DIAG), added to after a forward (calls, worlds, worlds with info[3]
+ * bits, at the iteration cap, tape records and their REFACT / NONCONV / SINGULAR flags, contact / row overflow worlds)
+ * and after a backward (calls, rows, rows with non-finite gradients of qpos / qvel / ctrl or non-finite cotangents,
+ * replay mismatches). The backward's also ORs the non-finite bits (1 qpos, 2 qvel, 4 ctrl, 8 cotangent) << 16 into
+ * its info. */
+int dk_torch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, int iterations, const int* info,
+                      const float* tape);
+int dk_torch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float* gq, const float* gv, const float* gu,
+                      const float* cq, const float* cv, int* info);
 /* Replaces <unit>_upload (jax_ffi.py:214-225): the model constants are compiled into this library, so the call only
  * checks that the current device can run the kernels; consts may be NULL. */
 int dk_fwd_upload(const float* consts, hipStream_t st);
@@ -63,7 +74,8 @@ int dk_prof_read(unsigned long long* out, int nw);
 /* Replaces <variant>_adjoint (jax_ffi.py:228-241) for every (clamp_kv, normal) variant at once: the VJP of one control
  * step from its tape. in: tape (nw, nsub * DK_REC_WORDS), fric, com as the forward's, gq_out (nw, 36), gv_out (nw, 35)
  * the output cotangents, ctrl (nw, 29) (clamp_kv 2 only, else may be NULL), clamp_soft (clamp_kv 2); out: gq_in (nw, 36)
- * qpos-form, gv_in (nw, 35), gctrl (nw, 29), info (nw,) flags. */
+ * qpos-form, gv_in (nw, 35), gctrl (nw, 29), info (nw,): the union of the records' flags, 1 << 13 a replayed contact
+ * not found (the reference's ADJ_REPLAY_MISMATCH). */
 int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                const float* ctrl, float clamp_soft, int clamp_kv, int normal);

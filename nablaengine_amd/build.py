@@ -9,7 +9,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnablaengine_g1.so")
 PROF_LIB = os.path.join(HERE, "libnablaengine_g1_prof.so")
-SOURCES = ["g1_forward.hip", "g1_adjoint.hip", "g1_order.hip", "g1_kinematics.hip", "g1_capi.hip"]
+SOURCES = ["g1_forward.hip", "g1_adjoint.hip", "g1_order.hip", "g1_kinematics.hip", "g1_diag.hip", "g1_capi.hip"]
 ARCH = os.environ.get("NABLA_OFFLOAD_ARCH", "gfx950")
 # packed FP32 instructions off (-packed-fp32-ops): the kernels are written for scalar FP32. Warnings that mark
 # undefined behaviour the optimizer exploits (a non-void function falling off its end becomes unreachable code, and a

@@ -764,7 +764,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
   }
   wsync();
-  for (int k = nsub - 1; k >= 0; k--) adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
+  for (int k = nsub - 1; k >= 0; k--) {
+    if (lane == 0) s.flags |= (int)__float_as_uint(wt[(size_t)k * REC_WORDS + REC_FLAGS]);  // the records' flags
+    adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
+  }
   // gradients: qpos form (the quaternion's 2 q (x) (0, t)), qvel, ctrl
   float* oq = gq_in + (size_t)w * NQ;
   if (lane < 3) oq[lane] = s.qb[lane];

@@ -12,6 +12,10 @@ size_t order_work_bytes(int nw);
 size_t forward_lds_bytes();
 size_t adjoint_lds_bytes();
 int prof_read(unsigned long long* out, int nw);
+int launch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, int iterations, const int* info,
+                    const float* tape);
+int launch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float* gq, const float* gv, const float* gu,
+                    const float* cq, const float* cv, int* info);
 int launch_kinematics(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com, float* qn,
                       float* xpos, float* xquat, float* cvel, float* sc);
 int launch_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com,
@@ -68,6 +72,18 @@ int dk_fwd_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float
                           const float* gsc, const float* gq_in, const float* gv_in, float* gq, float* gv) {
   if (nw < 0) return (int)hipErrorInvalidValue;
   return g1k::launch_kinematics_vjp(st, nw, qpos, qvel, com, gqn, gxpos, gxquat, gcvel, gsc, gq_in, gv_in, gq, gv);
+}
+
+int dk_torch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, int iterations, const int* info,
+                      const float* tape) {
+  if (nw < 0 || nsub < 1 || !d) return (int)hipErrorInvalidValue;
+  return g1k::launch_diag_fwd(st, d, nw, nsub, iterations, info, tape);
+}
+
+int dk_torch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float* gq, const float* gv, const float* gu,
+                      const float* cq, const float* cv, int* info) {
+  if (nw < 0 || !d) return (int)hipErrorInvalidValue;
+  return g1k::launch_diag_bwd(st, d, nw, gq, gv, gu, cq, cv, info);
 }
 
 long long dk_fwd_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }

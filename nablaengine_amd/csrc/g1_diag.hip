@@ -1,0 +1,113 @@
+// Diagnostic counters of the forward and the backward (the reference's dk_torch_diag_fwd / dk_torch_diag_bwd,
+// torch_ffi.py:85-156): a caller-owned array of 18 uint64 counters per device, added to by one small kernel after each
+// forward / backward, in the reference's order (torch_ffi.py:56-59 DIAG):
+//   0 fwd_calls, 1 fwd_worlds, 2 fwd_unsupported_worlds (info[3] != 0), 3 fwd_iteration_limit_worlds (the last
+//   substep's iterations reached the cap), 4 tape_records, 5 refact_records, 6 nonconv_records, 7 singular_records (the
+//   records' flags), 8 bwd_calls, 9 bwd_rows, 10 nonfinite_rows (a non-finite gradient), 11-13 nonfinite_{qpos,qvel,
+//   ctrl}_rows, 14 nonfinite_cotangent_rows, 15 replay_mismatch_worlds, 16 fwd_contact_overflow_worlds,
+//   17 fwd_row_overflow_worlds.
+// The backward also writes the non-finite bits (1 qpos, 2 qvel, 4 ctrl, 8 cotangent) << 16 into its info. One thread per
+// world (grid-stride), a wave sum per count, one 64-bit atomic add per wave and count; integer counts only.
+#include "g1_device.h"
+#include "g1_tape.h"
+
+namespace g1k {
+
+enum {
+  D_FWD_CALLS = 0, D_FWD_WORLDS, D_FWD_UNSUPPORTED, D_FWD_ITER_LIMIT, D_TAPE_RECORDS, D_REFACT, D_NONCONV, D_SINGULAR,
+  D_BWD_CALLS, D_BWD_ROWS, D_NONFINITE, D_NONFINITE_QPOS, D_NONFINITE_QVEL, D_NONFINITE_CTRL, D_NONFINITE_COT,
+  D_REPLAY_MISMATCH, D_CONTACT_OVERFLOW, D_ROW_OVERFLOW, NDIAG
+};
+constexpr int NONFINITE_SHIFT = 16;
+constexpr int ADJ_REPLAY_MISMATCH = 1 << 13;
+
+__device__ __forceinline__ void diag_add(unsigned long long* d, int k, int v) {
+  const int t = wsumi(v);
+  if ((threadIdx.x & 63) == 0 && t) atomicAdd(&d[k], (unsigned long long)t);
+}
+
+__device__ __forceinline__ bool all_finite(const float* x, int n) {
+  bool ok = true;
+  for (int i = 0; i < n; i++) ok &= __builtin_isfinite(x[i]);
+  return ok;
+}
+
+__global__ __launch_bounds__(256) void k_diag_fwd(unsigned long long* d, int nw, int nsub, int iterations,
+                                                  const int* __restrict__ info, const float* __restrict__ tape) {
+  int unsup = 0, lim = 0, refact = 0, nonconv = 0, sing = 0, ocon = 0, orow = 0;
+  for (int w = blockIdx.x * blockDim.x + threadIdx.x; w < nw; w += gridDim.x * blockDim.x) {
+    const int f = info[4 * w + 3];
+    unsup += f != 0;
+    ocon += (f & 4) != 0;
+    orow += (f & 16) != 0;
+    lim += info[4 * w] >= iterations;
+    if (tape)
+      for (int k = 0; k < nsub; k++) {
+        const unsigned fl = __float_as_uint(tape[((size_t)w * nsub + k) * REC_WORDS + REC_FLAGS]);
+        refact += (fl & FLAG_REFACT) != 0;
+        nonconv += (fl & FLAG_NONCONV) != 0;
+        sing += (fl & FLAG_SINGULAR) != 0;
+      }
+  }
+  diag_add(d, D_FWD_UNSUPPORTED, unsup);
+  diag_add(d, D_FWD_ITER_LIMIT, lim);
+  diag_add(d, D_REFACT, refact);
+  diag_add(d, D_NONCONV, nonconv);
+  diag_add(d, D_SINGULAR, sing);
+  diag_add(d, D_CONTACT_OVERFLOW, ocon);
+  diag_add(d, D_ROW_OVERFLOW, orow);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    atomicAdd(&d[D_FWD_CALLS], 1ull);
+    atomicAdd(&d[D_FWD_WORLDS], (unsigned long long)nw);
+    if (tape) atomicAdd(&d[D_TAPE_RECORDS], (unsigned long long)nw * (unsigned long long)nsub);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_diag_bwd(unsigned long long* d, int nw, const float* __restrict__ gq,
+                                                  const float* __restrict__ gv, const float* __restrict__ gu,
+                                                  const float* __restrict__ cq, const float* __restrict__ cv,
+                                                  int* __restrict__ info) {
+  int rows = 0, rq = 0, rv = 0, ru = 0, rc = 0, rm = 0;
+  for (int w = blockIdx.x * blockDim.x + threadIdx.x; w < nw; w += gridDim.x * blockDim.x) {
+    const unsigned b = (all_finite(gq + (size_t)w * NQ, NQ) ? 0u : 1u) | (all_finite(gv + (size_t)w * NV, NV) ? 0u : 2u)
+                       | (all_finite(gu + (size_t)w * NU, NU) ? 0u : 4u)
+                       | (all_finite(cq + (size_t)w * NQ, NQ) && all_finite(cv + (size_t)w * NV, NV) ? 0u : 8u);
+    const int f = info[w];
+    info[w] = f | (int)(b << NONFINITE_SHIFT);
+    rows += (b & 7u) != 0;
+    rq += (b & 1u) != 0;
+    rv += (b & 2u) != 0;
+    ru += (b & 4u) != 0;
+    rc += (b & 8u) != 0;
+    rm += (f & ADJ_REPLAY_MISMATCH) != 0;
+  }
+  diag_add(d, D_NONFINITE, rows);
+  diag_add(d, D_NONFINITE_QPOS, rq);
+  diag_add(d, D_NONFINITE_QVEL, rv);
+  diag_add(d, D_NONFINITE_CTRL, ru);
+  diag_add(d, D_NONFINITE_COT, rc);
+  diag_add(d, D_REPLAY_MISMATCH, rm);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    atomicAdd(&d[D_BWD_CALLS], 1ull);
+    atomicAdd(&d[D_BWD_ROWS], (unsigned long long)nw);
+  }
+}
+
+static unsigned diag_grid(int nw) {
+  const int g = (nw + 255) / 256;
+  return (unsigned)(g < 1 ? 1 : g > 256 ? 256 : g);
+}
+
+int launch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, int iterations, const int* info,
+                    const float* tape) {
+  hipLaunchKernelGGL(k_diag_fwd, dim3(diag_grid(nw)), dim3(256), 0, st, d, nw, nsub, iterations, info, tape);
+  return (int)hipGetLastError();
+}
+
+int launch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float* gq, const float* gv, const float* gu,
+                    const float* cq, const float* cv, int* info) {
+  hipLaunchKernelGGL(k_diag_bwd, dim3(diag_grid(nw)), dim3(256), 0, st, d, nw, gq, gv, gu, cq, cv, info);
+  return (int)hipGetLastError();
+}
+
+}  // namespace g1k

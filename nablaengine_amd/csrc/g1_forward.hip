@@ -917,6 +917,17 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   }
   wsync();
   PROF(PH_ROWS);
+  // a self contact between nearly meeting geom centres / axes (its distance plus both radii: the centre or axis
+  // distance of the sphere / capsule primitives)
+  bool sing = false;
+  if (rec) {
+    float nu = 1e30f;
+    if (con && R.b1 != 0) {
+      const unsigned pw = cPairW[pair];
+      nu = dist + cGsize[3 * (pw & 255u)] + cGsize[3 * ((pw >> 8) & 255u)];
+    }
+    sing = ballot(nu < SINGULAR_NU) != 0ull;
+  }
   const NewtonOut no = newton(s, R, lane, con, iterations);
   PROF(PH_NINIT);
   if (lane == 0) s.niter = no.it;
@@ -941,7 +952,8 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
     if (lane == 0) {
       rec[REC_HDR] = __uint_as_float((unsigned)s.ncon | (unsigned)s.nefc << 8 | (unsigned)s.nlim << 16
                                      | (unsigned)min(no.it, 255) << 24);
-      rec[REC_FLAGS] = __uint_as_float((unsigned)(s.flags & 20) | (no.fresh ? 0u : (unsigned)FLAG_REFACT));
+      rec[REC_FLAGS] = __uint_as_float((unsigned)(s.flags & 20) | (no.fresh ? 0u : (unsigned)FLAG_REFACT)
+                                       | (no.conv ? 0u : (unsigned)FLAG_NONCONV) | (sing ? (unsigned)FLAG_SINGULAR : 0u));
     }
     wsync();
   }

@@ -5,7 +5,8 @@
 
 namespace g1k {
 constexpr int REC_HDR = 0;        // ncon | nefc << 8 | nlim << 16 | Newton iterations << 24
-constexpr int REC_FLAGS = 1;      // 4 contacts beyond capacity, 16 rows beyond capacity, 32 refactored at final zones
+constexpr int REC_FLAGS = 1;      // the reference's record flags (tape.py:20-23): 4 contacts beyond capacity, 16 rows
+                                  // beyond capacity, FLAG_REFACT, FLAG_NONCONV, FLAG_SINGULAR
 constexpr int REC_CLAMP = 2;      // 2 words: dofs whose actuator force is at its limit (bit i: dof i)
 constexpr int REC_LIMZONE = 4;    // 2 words: dofs whose limit row is in its quadratic zone at a*
 constexpr int REC_LIMROW = 6;     // 2 words: dofs with a limit row
@@ -19,5 +20,8 @@ constexpr int REC_LH = 200;       // 630: factor L of H = L' L = M + J'DJ at the
 constexpr int REC_LQ = 832;       // 630: factor L of M + h kv = L' L
 constexpr int REC_WORDS = 1472;
 constexpr unsigned TAPE_CON_NONE = 0xFFFFu;
-constexpr int FLAG_REFACT = 32;
+constexpr int FLAG_REFACT = 1 << 8;    // the zones changed after the last Newton factorization: H re-factored for the tape
+constexpr int FLAG_NONCONV = 1 << 9;   // the Newton iterations ran out before the stopping test held
+constexpr int FLAG_SINGULAR = 1 << 10; // a self contact whose geom centres / axes are nearer than SINGULAR_NU
+constexpr float SINGULAR_NU = 5e-3f;   // m
 }  // namespace g1k

@@ -24,7 +24,14 @@ with ctypes; every call goes to its C entries (include/nablaengine_g1.h) with to
 device pointers, the inputs' device made current. There is no fallback: without the library, or without a GPU, the
 calls raise. After init() the calls only launch kernels and allocate through torch's caching allocator (no host
 synchronization), so they can be captured in a HIP graph with fixed shapes.
+
+Diagnostics (reference torch_ffi.py:56-62, 664-742): per device 18 int64 counters (DIAG) added to on the device by one
+small kernel after each forward and backward (set_diagnostics(False) skips it), read with diagnostics() (the tensor)
+or read_diagnostics() (a dict; resets). The backward's info then also carries the non-finite bits (NONFINITE_* <<
+NONFINITE_SHIFT) besides the union of the records' flags and ADJ_REPLAY_MISMATCH. set_overflow_warnings(True) warns
+when worlds exceeded the contact or row capacity.
 """
+import atexit
 import ctypes
 import math
 import os
@@ -35,6 +42,14 @@ CLAMP_SOFT, GRAD_DECAY = 0.2, 1.0  # reference torch_ffi.py:55
 NQ, NV, NU, NBODY = 36, 35, 29, 31
 MAXCON = 64
 OVERFLOW_CONTACTS, OVERFLOW_ROWS = 4, 16  # forward info[:, 3] bits (reference torch_ffi.py:60)
+# the diagnostic counters, in the reference's order (torch_ffi.py:56-59); backward info's non-finite bits (61)
+DIAG = ("fwd_calls", "fwd_worlds", "fwd_unsupported_worlds", "fwd_iteration_limit_worlds", "tape_records",
+        "refact_records", "nonconv_records", "singular_records", "bwd_calls", "bwd_rows", "nonfinite_rows",
+        "nonfinite_qpos_rows", "nonfinite_qvel_rows", "nonfinite_ctrl_rows", "nonfinite_cotangent_rows",
+        "replay_mismatch_worlds", "fwd_contact_overflow_worlds", "fwd_row_overflow_worlds")
+NONFINITE_QPOS, NONFINITE_QVEL, NONFINITE_CTRL, NONFINITE_COT, NONFINITE_SHIFT = 1, 2, 4, 8, 16
+ADJ_REPLAY_MISMATCH = 1 << 13  # backward info: a replayed contact was not found
+TAPE_REFACT, TAPE_NONCONV, TAPE_SINGULAR = 1 << 8, 1 << 9, 1 << 10  # the records' flags (also in backward info)
 VARIANTS = tuple((kv, n) for kv in (0, 1, 2) for n in (0, 1, 2, 3))  # adjoint variants (clamp_kv, normal)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -43,6 +58,9 @@ LIB_PATH = os.path.join(HERE, "libnablaengine_g1.so")
 _LOCK = threading.Lock()
 _STATE = {}
 _READY = set()
+_DIAG = {}  # device index -> int64 (len(DIAG),) counters on that device
+_DIAG_ON = [True]  # set_diagnostics
+_OVERFLOW_WARN = [os.environ.get("DK_OVERFLOW_WARN", "0") not in ("", "0")]  # set_overflow_warnings
 
 
 def _err(msg, exc=TypeError):
@@ -74,6 +92,8 @@ def load_library(path=None):
         lib.dk_adjoint_work.restype = i32
         lib.dk_adjoint_work_bytes.argtypes, lib.dk_adjoint_work_bytes.restype = [i32], ctypes.c_longlong
         lib.dk_fwd_kinematics.argtypes, lib.dk_fwd_kinematics.restype = [vp, i32] + [vp] * 8, i32
+        lib.dk_torch_diag_fwd.argtypes, lib.dk_torch_diag_fwd.restype = [vp, vp, i32, i32, i32, vp, vp], i32
+        lib.dk_torch_diag_bwd.argtypes, lib.dk_torch_diag_bwd.restype = [vp, vp, i32] + [vp] * 6, i32
         lib.dk_fwd_kinematics_vjp.argtypes, lib.dk_fwd_kinematics_vjp.restype = [vp, i32] + [vp] * 12, i32
         sizes = (ctypes.c_longlong * 9)()
         lib.dk_fwd_sizes(ctypes.cast(sizes, vp))
@@ -102,6 +122,7 @@ def init(device=None):
             rc = lib.dk_fwd_upload(None, ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
         if rc:
             raise _err(f"device cuda:{dev} cannot run the kernels (code {rc})", RuntimeError)
+        _DIAG[dev] = torch.zeros(len(DIAG), dtype=torch.int64, device=f"cuda:{dev}")
         _READY.add(dev)
     return dict(path=LIB_PATH, sizes=list(_STATE["sizes"]))
 
@@ -202,6 +223,9 @@ def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, t
             "the forward launch")
         if kinematics:  # the output state's kinematics (reference torch_ffi.py:488-489)
             _rc(lib.dk_fwd_kinematics(st, B, _ptr(q1), _ptr(v1), _ptr(com), *map(_ptr, kin)), "the kinematics launch")
+        if _DIAG_ON[0]:
+            _rc(lib.dk_torch_diag_fwd(st, _ptr(_DIAG[dev]), B, int(substeps), int(iterations), _ptr(info),
+                                      _ptr(tp) if tape else None), "the forward diagnostics launch")
     return [q1, v1, w1, info, tp] + kin
 
 
@@ -251,6 +275,9 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
                                 ctypes.c_float(0.0 if clamp_soft is None else clamp_soft), v[0], v[1],
                                 _ptr(work) if work.numel() else None),
             "the adjoint launch")
+        if _DIAG_ON[0]:  # counters, and the non-finite bits into info (reference torch_ffi.py:538-540)
+            _rc(lib.dk_torch_diag_bwd(st, _ptr(_DIAG[dev]), B, _ptr(gq), _ptr(gv), _ptr(gu), _ptr(g_qpos), _ptr(g_qvel),
+                                      _ptr(info)), "the backward diagnostics launch")
     return [gq, gv, gu, info]
 
 
@@ -412,6 +439,80 @@ def backward(tape, friction, com, g_qpos, g_qvel, *, substeps=SUBSTEPS, clamp_kv
         raise _err("kinematics = (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com)", ValueError)
     return tuple(_backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl if soft is not None else None, int(substeps),
                                 int(clamp_kv), int(normal), soft, ks, kc))
+
+
+def set_diagnostics(enabled):
+    """Switch the device counters and the backward's non-finite bits on (the default) or off; returns the previous
+    setting (reference torch_ffi.py:678-686). One small kernel per forward and per backward; outputs and gradients are
+    the same either way."""
+    prev = _DIAG_ON[0]
+    _DIAG_ON[0] = bool(enabled)
+    return prev
+
+
+def _device_index(device):
+    import torch
+    if device is None:
+        return torch.cuda.current_device()
+    d = torch.device(device)
+    return torch.cuda.current_device() if d.index is None else d.index
+
+
+def diagnostics(device=None):
+    """The device's counters: an int64 (len(DIAG),) GPU tensor in DIAG order, added up by every call since init or the
+    last reset; not copied or synchronized (reference torch_ffi.py:689-695)."""
+    dev = _device_index(device)
+    if dev not in _READY:
+        init(dev)
+    return _DIAG[dev]
+
+
+def read_diagnostics(device=None, reset=True):
+    """The device's counters as {name: int} (synchronizes); reset=True zeroes them afterwards; with
+    set_overflow_warnings(True) it warns when worlds exceeded the contact or row capacity (reference
+    torch_ffi.py:698-708)."""
+    d = diagnostics(device)
+    out = dict(zip(DIAG, (int(x) for x in d.cpu())))
+    if reset:
+        d.zero_()
+    if _OVERFLOW_WARN[0]:
+        warn_overflow(out)
+    return out
+
+
+def warn_overflow(d, where="nablaengine_amd"):
+    """A RuntimeWarning when the counters d count worlds whose contacts (64) or constraint rows (192) exceeded the
+    per-world capacity: the extra ones were dropped, so those worlds miss support and friction forces; returns the
+    count (reference torch_ffi.py:711-724)."""
+    import warnings
+    nc, nr = d.get("fwd_contact_overflow_worlds", 0), d.get("fwd_row_overflow_worlds", 0)
+    if nc or nr:
+        warnings.warn(f"{where}: {nc} world-steps exceeded the contact capacity ({MAXCON} per world) and {nr} the "
+                      f"constraint-row capacity (192); their extra contacts / rows were dropped, so those worlds miss "
+                      f"support and friction forces (e.g. deep interpenetration)", RuntimeWarning, stacklevel=3)
+    return nc + nr
+
+
+def set_overflow_warnings(enabled):
+    """Switch the capacity-overflow warnings on or off (default off, or $DK_OVERFLOW_WARN=1); when on, the counts
+    nobody read are reported once more at exit. Returns the previous setting (reference torch_ffi.py:727-735)."""
+    prev = _OVERFLOW_WARN[0]
+    _OVERFLOW_WARN[0] = bool(enabled)
+    return prev
+
+
+def _exit_report():
+    """At exit: the overflow warning for each device's counts since the last read (no reset); never raises."""
+    try:
+        if not (_DIAG_ON[0] and _OVERFLOW_WARN[0]):
+            return
+        for dev in sorted(_DIAG):
+            warn_overflow(dict(zip(DIAG, (int(x) for x in _DIAG[dev].cpu()))), where=f"nablaengine_amd (cuda:{dev})")
+    except Exception:  # noqa: BLE001  (interpreter or the runtime shutting down)
+        pass
+
+
+atexit.register(_exit_report)
 
 
 def _make_scale_fn():

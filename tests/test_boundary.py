@@ -81,3 +81,18 @@ def test_python_surface_errors_without_gpu():
 def test_bench_refuses_several_gpus():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode != 0 and "one GPU" in r.stderr
+
+
+def test_diagnostics_names_and_overflow_warning():
+    """The counters' names and order are the reference's (torch_ffi.py:56-59); warn_overflow warns only when worlds
+    overflowed, and returns their count."""
+    import warnings
+    from nablaengine_amd import torch_ffi
+    assert len(torch_ffi.DIAG) == 18 and torch_ffi.DIAG[0] == "fwd_calls" and torch_ffi.DIAG[-1] == "fwd_row_overflow_worlds"
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        assert torch_ffi.warn_overflow(dict.fromkeys(torch_ffi.DIAG, 0)) == 0 and not w
+        assert torch_ffi.warn_overflow({"fwd_contact_overflow_worlds": 2, "fwd_row_overflow_worlds": 1}) == 3
+        assert len(w) == 1 and issubclass(w[0].category, RuntimeWarning)
+    assert torch_ffi.set_overflow_warnings(True) in (False, True)
+    assert torch_ffi.set_overflow_warnings(False) is True

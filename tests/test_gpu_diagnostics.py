@@ -1,0 +1,83 @@
+"""GPU diagnostics (reference torch_ffi.py:56-62, 85-156, 664-742): the device counters after a forward and a
+backward agree with what the outputs, info and the tape's flags say; the backward's info carries the union of the
+records' flags and the non-finite bits; set_diagnostics(False) leaves the counters and info alone."""
+import numpy as np
+import pytest
+
+from nablaengine_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+KEYS = ("qpos", "qvel", "warm", "ctrl", "friction", "com")
+
+
+@pytest.fixture(scope="module")
+def ffi():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible")
+    from nablaengine_amd import torch_ffi
+    torch_ffi.init(0)
+    return torch_ffi
+
+
+def _t(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+@pytest.mark.parametrize("config", [1, 4])
+def test_counters_match_outputs(ffi, config):
+    import torch
+    B = 1024
+    st = synthetic.states(B, config=config)
+    args = [_t(st[k]) for k in KEYS]
+    cq, cv = synthetic.cotangents(B)
+    ffi.set_diagnostics(True)
+    ffi.read_diagnostics(reset=True)
+    q1, v1, w1, info, tape = ffi.forward(*args, tape=True)
+    gq, gv, gu, binfo = ffi.backward(tape, args[4], args[5], _t(cq), _t(cv))
+    d = ffi.read_diagnostics()
+    info, binfo = info.cpu().numpy(), binfo.cpu().numpy()
+    flags = tape.view(torch.int32).cpu().numpy().reshape(B, 4, -1)[:, :, 1]
+    print(f"config {config}:", {k: v for k, v in d.items() if v})
+    assert d["fwd_calls"] == 1 and d["fwd_worlds"] == B and d["tape_records"] == 4 * B
+    assert d["fwd_unsupported_worlds"] == int((info[:, 3] != 0).sum())
+    assert d["fwd_iteration_limit_worlds"] == int((info[:, 0] >= ffi.ITERATIONS).sum())
+    assert d["fwd_contact_overflow_worlds"] == int((info[:, 3] & 4 != 0).sum())
+    assert d["fwd_row_overflow_worlds"] == int((info[:, 3] & 16 != 0).sum())
+    assert d["refact_records"] == int((flags & ffi.TAPE_REFACT != 0).sum())
+    assert d["nonconv_records"] == int((flags & ffi.TAPE_NONCONV != 0).sum())
+    assert d["singular_records"] == int((flags & ffi.TAPE_SINGULAR != 0).sum())
+    assert d["nonconv_records"] >= d["fwd_iteration_limit_worlds"] > 0  # the cap of 10 binds on some worlds
+    assert d["bwd_calls"] == 1 and d["bwd_rows"] == B and d["nonfinite_rows"] == 0
+    assert d["replay_mismatch_worlds"] == int((binfo & ffi.ADJ_REPLAY_MISMATCH != 0).sum()) == 0
+    # the backward's info: the union of the records' flags (no non-finite bits here)
+    union = np.bitwise_or.reduce(flags, axis=1)
+    assert np.array_equal(binfo & ~ffi.ADJ_REPLAY_MISMATCH, union)
+
+
+def test_nonfinite_bits_and_switch(ffi):
+    import torch
+    B = 256
+    st = synthetic.states(B, config=1)
+    args = [_t(st[k]) for k in KEYS]
+    cq, cv = synthetic.cotangents(B)
+    cv[5, 3] = np.nan
+    ffi.read_diagnostics(reset=True)
+    q1, v1, w1, info, tape = ffi.forward(*args, tape=True)
+    gq, gv, gu, binfo = ffi.backward(tape, args[4], args[5], _t(cq), _t(cv))
+    d = ffi.read_diagnostics()
+    nf = (binfo.cpu().numpy() >> ffi.NONFINITE_SHIFT) & 15
+    assert nf[5] & ffi.NONFINITE_COT and not np.delete(nf, 5).any()
+    assert d["nonfinite_cotangent_rows"] == 1 and d["nonfinite_rows"] == int((nf[5] & 7) != 0)
+    prev = ffi.set_diagnostics(False)
+    try:
+        gq2, gv2, gu2, binfo2 = ffi.backward(tape, args[4], args[5], _t(cq), _t(cv))
+        q2 = ffi.forward(*args)[0]
+        d2 = ffi.read_diagnostics()
+        assert not any(d2.values())  # nothing counted while off
+        assert not ((binfo2.cpu().numpy() >> ffi.NONFINITE_SHIFT) & 15).any()
+        assert torch.equal(q2, q1)
+        assert torch.equal(torch.nan_to_num(gq2), torch.nan_to_num(gq))
+    finally:
+        ffi.set_diagnostics(prev)
