@@ -1,0 +1,85 @@
+"""Drivers over the step (BASELINE configs 3 and 4; reference scripts/paper_bench/ours.py:1-13 for the Jacobian,
+torch_ffi.py module docstring for rollouts with torch.utils.checkpoint):
+
+  jacobian(qpos, qvel, warm, ctrl, friction, com, *, iterations, substeps, clamp_kv, normal, clamp_soft)
+      -> (J (B, 71, 99), info (B, 4)): the full step Jacobian per world, rows the outputs (qpos' in qpos form 36,
+         qvel' 35), columns the inputs (qpos tangent 35, qvel 35, ctrl 29), from one taped forward and 71 one-hot
+         VJPs on that tape (the reference's method);
+  rollout(qpos, qvel, warm, ctrls, friction, com, *, checkpoint_every=8, **step_kw) -> [(qpos_t, qvel_t)]: T steps
+      under autograd, each segment of checkpoint_every steps recomputed in the backward (torch.utils.checkpoint):
+      only the segment being differentiated holds its tapes.
+
+qpos tangent: a qpos-form cotangent g (36) of a state with root quaternion q maps to the tangent of
+integrate_pos(q, dq) at dq = 0 (position 3, the local rotation vector 3 as 1/2 vec(q* (x) g_q), hinges 29).
+"""
+from . import torch_ffi
+
+NOUT, NIN = torch_ffi.NQ + torch_ffi.NV, 2 * torch_ffi.NV + torch_ffi.NU  # 71 x 99
+
+
+def qpos_tangent(qpos, g):
+    """(B, 36) qpos-form cotangents -> (B, 35) tangent-form (integrate_pos's transpose at 0) at states qpos."""
+    import torch
+    q = qpos[:, 3:7] / qpos[:, 3:7].norm(dim=1, keepdim=True)
+    gq = g[:, 3:7]
+    # vec(conj(q) (x) gq): w = q0, v = -q[1:]; (w, v) (x) (s, u) = (w s - v.u, w u + s v + v x u)
+    w, v = q[:, :1], -q[:, 1:]
+    s, u = gq[:, :1], gq[:, 1:]
+    rot = 0.5 * (w * u + s * v + torch.cross(v, u, dim=1))
+    return torch.cat([g[:, :3], rot, g[:, 7:]], dim=1)
+
+
+def jacobian(qpos, qvel, warm, ctrl, friction, com, *, iterations=torch_ffi.ITERATIONS, substeps=torch_ffi.SUBSTEPS,
+             clamp_kv=torch_ffi.CLAMP_KV, normal=torch_ffi.NORMAL, clamp_soft=None):
+    """The step Jacobian of every world (B, 71, 99) float32 and the forward's info."""
+    import torch
+    q1, v1, w1, info, tape = torch_ffi.forward(qpos, qvel, warm, ctrl, friction, com, iterations=iterations,
+                                               substeps=substeps, tape=True)
+    B = qpos.shape[0]
+    kw = dict(dtype=torch.float32, device=qpos.device)
+    J = torch.empty((B, NOUT, NIN), **kw)
+    gq_out, gv_out = torch.zeros((B, torch_ffi.NQ), **kw), torch.zeros((B, torch_ffi.NV), **kw)
+    soft_ctrl = ctrl if int(clamp_kv) == 2 else None
+    for r in range(NOUT):
+        g = gq_out if r < torch_ffi.NQ else gv_out
+        c = r if r < torch_ffi.NQ else r - torch_ffi.NQ
+        g[:, c] = 1.0
+        gq, gv, gu, _ = torch_ffi.backward(tape, friction, com, gq_out, gv_out, substeps=substeps, clamp_kv=clamp_kv,
+                                           normal=normal, ctrl=soft_ctrl, clamp_soft=clamp_soft)
+        g[:, c] = 0.0
+        J[:, r, :torch_ffi.NV] = qpos_tangent(qpos, gq)
+        J[:, r, torch_ffi.NV:2 * torch_ffi.NV] = gv
+        J[:, r, 2 * torch_ffi.NV:] = gu
+    return J, info
+
+
+def rollout(qpos, qvel, warm, ctrls, friction, com, *, checkpoint_every=8, **step_kw):
+    """T = len(ctrls) differentiable steps from (qpos, qvel, warm) with the controls ctrls (T, B, 29): the states
+    [(qpos_t, qvel_t)] for t = 1..T. With checkpoint_every = k > 0 each segment of k steps runs once without keeping
+    its tapes and again in the backward (the forward is deterministic: the recomputed tapes are bitwise the first
+    ones); k = 0 keeps every tape."""
+    import torch
+    from torch.utils.checkpoint import checkpoint
+    T = len(ctrls)
+    out = []
+    q, v, w = qpos, qvel, warm
+
+    def segment(q, v, w, *us):
+        states = []
+        for u in us:
+            q, v, w = torch_ffi.step(q, v, w, u, friction, com, **step_kw)
+            states += [q, v]
+        return (w,) + tuple(states)
+
+    k = checkpoint_every if checkpoint_every and checkpoint_every > 0 else T
+    for t0 in range(0, T, k):
+        us = tuple(ctrls[t] for t in range(t0, min(T, t0 + k)))
+        if checkpoint_every:
+            r = checkpoint(segment, q, v, w, *us, use_reentrant=False)
+        else:
+            r = segment(q, v, w, *us)
+        w = r[0]
+        pairs = list(zip(r[1::2], r[2::2]))
+        out += pairs
+        q, v = pairs[-1]
+    return out

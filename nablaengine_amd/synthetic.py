@@ -51,3 +51,12 @@ def cotangents(n, seed=None, dtype=np.float32):
     """Output cotangents N(0, 1) over (n, 36), (n, 35) (config 2)."""
     rng = np.random.default_rng(SEED + 102 if seed is None else seed)
     return (rng.normal(0, 1, (n, 36)).astype(dtype), rng.normal(0, 1, (n, 35)).astype(dtype))
+
+
+def ctrl_sequence(T, n, seed=None, dtype=np.float32):
+    """A (T, n, 29) control sequence N(0, 0.2) around the home keyframe, clipped to ctrlrange (config 4)."""
+    m = model()
+    rng = np.random.default_rng(SEED + 104 if seed is None else seed)
+    home_u = np.asarray(m["key_home_ctrl"])
+    cr = np.asarray(m["ctrlrange"]).reshape(-1, 2)
+    return np.ascontiguousarray(np.clip(home_u + rng.normal(0.0, 0.2, (T, n, 29)), cr[:, 0], cr[:, 1]).astype(dtype))

@@ -39,7 +39,7 @@ def main():
                                 cot_qpos=c["cot_qpos"][gi], cot_qvel=c["cot_qvel"][gi],
                                 **{g: t["group_" + g] for g in ("G0", "G4", "G5", "G6")},
                                 **{k: c[k][gi] for k in INPUTS}, **extra,
-                                **{"jac_" + k: c[k][ji] for k in INPUTS})
+                                **{"jac_" + k: c[k][gi[ji]] for k in INPUTS})  # jac_index: positions into index
     m = np.load(os.path.join(REF, "fixtures", "mjlab", "mjw317_mf_s0.npz"))
     c = np.load(os.path.join(data, "mf_s0.npz"))
     n = 512
