@@ -1,13 +1,17 @@
 """Benchmark of the MI355X G1 control step (BASELINE.json metric): ms per 20 ms control step and world-steps/s, forward
 and forward+VJP, at 4096 worlds (and 16384), on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu] [--no-16k]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu] [--no-16k] [--no-configs]
 
 A step is one control step (4 substeps of 5 ms, Newton 10 iterations) of B worlds of BASELINE config 1 (seeded
 synthetic states, inputs resident in HBM before the timed region), exactly what torch_ffi.forward runs: the dispatch
 order pre-pass and the forward kernel. K steps are timed back to back between two synchronizations with HIP events on
 the launch stream; rank 0 prints one JSON line. Forward+VJP is the taped forward plus the adjoint (torch_ffi.forward
 (tape=True) + torch_ffi.backward), timed the same way.
+
+Also reported: config 3 (`config3_jacobian`: full 71 x 99 step Jacobians of the 4096 worlds from one taped forward
+and 71 VJPs, us per world-Jacobian) and config 4 (`config4_bptt`: a 32-step rollout of 16384 contact-heavy worlds with
+backprop through time, checkpoint segments of 8 steps, and its capped world-steps).
 
 `roofline` is the dominant kernel's, k_forward: algorithmic flops per launch (the float64 CPU restatement's
 closed-form phase counts on the same inputs, counted once before timing, per world-step x B) divided by k_forward's
@@ -126,6 +130,49 @@ def measure(B, steps, warmup, kernel=False):
     return ms, vjp_ms, kms, info
 
 
+def measure_jacobian(B, reps=2):
+    """ms per batch of B full step Jacobians (one taped forward + 71 VJPs on its tape) and us per
+    world-Jacobian."""
+    import torch
+    from nablaengine_amd import rollout, synthetic
+    st = synthetic.states(B, config=1)
+    args = [torch.from_numpy(st[k]).cuda() for k in KEYS]
+    ms = timed(lambda: rollout.jacobian(*args), reps, 1, torch.cuda.current_stream())
+    return {"worlds": B, "ms_per_batch": ms, "us_per_world_jacobian": 1e3 * ms / B,
+            "method": "1 taped forward + 71 one-hot VJPs on that tape (the reference's), rows qpos' (36) and qvel' "
+                      "(35), columns qpos tangent (35), qvel (35), ctrl (29)"}
+
+
+def measure_bptt(B, T=32, k=8):
+    """a T-step rollout of B contact-heavy worlds with backprop through time, segments of k steps
+    recomputed in the backward; ms per rollout (forward + backward) and the capped world-steps of its forward."""
+    import torch
+    from nablaengine_amd import rollout, synthetic, torch_ffi
+    st = synthetic.states(B, config=4)
+    us = torch.from_numpy(synthetic.ctrl_sequence(T, B)).cuda()
+    g = {k_: torch.from_numpy(st[k_]).cuda() for k_ in KEYS}
+
+    def run():
+        q = g["qpos"].clone().requires_grad_(True)
+        v = g["qvel"].clone().requires_grad_(True)
+        u = us.clone().requires_grad_(True)
+        states = rollout.rollout(q, v, g["warm"], u, g["friction"], g["com"], checkpoint_every=k)
+        loss = sum((qt[:, 2] ** 2).sum() + 0.01 * (vt ** 2).sum() for qt, vt in states)
+        loss.backward()
+    ms = timed(run, 1, 1, torch.cuda.current_stream())
+    # the capped world-steps of the rollout's forward (info[:, 3] & (4 | 16)), from a forward-only pass
+    q, v, w = g["qpos"], g["qvel"], g["warm"]
+    capped = contacts_max = rows_max = 0
+    for t in range(T):
+        q, v, w, info = torch_ffi.forward(q, v, w, us[t], g["friction"], g["com"])
+        i = info.cpu().numpy()
+        capped += int(((i[:, 3] & 20) != 0).sum())
+        contacts_max, rows_max = max(contacts_max, int(i[:, 1].max())), max(rows_max, int(i[:, 2].max()))
+    return {"worlds": B, "steps": T, "checkpoint_every": k, "ms_per_rollout_fwd_bwd": ms,
+            "world_steps_per_s_fwd_bwd": B * T * 1e3 / ms, "capped_world_steps": capped,
+            "contacts_max": contacts_max, "rows_max": rows_max}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,6 +181,7 @@ def main():
     ap.add_argument("--worlds", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-16k", action="store_true", help="skip the 16384-world forward and fwd+VJP lines")
+    ap.add_argument("--no-configs", action="store_true", help="skip the config 3 (Jacobian) and 4 (BPTT) lines")
     ap.add_argument("--flop-sample", type=int, default=512, help="worlds the flop count is taken on")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="before the timed steps, copy a buffer of this many MiB 3 times (a kernel of known HBM "
@@ -188,6 +236,9 @@ def main():
     }
     if big:
         res["worlds_16384"] = big
+    if not a.no_configs:
+        res["config3_jacobian"] = measure_jacobian(B)
+        res["config4_bptt"] = measure_bptt(16384)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res))
