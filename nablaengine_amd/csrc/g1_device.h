@@ -235,7 +235,7 @@ __device__ __forceinline__ float dot3(const float* a, const float* b) { return a
 // triangle in registers (c[m] = A[m][j], m >= j), so row k's entries L[k][j] are lane-local and L[k][m] is one
 // v_readlane away: step k is one pivot and, per ancestor m of k, a broadcast and one FMA on every lane.
 // SPARSE = false visits every m < k (the dense factor of a matrix with cross-branch entries). In place in Lp (packed
-// lower, TRI layout). Lane j's registers c[m] for m < j hold other entries of the matrix (loaded from in-bounds
+// lower, TRI layout, followed by the 64-float sink at LSINK). Lane j's registers c[m] for m < j hold other entries of the matrix (loaded from in-bounds
 // addresses, not zeroed): they are updated from one another only, never broadcast (a broadcast reads lane m's c[k],
 // k > m) and never stored, so the valid entries do not depend on them.
 template <bool SPARSE>
@@ -261,9 +261,9 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
     for (int m = 0; m < k; m++)
       if (!SPARSE || ((TREE.dofanc[k] >> m) & 1ull)) c[m] = fmaf(-c[k], bc[m], c[m]);  // A[m][j] -= L[k][j] L[k][m]
   }
+  // lane j stores column j's entries m >= j; the other lanes store into their sink slot (no branch per store)
 #pragma unroll
-  for (int m = 0; m < NV; m++)
-    if (m >= lane && lane < NV) Lp[tri(m, lane)] = c[m];
+  for (int m = 0; m < NV; m++) Lp[m >= lane && lane < NV ? tri(m, lane) : LSINK + lane] = c[m];
 }
 
 // x = A^-1 b for A = L' L (ltl_factor), b and x on lane i < NV: L' y = b leaf-first (reads row i of L: lane k takes

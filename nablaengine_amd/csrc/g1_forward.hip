@@ -79,7 +79,7 @@ __device__ __forceinline__ void m_to_L(Sim& s, int lane, float dg) {
       bool on;
       const int j = chain_dof(ch, t, &on);
       const float m = s.M[lane][j] + (j == lane ? dd : 0.f);
-      if (on && j <= lane) s.L[tri(lane, j)] = m;
+      s.L[on && j <= lane ? tri(lane, j) : LSINK + lane] = m;
     }
   }
   wsync();
@@ -239,7 +239,9 @@ __device__ void smooth(Sim& s, int lane) {
       const int j = chain_dof(ch, t, &on);
       const float mij = s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
                         + s.S[j][6] * f[2] + (j == lane ? arm : 0.f);
-      if (on && j <= lane) { s.M[lane][j] = mij; s.M[j][lane] = mij; }
+      const bool st = on && j <= lane;  // else both stores go to the row's unused column 35 (no branch)
+      s.M[lane][st ? j : MSTRIDE - 1] = mij;
+      s.M[st ? j : lane][st ? lane : MSTRIDE - 1] = mij;
     }
     float act = 0.f;
     if (lane >= 6) {
@@ -382,7 +384,7 @@ __device__ __forceinline__ void body_vel(Sim& s, const float* v, int lane) {
     for (int t = 0; t < MAXCHAIN; t++) {
       bool on;
       const int d = chain_dof(ch, t, &on);
-      const float vd = on ? v[d] : 0.f;
+      const float vd = v[d] * (on ? 1.f : 0.f);  // d is a valid dof past the chain's end: every load unconditional
       for (int k = 0; k < 3; k++) { w[k] = fmaf(s.S[d][k], vd, w[k]); u[k] = fmaf(s.S[d][4 + k], vd, u[k]); }
     }
     for (int k = 0; k < 3; k++) { s.u.nt.bw[lane][k] = w[k]; s.u.nt.bw[lane][4 + k] = u[k]; }
@@ -602,8 +604,7 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
                                 + s.S[j][5] * f[1] + s.S[j][6] * f[2]);
       }
 #pragma unroll
-      for (int e = 0; e < 8; e++)
-        if (hon[e]) s.L[ha[e]] = hv[e];
+      for (int e = 0; e < 8; e++) s.L[hon[e] ? ha[e] : LSINK + lane] = hv[e];
     }
     if (R.lsg != 0.f && R.ljar < 0.f) s.L[tri(lane, lane)] += R.lD;
   }
@@ -661,7 +662,7 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             const int i = 16 * ti + 4 * lk + e, j = 16 * tj + lr;
-            if (i < NV && j <= i) s.L[tri(i, j)] += acc[e];
+            s.L[i < NV && j <= i ? tri(i, j) : LSINK + lane] += acc[e];  // off the triangle: the lane's sink
           }
         }
       }

@@ -10,6 +10,8 @@ namespace g1t {
 using namespace g1;
 constexpr int NB = NBODY;
 constexpr int NTRI = NV * (NV + 1) / 2;
+constexpr int LSINK = NTRI + 2;  // a packed factor buffer's per-lane sink (64 floats after the matrix and its padding):
+                                 // lanes without an entry to store write there instead of branching around the store
 constexpr int MAXCON = 64;     // contact capacity per world (step.py:70-79 maxcon for 502 pairs)
 constexpr int NEFC = 192;      // constraint row capacity (step.py:43)
 constexpr int MAXCHAIN = 16;   // dofs on a body's chain: root 6 + at most 10 hinges (waist 3 + arm 7)
