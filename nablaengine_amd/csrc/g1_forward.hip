@@ -293,23 +293,19 @@ __device__ void collision(Sim& s, int lane) {
     zaxis(q0, fn);
   }
   int ncand = 0;
-  for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {
+  for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {  // branch-free: both tests, clamped pair index, sink store
     const int pr = lane + WL * k;
-    bool keep = false;
-    if (pr < NPAIR) {
-      const unsigned w = cPairW[pr];
-      const int g1 = w & 255u, g2 = (w >> 8) & 255u;
-      float dif[3] = {s.u.col.gx[g2][0] - s.u.col.gx[g1][0], s.u.col.gx[g2][1] - s.u.col.gx[g1][1],
-                      s.u.col.gx[g2][2] - s.u.col.gx[g1][2]};
-      const unsigned cls = (w >> 21) & 7u;
-      if (cls == 0u || cls == 4u) keep = dot3(dif, fn) <= cGrb[g2] * (1.f + 1e-5f) + 1e-6f;
-      else {
-        float rb = cGrb[g1] + cGrb[g2];
-        keep = dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f;
-      }
-    }
+    const unsigned w = cPairW[pr < NPAIR ? pr : NPAIR - 1];
+    const int g1 = w & 255u, g2 = (w >> 8) & 255u;
+    const float dif[3] = {s.u.col.gx[g2][0] - s.u.col.gx[g1][0], s.u.col.gx[g2][1] - s.u.col.gx[g1][1],
+                          s.u.col.gx[g2][2] - s.u.col.gx[g1][2]};
+    const unsigned cls = (w >> 21) & 7u;
+    const float r1 = cGrb[g1], r2 = cGrb[g2], rb = r1 + r2;
+    const bool plane = cls == 0u || cls == 4u;
+    const bool keep = pr < NPAIR && (plane ? dot3(dif, fn) <= r2 * (1.f + 1e-5f) + 1e-6f
+                                           : dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f);
     const unsigned long long bal = ballot(keep);
-    if (keep) s.u.col.cand[ncand + prefix_count(bal, lane)] = (unsigned short)pr;
+    s.u.col.cand[keep ? ncand + prefix_count(bal, lane) : NPAIR + 1] = (unsigned short)pr;  // else the spare slot
     ncand += __popcll(bal);
   }
   wsync();
@@ -494,9 +490,10 @@ __device__ __forceinline__ float lane_cost(const Sim& s, const Rows& R, int lane
   return g;
 }
 
-// Ma = M qacc and jar = J qacc - aref
-__device__ void refresh(Sim& s, Rows& R, int lane, bool con) {
-  float ma = matvec(s, s.qacc, lane);
+// Ma = M qacc and jar = J qacc - aref; at qacc = qacc_smooth (smooth), M qacc is qfrc_smooth (qacc_smooth solves
+// M qacc_smooth = qfrc_smooth), taken as it is
+__device__ void refresh(Sim& s, Rows& R, int lane, bool con, bool smooth = false) {
+  const float ma = smooth ? (lane < NV ? s.qsm[lane] : 0.f) : matvec(s, s.qacc, lane);
   if (lane < NV) s.Ma[lane] = ma;
   float jv[4], ljv;
   rows_jv(s, R, s.qacc, lane, con, jv, &ljv);
@@ -682,7 +679,7 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
   for (int t = 0; t < 4; t++) wj[t] = R.jar[t];
   if (lane < NV) s.qacc[lane] = s.qacc0[lane];
   wsync();
-  refresh(s, R, lane, con);
+  refresh(s, R, lane, con, true);
   const float cost0 = wsum(lane_cost(s, R, lane));
   if (cost0 > cost) {
     if (lane < NV) { s.qacc[lane] = wq; s.Ma[lane] = wma; }
