@@ -103,17 +103,17 @@ static_assert(sizeof(Adj) <= 20480, "Adj outgrew the LDS of 8 worlds per CU");
 __device__ __forceinline__ void imp_d(const float* solimp, float pos, float* imp, float* dimp) {
   const float dmin = fminf(fmaxf(solimp[0], 1e-4f), 0.9999f), dmax = fminf(fmaxf(solimp[1], 1e-4f), 0.9999f);
   const float width = fmaxf(1e-15f, solimp[2]), mid = fminf(fmaxf(solimp[3], 1e-4f), 0.9999f);
-  const float x = fabsf(pos) / width, sg = pos < 0.f ? -1.f : 1.f;
+  const float iwd = 1.f / width, x = fabsf(pos) * iwd, sg = pos < 0.f ? -1.f : 1.f;
   *dimp = 0.f;
   if (x <= 0.f) { *imp = dmin; return; }
   if (x >= 1.f) { *imp = dmax; return; }
   float y, dy;
-  if (x <= mid) { y = x * x / mid; dy = 2.f * x / mid; }
-  else { y = 1.f - (1.f - x) * (1.f - x) / (1.f - mid); dy = 2.f * (1.f - x) / (1.f - mid); }
+  if (x <= mid) { const float im = 1.f / mid; y = x * x * im; dy = 2.f * x * im; }
+  else { const float im = 1.f / (1.f - mid); y = 1.f - (1.f - x) * (1.f - x) * im; dy = 2.f * (1.f - x) * im; }
   const float v = dmin + y * (dmax - dmin);
   if (v < dmin || v > dmax) { *imp = fminf(fmaxf(v, dmin), dmax); return; }
   *imp = v;
-  *dimp = dy * (dmax - dmin) * sg / width;
+  *dimp = dy * (dmax - dmin) * sg * iwd;
 }
 __device__ __forceinline__ void kb_consts(const float* solref, const float* solimp, float* k, float* b) {
   const float tc = fmaxf(solref[0], 2.f * kH), dr = solref[1];
@@ -145,14 +145,15 @@ __device__ __forceinline__ void make_frame_vjp(const float* n, const float* frb,
   for (int k = 0; k < 3; k++) b0[k] = e[k] - n[k] * ne;
   const float bl = sqrtf(dot3(b0, b0));
   float b[3], bbar[3], t[3];
-  for (int k = 0; k < 3; k++) b[k] = b0[k] / bl;
+  const float ibl = 1.f / bl;
+  for (int k = 0; k < 3; k++) b[k] = b0[k] * ibl;
   cross(b, frb + 6, t);
   for (int k = 0; k < 3; k++) nb[k] += frb[k] + t[k];
   cross(frb + 6, n, t);
   for (int k = 0; k < 3; k++) bbar[k] = frb[3 + k] + t[k];
   const float bb = dot3(b, bbar);
   float b0b[3];
-  for (int k = 0; k < 3; k++) b0b[k] = (bbar[k] - b[k] * bb) / bl;
+  for (int k = 0; k < 3; k++) b0b[k] = (bbar[k] - b[k] * bb) * ibl;
   const float nb0 = dot3(n, b0b);
   for (int k = 0; k < 3; k++) nb[k] += -ne * b0b[k] - nb0 * e[k];
 }
@@ -166,7 +167,8 @@ __device__ __forceinline__ void sphere_core_vjp(const float* p1, float r1, const
   for (int k = 0; k < 3; k++) { p1b[k] += posb[k]; dlb[k] = 0.5f * posb[k]; }
   if (l > 0.f) {
     float n[3], nt[3];
-    for (int k = 0; k < 3; k++) { n[k] = dl[k] / l; nt[k] = nb[k] + 0.5f * (r1 - r2) * posb[k]; }
+    const float il = 1.f / l;
+    for (int k = 0; k < 3; k++) { n[k] = dl[k] * il; nt[k] = nb[k] + 0.5f * (r1 - r2) * posb[k]; }
     const float nn = dot3(n, nt), kap = kappa(l, normal);
     for (int k = 0; k < 3; k++) dlb[k] += kap * (nt[k] - n[k] * nn) + n[k] * db;
   }
@@ -203,12 +205,13 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
       const float bn = sqrtf(dot3(b0, b0));
       if (bn >= 0.5f) {
         float b[3], bbar[3], t[3];
-        for (int k = 0; k < 3; k++) b[k] = b0[k] / bn;
+        const float ibn = 1.f / bn;
+        for (int k = 0; k < 3; k++) b[k] = b0[k] * ibn;
         cross(frb + 6, n, t);
         for (int k = 0; k < 3; k++) bbar[k] = frb[3 + k] + t[k];
         const float bb = dot3(b, bbar);
         float b0b[3];
-        for (int k = 0; k < 3; k++) b0b[k] = (bbar[k] - b[k] * bb) / bn;
+        for (int k = 0; k < 3; k++) b0b[k] = (bbar[k] - b[k] * bb) * ibn;
         const float nb0 = dot3(n, b0b);
         for (int k = 0; k < 3; k++) axb[k] += b0b[k] - n[k] * nb0;
       }
@@ -232,11 +235,13 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
     const float tb = dot3(ptb, ab);
     float abb[3], apb[3] = {0.f, 0.f, 0.f}, aab[3], axb[3];
     for (int k = 0; k < 3; k++) { abb[k] = t * ptb[k]; aab[k] = ptb[k]; }
-    if (raw > 0.f && raw < 1.f)
+    if (raw > 0.f && raw < 1.f) {
+      const float ig = tb / gam;
       for (int k = 0; k < 3; k++) {
-        apb[k] = tb * ab[k] / gam;
-        abb[k] += tb * ap[k] / gam - tb * raw / gam * 2.f * ab[k];
+        apb[k] = ig * ab[k];
+        abb[k] += ig * ap[k] - ig * raw * 2.f * ab[k];
       }
+    }
     for (int k = 0; k < 3; k++) { x1b[k] += apb[k]; aab[k] -= apb[k]; }
     for (int k = 0; k < 3; k++) { x2b[k] += aab[k]; axb[k] = -h2 * aab[k] + 2.f * h2 * abb[k]; }
     cross(axis, axb, t2b);
@@ -251,9 +256,10 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
   const float det = ma * mc - mb * mb;
   float x1, x2;
   int mode;  // 0 both free, 1 x2 free (x1 fixed), 2 x1 free (x2 fixed), 3 both fixed
+  const float idet = 1.f / det;  // used only where |det| >= 1e-15 (the forward's capcap: the same products)
   if (fabsf(det) >= 1e-15f) {
-    x1 = (mc * u - mb * v) / det;
-    x2 = (ma * v - mb * u) / det;
+    x1 = (mc * u - mb * v) * idet;
+    x2 = (ma * v - mb * u) * idet;
     mode = 0;
     if (x1 > 1.f) { x1 = 1.f; x2 = (v - mb) / mc; mode = 1; }
     else if (x1 < -1.f) { x1 = -1.f; x2 = (v + mb) / mc; mode = 1; }
@@ -288,14 +294,16 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
   }
   float mab = 0.f, mbb = 0.f, mcb = 0.f, ub = 0.f, vb = 0.f;
   if (mode == 0) {
-    const float N1b = x1bar / det, N2b = x2bar / det, detb = -x1bar * x1 / det - x2bar * x2 / det;
+    const float N1b = x1bar * idet, N2b = x2bar * idet, detb = -(x1bar * x1 + x2bar * x2) * idet;
     mcb += N1b * u; ub += N1b * mc; mbb -= N1b * v; vb -= N1b * mb;
     mab += N2b * v; vb += N2b * ma; mbb -= N2b * u; ub -= N2b * mb;
     mab += detb * mc; mcb += detb * ma; mbb -= 2.f * mb * detb;
   } else if (mode == 1) {
-    vb += x2bar / mc; mbb -= x2bar * x1 / mc; mcb -= x2bar * x2 / mc;
+    const float g = x2bar / mc;
+    vb += g; mbb -= g * x1; mcb -= g * x2;
   } else if (mode == 2) {
-    ub += x1bar / ma; mbb -= x1bar * x2 / ma; mab -= x1bar * x1 / ma;
+    const float g = x1bar / ma;
+    ub += g; mbb -= g * x2; mab -= g * x1;
   }
   float dbv[3];
   for (int k = 0; k < 3; k++) {
@@ -441,7 +449,8 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     if (th > 0.f) {
       float sn, cs;
       sincosf(0.5f * th, &sn, &cs);
-      dq[0] = cs; dq[1] = sn * phi[0] / th; dq[2] = sn * phi[1] / th; dq[3] = sn * phi[2] / th;
+      const float st = sn / th;
+      dq[0] = cs; dq[1] = st * phi[0]; dq[2] = st * phi[1]; dq[3] = st * phi[2];
     }
     float rt[3];
     qrot(dq, t, rt);  // t = R(dq) t'
@@ -449,7 +458,11 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     // J_r(phi)' t' = t' + c1 phi x t' + c2 phi x (phi x t')
     float c1, c2;
     if (th < 1e-2f) { c1 = 0.5f - th * th / 24.f; c2 = 1.f / 6.f - th * th / 120.f; }
-    else { c1 = (1.f - cosf(th)) / (th * th); c2 = (th - sinf(th)) / (th * th * th); }
+    else {
+      const float i2 = 1.f / (th * th);
+      c1 = (1.f - cosf(th)) * i2;
+      c2 = (th - sinf(th)) * i2 / th;
+    }
     float pt[3], ppt[3];
     cross(phi, t, pt);
     cross(phi, pt, ppt);
@@ -750,7 +763,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     if (nw > 0.f) {
       float sa, ca, o[4];
       sincosf(0.5f * kH * nw, &sa, &ca);
-      const float dq[4] = {ca, sa * wv[0] / nw, sa * wv[1] / nw, sa * wv[2] / nw};
+      const float sw = sa / nw;
+      const float dq[4] = {ca, sw * wv[0], sw * wv[1], sw * wv[2]};
       qmul(q, dq, o);
       const float on = rsqrtf(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
       for (int k = 0; k < 4; k++) q[k] = o[k] * on;

@@ -15,7 +15,10 @@ __device__ __forceinline__ void make_frame(const float* n, float* fr) {
   float d = dot3(n, b);
   for (int k = 0; k < 3; k++) b[k] -= n[k] * d;
   float bn = sqrtf(dot3(b, b));
-  if (bn > 0.f) for (int k = 0; k < 3; k++) b[k] /= bn;
+  if (bn > 0.f) {
+    const float ib = 1.f / bn;  // one division, three products
+    for (int k = 0; k < 3; k++) b[k] *= ib;
+  }
   float c[3];
   cross(n, b, c);
   for (int k = 0; k < 3; k++) { fr[k] = n[k]; fr[3 + k] = b[k]; fr[6 + k] = c[k]; }
@@ -25,7 +28,10 @@ __device__ __forceinline__ void sphere_sphere(const float* p1, float r1, const f
                                               float* pos, float* n) {
   float dir[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
   float d = sqrtf(dot3(dir, dir));
-  if (d == 0.f) { n[0] = 1.f; n[1] = 0.f; n[2] = 0.f; } else { for (int k = 0; k < 3; k++) n[k] = dir[k] / d; }
+  if (d == 0.f) { n[0] = 1.f; n[1] = 0.f; n[2] = 0.f; } else {
+    const float id = 1.f / d;
+    for (int k = 0; k < 3; k++) n[k] = dir[k] * id;
+  }
   *dist = d - (r1 + r2);
   float hp = 0.5f * *dist + r1;
   for (int k = 0; k < 3; k++) pos[k] = p1[k] + n[k] * hp;
@@ -83,7 +89,10 @@ __device__ void collide_pair(const float (*gx)[4], const float (*gq)[4], int pr,
       float na = dot3(n, axis), b[3];
       for (int k = 0; k < 3; k++) b[k] = axis[k] - n[k] * na;
       float bn = sqrtf(dot3(b, b));
-      if (bn > 0.f) for (int k = 0; k < 3; k++) b[k] /= bn;
+      if (bn > 0.f) {
+        const float ib = 1.f / bn;
+        for (int k = 0; k < 3; k++) b[k] *= ib;
+      }
       if (bn < 0.5f) {
         b[0] = b[1] = b[2] = 0.f;
         if (-0.5f < n[1] && n[1] < 0.5f) b[1] = 1.f; else b[2] = 1.f;
@@ -128,7 +137,8 @@ __device__ void collide_pair(const float (*gx)[4], const float (*gq)[4], int pr,
   const float ma = dot3(a1, a1), mb = -dot3(a1, a2), mc = dot3(a2, a2), u = -dot3(a1, d), v = dot3(a2, d);
   const float det = ma * mc - mb * mb;
   if (fabsf(det) >= 1e-15f) {
-    float x1 = (mc * u - mb * v) / det, x2 = (ma * v - mb * u) / det;
+    const float idet = 1.f / det;
+    float x1 = (mc * u - mb * v) * idet, x2 = (ma * v - mb * u) * idet;
     if (x1 > 1.f) { x1 = 1.f; x2 = (v - mb) / mc; }
     else if (x1 < -1.f) { x1 = -1.f; x2 = (v + mb) / mc; }
     if (x2 > 1.f || x2 < -1.f) {

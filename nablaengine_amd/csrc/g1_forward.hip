@@ -974,7 +974,8 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
     if (nw > 0.f) {
       float sa, ca;
       sincosf(0.5f * kH * nw, &sa, &ca);
-      float dq[4] = {ca, sa * w[0] / nw, sa * w[1] / nw, sa * w[2] / nw};
+      const float sw = sa / nw;  // the adjoint replays this rotation with the same products
+      float dq[4] = {ca, sw * w[0], sw * w[1], sw * w[2]};
       float q[4] = {s.qpos[3], s.qpos[4], s.qpos[5], s.qpos[6]}, o[4];
       qmul(q, dq, o);
       float on = rsqrtf(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
