@@ -23,7 +23,10 @@ The library is libnablaengine_g1.so next to this file (built in-tree by ``python
 with ctypes; every call goes to its C entries (include/nablaengine_g1.h) with torch's current stream and the tensors'
 device pointers, the inputs' device made current. There is no fallback: without the library, or without a GPU, the
 calls raise. After init() the calls only launch kernels and allocate through torch's caching allocator (no host
-synchronization), so they can be captured in a HIP graph with fixed shapes.
+synchronization), so they can be captured in a HIP graph with fixed shapes. While torch.compile traces, the library
+calls are the torch.library custom ops nablaengine::forward, ::backward, ::kinematics and ::kinematics_backward with
+fake implementations (opaque nodes, no graph break with fullgraph=True; reference torch_ffi.py:583-655); in eager mode
+the same functions are called directly.
 
 Diagnostics (reference torch_ffi.py:56-62, 664-742): per device 18 int64 counters (DIAG) added to on the device by one
 small kernel after each forward and backward (set_diagnostics(False) skips it), read with diagnostics() (the tensor)
@@ -124,6 +127,9 @@ def init(device=None):
             raise _err(f"device cuda:{dev} cannot run the kernels (code {rc})", RuntimeError)
         _DIAG[dev] = torch.zeros(len(DIAG), dtype=torch.int64, device=f"cuda:{dev}")
         _READY.add(dev)
+    _custom_ops()  # defined here, outside any torch.compile trace (a definition inside one is not traceable),
+    _fn("step", _make_step_fn)  # as the autograd functions
+    _fn("kin", _make_kin_fn)
     return dict(path=LIB_PATH, sizes=list(_STATE["sizes"]))
 
 
@@ -318,6 +324,85 @@ def _kinematics_backward_impl(qpos, qvel, com, *cot):
     return [gq, gv]
 
 
+def _backward_op_impl(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv, normal,
+                      clamp_soft):
+    """_backward_impl with the custom op's argument order (reference torch_ffi.py:617-622): clamp_soft 0.0 for none."""
+    return _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal,
+                          None if clamp_kv != 2 else clamp_soft, tuple(kin_state), tuple(kin_cot))
+
+
+_OPS = {}
+_IMPL = dict(forward=_forward_impl, backward=_backward_op_impl, kinematics=_kinematics_impl,
+             kinematics_backward=_kinematics_backward_impl)
+
+
+def _ops():
+    """The library calls: the custom ops while torch.compile traces, the same functions called directly in eager
+    mode (no custom-op dispatch on the host path); reference torch_ffi.py:583-592."""
+    import torch
+    if not torch.compiler.is_compiling():
+        return _IMPL
+    return _custom_ops()
+
+
+def _custom_ops():
+    """nablaengine::forward, ::backward, ::kinematics, ::kinematics_backward (torch.library custom ops, no mutated
+    arguments, fresh outputs) with fake implementations giving the outputs' shapes; defined once per process
+    (reference torch_ffi.py:595-649)."""
+    if _OPS:
+        return _OPS
+    import torch
+    from typing import List, Optional
+    from torch import Tensor
+
+    @torch.library.custom_op("nablaengine::forward", mutates_args=())
+    def forward_op(qpos: Tensor, qvel: Tensor, warm: Tensor, ctrl: Tensor, friction: Tensor, com: Tensor,
+                   iterations: int, substeps: int, tape: bool, kinematics: bool) -> List[Tensor]:
+        return _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics)
+
+    @forward_op.register_fake
+    def _(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics):
+        B = qpos.shape[0]
+        out = [qpos.new_empty((B, NQ)), qpos.new_empty((B, NV)), qpos.new_empty((B, NV)),
+               qpos.new_empty((B, 4), dtype=torch.int32), qpos.new_empty((B if tape else 0, substeps * rec_words()))]
+        return out + ([qpos.new_empty(sh) for sh in _kin_shapes(B)] if kinematics else [])
+
+    @torch.library.custom_op("nablaengine::backward", mutates_args=())
+    def backward_op(tape: Tensor, friction: Tensor, com: Tensor, g_qpos: Tensor, g_qvel: Tensor,
+                    ctrl: Optional[Tensor], kin_state: List[Tensor], kin_cot: List[Tensor], substeps: int,
+                    clamp_kv: int, normal: int, clamp_soft: float) -> List[Tensor]:
+        return _backward_op_impl(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv,
+                                 normal, clamp_soft)
+
+    @backward_op.register_fake
+    def _(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv, normal, clamp_soft):
+        B = tape.shape[0]
+        return [tape.new_empty((B, NQ)), tape.new_empty((B, NV)), tape.new_empty((B, NU)),
+                tape.new_empty((B,), dtype=torch.int32)]
+
+    @torch.library.custom_op("nablaengine::kinematics", mutates_args=())
+    def kinematics_op(qpos: Tensor, qvel: Tensor, com: Tensor) -> List[Tensor]:
+        return _kinematics_impl(qpos, qvel, com)
+
+    @kinematics_op.register_fake
+    def _(qpos, qvel, com):
+        return [qpos.new_empty(sh) for sh in _kin_shapes(qpos.shape[0])]
+
+    @torch.library.custom_op("nablaengine::kinematics_backward", mutates_args=())
+    def kinematics_backward_op(qpos: Tensor, qvel: Tensor, com: Tensor, g_qpos_n: Tensor, g_xpos: Tensor,
+                               g_xquat: Tensor, g_cvel: Tensor, g_subtree_com: Tensor) -> List[Tensor]:
+        return _kinematics_backward_impl(qpos, qvel, com, g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com)
+
+    @kinematics_backward_op.register_fake
+    def _(qpos, qvel, com, g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com):
+        B = qpos.shape[0]
+        return [qpos.new_empty((B, NQ)), qpos.new_empty((B, NV))]
+
+    _OPS.update(forward=forward_op, backward=backward_op, kinematics=kinematics_op,
+                kinematics_backward=kinematics_backward_op)
+    return _OPS
+
+
 def _make_step_fn():
     import torch
 
@@ -328,7 +413,7 @@ def _make_step_fn():
         @staticmethod
         def forward(ctx, qpos, qvel, warm, ctrl, friction, com, iterations, substeps, clamp_kv, normal, clamp_soft,
                     grad_decay, kin):
-            r = _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, True, kin)
+            r = _ops()["forward"](qpos, qvel, warm, ctrl, friction, com, iterations, substeps, True, kin)
             q1, v1, w1, info, tp = r[:5]
             ctx.save_for_backward(tp, friction, com, ctrl, q1, v1)
             ctx.opts = (substeps, clamp_kv, normal, clamp_soft, grad_decay, kin)
@@ -341,13 +426,13 @@ def _make_step_fn():
             substeps, clamp_kv, normal, clamp_soft, grad_decay, kin = ctx.opts
             g_q1 = torch.zeros_like(q1) if g_q1 is None else g_q1.contiguous()
             g_v1 = torch.zeros_like(v1) if g_v1 is None else g_v1.contiguous()
-            ks, kc = (), ()
+            ks, kc = [], []
             if kin and any(g is not None for g in g_kin):
-                ks = (q1, v1)
-                kc = tuple(torch.zeros(sh, dtype=torch.float32, device=q1.device) if g is None else g.contiguous()
-                           for g, sh in zip(g_kin, _kin_shapes(q1.shape[0])))
-            gq, gv, gu, _ = _backward_impl(tp, friction, com, g_q1, g_v1, ctrl if clamp_kv == 2 else None, substeps,
-                                           clamp_kv, normal, clamp_soft, ks, kc)
+                ks = [q1, v1]
+                kc = [torch.zeros(sh, dtype=torch.float32, device=q1.device) if g is None else g.contiguous()
+                      for g, sh in zip(g_kin, _kin_shapes(q1.shape[0]))]
+            gq, gv, gu, _ = _ops()["backward"](tp, friction, com, g_q1, g_v1, ctrl if clamp_kv == 2 else None, ks, kc,
+                                               substeps, clamp_kv, normal, 0.0 if clamp_soft is None else clamp_soft)
             if grad_decay != 1.0:  # the state cotangent through this step times it, ctrl's not (float32 product)
                 gq, gv = gq * grad_decay, gv * grad_decay
             return gq, gv, None, gu, None, None, None, None, None, None, None, None, None
@@ -363,7 +448,7 @@ def _make_kin_fn():
 
         @staticmethod
         def forward(ctx, qpos, qvel, com):
-            out = _kinematics_impl(qpos, qvel, com)
+            out = _ops()["kinematics"](qpos, qvel, com)
             ctx.save_for_backward(qpos, qvel, com)
             return tuple(out)
 
@@ -372,7 +457,7 @@ def _make_kin_fn():
             qpos, qvel, com = ctx.saved_tensors
             g = [torch.zeros(sh, dtype=torch.float32, device=qpos.device) if x is None else x.contiguous()
                  for x, sh in zip(g, _kin_shapes(qpos.shape[0]))]
-            gq, gv = _kinematics_backward_impl(qpos, qvel, com, *g)
+            gq, gv = _ops()["kinematics_backward"](qpos, qvel, com, *g)
             return gq, gv, None
 
     return _Kin
@@ -403,7 +488,7 @@ def step(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, subste
     if torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in args):
         return _fn("step", _make_step_fn).apply(*args, int(iterations), int(substeps), int(clamp_kv), int(normal),
                                                 soft, gd, bool(kinematics))
-    r = _forward_impl(*args, int(iterations), int(substeps), False, bool(kinematics))
+    r = _ops()["forward"](*args, int(iterations), int(substeps), False, bool(kinematics))
     return tuple(r[:3]) + tuple(r[5:])
 
 
@@ -414,15 +499,15 @@ def kinematics(qpos, qvel, com):
     import torch
     if torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in (qpos, qvel, com)):
         return _fn("kin", _make_kin_fn).apply(qpos, qvel, com)
-    return tuple(_kinematics_impl(qpos, qvel, com))
+    return tuple(_ops()["kinematics"](qpos, qvel, com))
 
 
 def forward(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, tape=False,
             kinematics=False):
     """One control step without autograd: (qpos', qvel', warm', info (B, 4) int32[, tape][, the kinematics outputs])
     (reference torch_ffi.py:845-851)."""
-    r = _forward_impl(qpos, qvel, warm, ctrl, friction, com, int(iterations), int(substeps), bool(tape),
-                      bool(kinematics))
+    r = _ops()["forward"](qpos, qvel, warm, ctrl, friction, com, int(iterations), int(substeps), bool(tape),
+                          bool(kinematics))
     return tuple(r[:4]) + ((r[4],) if tape else ()) + tuple(r[5:])
 
 
@@ -434,11 +519,11 @@ def backward(tape, friction, com, g_qpos, g_qvel, *, substeps=SUBSTEPS, clamp_kv
     soft = _soft(clamp_kv, clamp_soft)
     if soft is not None and ctrl is None:
         raise _err("clamp_kv=2 (the soft clamp) needs the step's ctrl", ValueError)
-    ks, kc = ((), ()) if kinematics is None else (tuple(kinematics[:2]), tuple(kinematics[2:]))
+    ks, kc = ([], []) if kinematics is None else (list(kinematics[:2]), list(kinematics[2:]))
     if kinematics is not None and len(kc) != 5:
         raise _err("kinematics = (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com)", ValueError)
-    return tuple(_backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl if soft is not None else None, int(substeps),
-                                int(clamp_kv), int(normal), soft, ks, kc))
+    return tuple(_ops()["backward"](tape, friction, com, g_qpos, g_qvel, ctrl if soft is not None else None, ks, kc,
+                                    int(substeps), int(clamp_kv), int(normal), 0.0 if soft is None else soft))
 
 
 def set_diagnostics(enabled):

@@ -78,6 +78,32 @@ def test_python_surface_errors_without_gpu():
     assert torch_ffi.tape_bytes(4096) == 4096 * 4 * 1472 * 4
 
 
+def test_custom_ops_fake_shapes():
+    """The torch.library custom ops torch.compile traces (nablaengine::forward, ::backward, ::kinematics,
+    ::kinematics_backward) register without a GPU, and their fake implementations give the library's output shapes
+    and dtypes (reference torch_ffi.py:603-649)."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from nablaengine_amd import torch_ffi
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    torch_ffi._custom_ops()
+    B, rw = 5, torch_ffi.rec_words()
+    with FakeTensorMode():
+        a = [torch.empty(s) for s in ((B, 36), (B, 35), (B, 35), (B, 29), (B,), (B, 3))]
+        r = torch.ops.nablaengine.forward(*a, 10, 4, True, True)
+        assert [tuple(t.shape) for t in r] == [(B, 36), (B, 35), (B, 35), (B, 4), (B, 4 * rw), (B, 36), (B, 31, 3),
+                                               (B, 31, 4), (B, 31, 6), (B, 31, 3)]
+        assert r[3].dtype == torch.int32 and r[0].dtype == torch.float32
+        assert tuple(torch.ops.nablaengine.forward(*a, 10, 2, False, False)[4].shape) == (0, 2 * rw)
+        b = torch.ops.nablaengine.backward(r[4], a[4], a[5], r[0], r[1], None, [], [], 4, 0, 3, 0.0)
+        assert [tuple(t.shape) for t in b] == [(B, 36), (B, 35), (B, 29), (B,)] and b[3].dtype == torch.int32
+        k = torch.ops.nablaengine.kinematics(a[0], a[1], a[5])
+        assert [tuple(t.shape) for t in k] == [(B, 36), (B, 31, 3), (B, 31, 4), (B, 31, 6), (B, 31, 3)]
+        kb = torch.ops.nablaengine.kinematics_backward(a[0], a[1], a[5], *k)
+        assert [tuple(t.shape) for t in kb] == [(B, 36), (B, 35)]
+
+
 def test_bench_refuses_several_gpus():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode != 0 and "one GPU" in r.stderr
