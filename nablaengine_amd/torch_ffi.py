@@ -57,8 +57,9 @@ VARIANTS = tuple((kv, n) for kv in (0, 1, 2) for n in (0, 1, 2, 3))  # adjoint v
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libnablaengine_g1.so")
+ARCH = "gfx950"  # the one architecture the library is built for
 
-_LOCK = threading.Lock()
+_LOCK = threading.RLock()
 _STATE = {}
 _READY = set()
 _DIAG = {}  # device index -> int64 (len(DIAG),) counters on that device
@@ -70,13 +71,32 @@ def _err(msg, exc=TypeError):
     return exc(f"nablaengine_amd.torch_ffi: {msg}")
 
 
+def _library_path(artifact):
+    """The library an artifact names: a .so path, or a JSON file whose "library" key names it (relative to the JSON
+    file), as the reference's artifacts (torch_ffi.py:241-266); None: $DK_TORCH_ARTIFACT, $NABLA_G1_LIB, else the
+    in-tree build."""
+    a = artifact or os.environ.get("DK_TORCH_ARTIFACT") or os.environ.get("NABLA_G1_LIB") or LIB_PATH
+    a = os.fspath(a)
+    if a.endswith(".json"):
+        import json
+        with open(a) as f:
+            meta = json.load(f)
+        if "library" not in meta:
+            raise _err(f"artifact {a} names no library", RuntimeError)
+        return os.path.join(os.path.dirname(os.path.abspath(a)), meta["library"])
+    return a
+
+
 def load_library(path=None):
-    """ctypes handle of the library with the C entries' argument types set; raises RuntimeError when it is missing
-    (build it with `python -m nablaengine_amd.build`)."""
+    """ctypes handle of the library with the C entries' argument types set (path: as init's artifact); raises
+    RuntimeError when it is missing (build it with `python -m nablaengine_amd.build`), or when another library is
+    loaded already (one library per process)."""
     with _LOCK:
         if "lib" in _STATE:
+            if path is not None and os.path.realpath(_library_path(path)) != os.path.realpath(_STATE["path"]):
+                raise _err(f"{_STATE['path']} is loaded: one library per process", RuntimeError)
             return _STATE["lib"]
-        p = path or os.environ.get("NABLA_G1_LIB", LIB_PATH)
+        p = _library_path(path)
         if not os.path.exists(p):
             raise _err(f"{p} is missing: build it with `python -m nablaengine_amd.build`", RuntimeError)
         lib = ctypes.CDLL(p)
@@ -101,6 +121,7 @@ def load_library(path=None):
         sizes = (ctypes.c_longlong * 9)()
         lib.dk_fwd_sizes(ctypes.cast(sizes, vp))
         _STATE["sizes"] = [int(x) for x in sizes]
+        _STATE["path"] = p
         _STATE["lib"] = lib
         return lib
 
@@ -111,26 +132,37 @@ def rec_words():
     return _STATE["sizes"][2]
 
 
-def init(device=None):
-    """Load the library and check that `device` (default: torch's current device) can run it; idempotent per
-    device. The model constants are compiled into the library, so nothing is uploaded and nothing synchronizes."""
+def init(device=None, artifact=None, model_dir=None, model=None, foot_pairs=None):
+    """Load the library and check that `device` (default: torch's current device) can run it; idempotent per device,
+    one library per process (reference torch_ffi.py:268-290). artifact: the library (a .so, or a JSON artifact naming
+    it); default $DK_TORCH_ARTIFACT, else the in-tree build. The G1 model is compiled into the library, so nothing is
+    uploaded and nothing synchronizes; another model (model_dir / model / foot_pairs) is a ValueError. Returns the
+    library's path, architecture and sizes."""
     import torch
-    lib = load_library()
-    if not torch.cuda.is_available():
-        raise _err("no ROCm GPU visible: the engine runs on the GPU only", RuntimeError)
-    dev = torch.cuda.current_device() if device is None else torch.device(device).index
-    dev = torch.cuda.current_device() if dev is None else dev
-    if dev not in _READY:
-        with torch.cuda.device(dev):
-            rc = lib.dk_fwd_upload(None, ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
-        if rc:
-            raise _err(f"device cuda:{dev} cannot run the kernels (code {rc})", RuntimeError)
-        _DIAG[dev] = torch.zeros(len(DIAG), dtype=torch.int64, device=f"cuda:{dev}")
-        _READY.add(dev)
-    _custom_ops()  # defined here, outside any torch.compile trace (a definition inside one is not traceable),
-    _fn("step", _make_step_fn)  # as the autograd functions
-    _fn("kin", _make_kin_fn)
-    return dict(path=LIB_PATH, sizes=list(_STATE["sizes"]))
+    if model_dir is not None or model is not None or foot_pairs is not None:
+        raise _err("the G1 model is compiled into this library: model_dir / model / foot_pairs are not supported",
+                   ValueError)
+    with _LOCK:
+        lib = load_library(artifact)
+        if not torch.cuda.is_available():
+            raise _err("no ROCm GPU visible: the engine runs on the GPU only", RuntimeError)
+        dev = torch.cuda.current_device() if device is None else torch.device(device).index
+        dev = torch.cuda.current_device() if dev is None else dev
+        if dev not in _READY:
+            arch = getattr(torch.cuda.get_device_properties(dev), "gcnArchName", ARCH).split(":")[0]
+            if arch != ARCH:
+                raise _err(f"cuda:{dev} is {arch}, the library is built for {ARCH} (one architecture per process)",
+                           RuntimeError)
+            with torch.cuda.device(dev):
+                rc = lib.dk_fwd_upload(None, ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+            if rc:
+                raise _err(f"device cuda:{dev} cannot run the kernels (code {rc})", RuntimeError)
+            _DIAG[dev] = torch.zeros(len(DIAG), dtype=torch.int64, device=f"cuda:{dev}")
+            _READY.add(dev)
+        _custom_ops()  # defined here, outside any torch.compile trace (a definition inside one is not traceable),
+        _fn("step", _make_step_fn)  # as the autograd functions
+        _fn("kin", _make_kin_fn)
+        return dict(path=_STATE["path"], arch=ARCH, sizes=list(_STATE["sizes"]))
 
 
 def tape_bytes(nworld, substeps=SUBSTEPS, steps=1):

@@ -104,6 +104,26 @@ def test_custom_ops_fake_shapes():
         assert [tuple(t.shape) for t in kb] == [(B, 36), (B, 35)]
 
 
+def test_init_artifacts_one_library_per_process(tmp_path):
+    """init / load_library take the library as a .so path or a JSON artifact naming it (reference torch_ffi.py:241-290);
+    a second, different library in the same process is a RuntimeError; another model is a ValueError (the G1 model is
+    compiled in)."""
+    from nablaengine_amd import torch_ffi
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    lib = torch_ffi.load_library()
+    art = tmp_path / "g1.json"
+    art.write_text(json.dumps({"library": os.path.relpath(torch_ffi._STATE["path"], tmp_path)}))
+    assert os.path.realpath(torch_ffi._library_path(str(art))) == os.path.realpath(torch_ffi._STATE["path"])
+    assert torch_ffi.load_library(str(art)) is lib
+    other = tmp_path / "other.so"
+    other.write_bytes(b"")
+    with pytest.raises(RuntimeError):
+        torch_ffi.load_library(str(other))
+    with pytest.raises(ValueError):
+        torch_ffi.init(model="g1.xml")
+
+
 def test_bench_refuses_several_gpus():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode != 0 and "one GPU" in r.stderr
