@@ -1,0 +1,126 @@
+"""The forward's per-substep outputs through the C ABI (reference checks T1-T3, T8 of docs/verification.md:124-137 and
+the contact check of scripts/engine_step_check.py): the contacts of a substep (ocon) against MuJoCo Warp 3.17's on the
+corpus states; the tape's state chain (record k holds the state after k substeps, bitwise the k-substep forward's
+outputs); its contact table against the substep's contacts; and record coverage (a buffer prefilled with 0xA5 bytes
+gives bitwise the tape of a zeroed one)."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from nablaengine_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+KEYS = ("qpos", "qvel", "warm", "ctrl", "friction", "com")
+MAXCON = 64
+REC_HDR, REC_CON, REC_QPOS, REC_QVEL, REC_ASTAR = 0, 16, 48, 84, 128
+
+
+@pytest.fixture(scope="module")
+def ffi():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible")
+    from nablaengine_amd import torch_ffi
+    torch_ffi.init(0)
+    return torch_ffi
+
+
+def _t(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def _forward(ffi, args, nsub, tape_fill=None, con=False):
+    """dk_fwd_forward with an ocon buffer and (tape_fill not None) a tape prefilled with that 32-bit pattern."""
+    import torch
+    lib = ffi.load_library()
+    B = args[0].shape[0]
+    kw = dict(dtype=torch.float32, device="cuda")
+    q1, v1, w1 = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 35), **kw)
+    info = torch.empty((B, 4), dtype=torch.int32, device="cuda")
+    ocon = torch.empty((B, MAXCON, 8), **kw) if con else None
+    tape = None
+    if tape_fill is not None:
+        tape = torch.full((B, nsub * ffi.rec_words()), tape_fill, dtype=torch.int32, device="cuda").view(torch.float32)
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.dk_fwd_forward(st, B, *map(p, args), 10, nsub, p(q1), p(v1), p(w1), p(info), p(ocon), p(tape),
+                              None) == 0
+    torch.cuda.synchronize()
+    return q1, v1, w1, info, ocon, tape
+
+
+def test_contacts_vs_mujoco_warp(ffi):
+    """One substep's contacts (ocon: pair, dist, pos, normal) on 512 corpus states against MuJoCo Warp 3.17's at the
+    input state: the same pair multiset in >= 99% of the states; matched contacts (same pair, nearest point) agree in
+    position (1e-4 m), distance (2e-5 m) and normal (1e-4), in float32."""
+    z = np.load(os.path.join(GOLD, "mjw_mf_s0.npz"))
+    st = dict(qpos=z["qpos"], qvel=z["qvel"], warm=z["qacc_warmstart"], ctrl=z["ctrl"], friction=z["friction"],
+              com=z["com"])
+    q1, v1, w1, info, ocon, _ = _forward(ffi, [_t(st[k]) for k in KEYS], 1, con=True)
+    ocon = ocon.cpu().numpy().astype(np.float64)
+    n = len(z["con_count"])
+    same, worst = 0, [0.0, 0.0, 0.0]
+    for i in range(n):
+        mine = ocon[i][ocon[i][:, 0] >= 0]
+        ref = z["con"][i, :int(z["con_count"][i])]
+        assert len(mine) == info[i, 1].item()
+        if sorted(mine[:, 0].astype(int).tolist()) != sorted(ref[:, 0].astype(int).tolist()):
+            continue
+        same += 1
+        for row in ref:
+            cand = mine[mine[:, 0] == row[0]]
+            d = np.linalg.norm(cand[:, 2:5] - row[2:5], axis=1)
+            j = int(np.argmin(d))
+            worst = [max(worst[0], d[j]), max(worst[1], abs(cand[j, 1] - row[1])),
+                     max(worst[2], np.linalg.norm(cand[j, 5:8] - row[5:8]))]
+    print(f"same contact set in {same}/{n} states; worst matched pos {worst[0]:.3g} dist {worst[1]:.3g} "
+          f"normal {worst[2]:.3g}")
+    assert same / n >= 0.99
+    assert worst[0] <= 1e-4 and worst[1] <= 2e-5 and worst[2] <= 1e-4
+
+
+def test_tape_state_chain_and_contact_table(ffi):
+    """Record 0 holds the inputs; record k (k >= 1) the state after k substeps, bitwise the outputs of the k-substep
+    forward (qpos, qvel), whose warm' is bitwise record k-1's a*. Each record's contact table lists the pairs of that
+    substep's contacts (ocon of the (k+1)-substep forward), 0xFFFF past the count, and its header's count is theirs."""
+    import torch
+    B = 512
+    args = [_t(synthetic.states(B, config=4)[k]) for k in KEYS]
+    *_, tape = _forward(ffi, args, 4, tape_fill=0)
+    rw = ffi.rec_words()
+    rec = tape.view(torch.int32).cpu().numpy().reshape(B, 4, rw)
+    recf = rec.view(np.float32)
+    assert np.array_equal(recf[:, 0, REC_QPOS:REC_QPOS + 36].view(np.uint32),
+                          args[0].cpu().numpy().view(np.uint32))
+    assert np.array_equal(recf[:, 0, REC_QVEL:REC_QVEL + 35].view(np.uint32),
+                          args[1].cpu().numpy().view(np.uint32))
+    for k in range(1, 5):
+        q, v, w, info, ocon, _ = _forward(ffi, args, k, con=True)
+        q, v, w = (x.cpu().numpy() for x in (q, v, w))
+        assert np.array_equal(w.view(np.uint32), recf[:, k - 1, REC_ASTAR:REC_ASTAR + 35].view(np.uint32))
+        if k < 4:
+            assert np.array_equal(q.view(np.uint32), recf[:, k, REC_QPOS:REC_QPOS + 36].view(np.uint32))
+            assert np.array_equal(v.view(np.uint32), recf[:, k, REC_QVEL:REC_QVEL + 35].view(np.uint32))
+        ocon = ocon.cpu().numpy()
+        ncon = rec[:, k - 1, REC_HDR] & 255
+        assert np.array_equal(ncon, info[:, 1].cpu().numpy())
+        half = rec[:, k - 1, REC_CON:REC_CON + 32].view(np.uint16).reshape(B, 64)  # two 16-bit entries a word
+        for i in range(B):
+            n = int(ncon[i])
+            assert (half[i, n:] == 0xFFFF).all()
+            assert sorted((half[i, :n] & 511).tolist()) == sorted(ocon[i, :n, 0].astype(int).tolist())
+
+
+def test_tape_record_coverage(ffi):
+    """A tape buffer prefilled with 0xA5 bytes gives bitwise the tape of a zero-filled one (every word of every record
+    is written), with config-4 (contact-heavy) states."""
+    import torch
+    B = 512
+    args = [_t(synthetic.states(B, config=4)[k]) for k in KEYS]
+    *_, t0 = _forward(ffi, args, 4, tape_fill=0)
+    *_, t1 = _forward(ffi, args, 4, tape_fill=int(np.int32(np.uint32(0xA5A5A5A5))))
+    assert torch.equal(t0.view(torch.int32), t1.view(torch.int32))
