@@ -69,6 +69,33 @@ def test_adjoint_vs_mujoco_fd_truth(ffi, cname):
     assert not (info & (1 << 13)).any(), "a replayed contact was not found"
 
 
+@pytest.mark.parametrize("cname", ["mf_s0", "mf_s1"])
+def test_adjoint_reference_gradient_gates(ffi, cname):
+    """The reference's gradient gates (scripts/gradient_check.py: its default 50 iterations, exact mode clamp_kv=1,
+    normal=0, groups G0 / G4 / G5 / G6 on the model_ok states, tests/gradient_gates.py's scorer): per group and block
+    the floored relative error's p99 <= 2e-3 / 5e-4 / 1e-4 (qpos tangent / qvel / ctrl) and the cosine's 1st percentile
+    >= 0.99999; every gradient finite."""
+    import torch
+    from gradient_gates import block_scores, passes, truth_states
+    z = np.load(os.path.join(GOLD, f"grad_{cname}.npz"))
+    for group in ("G0", "G4", "G5", "G6"):
+        sel, st, cq, cv = truth_states(z, group)
+        n = len(sel)
+        args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+        r = ffi.forward(*args, iterations=50, tape=True)
+        g = np.zeros((n, 3, 99))
+        for c in range(3):
+            gq, gv, gu, info = ffi.backward(r[4], args[4], args[5], _t(cq[:, c]), _t(cv[:, c]), clamp_kv=1, normal=0)
+            torch.cuda.synchronize()
+            gq, gv, gu = (x.cpu().numpy().astype(np.float64) for x in (gq, gv, gu))
+            g[:, c] = np.concatenate([oracle.qpos_tangent(st["qpos"], gq), gv, gu], 1)
+        assert np.isfinite(g).all()
+        ok, stats = passes(block_scores(g, z["fd_vjp"][sel], z["fd_vjp_floor"][sel], z["bad"][sel] == 0))
+        print(f"{cname} {group} ({n} states): " + ", ".join(f"{b} p99 {p:.3g} cos p1 {c:.8f}"
+                                                            for b, (p, c) in stats.items()))
+        assert ok, (group, stats)
+
+
 def test_adjoint_vs_oracle_config2(ffi):
     """256 config-1 worlds, output cotangents N(0, 1); the float32 GPU VJP against the float64
     oracle's analytic VJP (exact mode) at the engine's settings, and on 8 of the worlds against the oracle's float64

@@ -163,6 +163,27 @@ def test_fd_machinery_and_adjoint_vs_mujoco_fd():
         assert all(np.median(e) > 1e-4 for e in _vjp_block_errors(bad, fd).values())
 
 
+def test_gradient_gate_self_test():
+    """The reference's gradient gates (tests/gradient_gates.py) pass for the oracle's analytic VJP (exact mode, the
+    truth's solver settings) on mf_s0's model_ok G0 states, and fail for the same VJPs moved by 3e-3 relative per
+    state, cotangent and block (scripts/gradient_check.py's perturbed_must_fail)."""
+    from gradient_gates import block_scores, passes, perturb, truth_states
+    z = np.load(os.path.join(GOLD, "grad_mf_s0.npz"))
+    sel, st, cq, cv = truth_states(z, "G0")
+    sel, cq, cv = sel[:24], cq[:24], cv[:24]
+    st = {k: v[:24] for k, v in st.items()}
+    n = len(sel)
+    g = np.zeros((n, 3, 99))
+    for c in range(3):
+        gq, gv, gu = oracle.vjp(**st, g_qpos=cq[:, c], g_qvel=cv[:, c], clamp_kv=1, normal=0, **oracle.TRUTH)
+        g[:, c] = np.concatenate([oracle.qpos_tangent(st["qpos"], gq), gv, gu], 1)
+    valid = z["bad"][sel] == 0
+    ok, stats = passes(block_scores(g, z["fd_vjp"][sel], z["fd_vjp_floor"][sel], valid))
+    assert ok, stats
+    bad, stats_bad = passes(block_scores(perturb(g, 3e-3), z["fd_vjp"][sel], z["fd_vjp_floor"][sel], valid))
+    assert not bad, stats_bad
+
+
 def test_adjoint_variants_differ_where_they_should():
     """clamp_kv 0 / 1 agree on states without a clamped actuator and differ on clamped ones (G4); the normal options
     agree on G0 states (no self contact below 1e-3 m)."""
