@@ -81,3 +81,46 @@ def test_nonfinite_bits_and_switch(ffi):
         assert torch.equal(torch.nan_to_num(gq2), torch.nan_to_num(gq))
     finally:
         ffi.set_diagnostics(prev)
+
+
+def test_capacity_overflow(ffi):
+    """The reference's overflow check (scripts/torch_ffi_check.py:350-388): states pushed 0.6 m into the floor with
+    scrambled joints exceed the 64 contacts and the 192 rows of a world in some worlds. info[:, 3] flags them
+    (OVERFLOW_CONTACTS / OVERFLOW_ROWS, over all substeps; info[:, 1] is the last substep's raw contact count), the
+    counters equal the flagged worlds, the outputs stay finite and deterministic, and read_diagnostics warns only with
+    set_overflow_warnings(True)."""
+    import warnings
+    import torch
+    B = 512
+    st = synthetic.states(B, config=1)
+    rng = np.random.default_rng(0)
+    st["qpos"][:, 2] -= 0.6
+    st["qpos"][:, 7:] += rng.uniform(-1.5, 1.5, st["qpos"][:, 7:].shape).astype(np.float32)
+    args = [_t(st[k]) for k in KEYS]
+    ffi.read_diagnostics(reset=True)
+    q1, v1, w1, info = ffi.forward(*args)
+    q2, v2, w2, info2 = ffi.forward(*args)
+    torch.cuda.synchronize()
+    for a, b in zip((q1, v1, w1, info), (q2, v2, w2, info2)):
+        assert torch.equal(a, b)
+    assert torch.isfinite(q1).all() and torch.isfinite(v1).all()
+    u = info[:, 3].cpu().numpy()
+    nc, nr = int((u & ffi.OVERFLOW_CONTACTS != 0).sum()), int((u & ffi.OVERFLOW_ROWS != 0).sum())
+    print(f"contact overflow {nc}/{B} worlds, row overflow {nr}/{B}")
+    assert nc > 0 and nr > 0
+    inf = info.cpu().numpy()  # the last substep's raw contact count and kept rows; the flags hold over all substeps
+    assert (u[inf[:, 1] > ffi.MAXCON] & ffi.OVERFLOW_CONTACTS != 0).all() and (inf[:, 1] > ffi.MAXCON).any()
+    assert (inf[:, 2] <= 192).all()
+    with warnings.catch_warnings(record=True) as w0:
+        warnings.simplefilter("always")
+        d = ffi.read_diagnostics(reset=False)
+    assert not any("capacity" in str(w.message) for w in w0)
+    assert d["fwd_contact_overflow_worlds"] == 2 * nc and d["fwd_row_overflow_worlds"] == 2 * nr
+    prev = ffi.set_overflow_warnings(True)
+    try:
+        with warnings.catch_warnings(record=True) as w1_:
+            warnings.simplefilter("always")
+            ffi.read_diagnostics()
+    finally:
+        ffi.set_overflow_warnings(prev)
+    assert any(issubclass(w.category, RuntimeWarning) and "capacity" in str(w.message) for w in w1_)
