@@ -70,12 +70,17 @@ void dk_fwd_sizes(long long* o);
  * and end (s_memrealtime, 100 MHz) and where it ran (HW_ID | XCC_ID << 32), then the cycles of parts of the smooth
  * dynamics (forward kinematics, body forces, subtree sums, CRBA and bias)); returns -1 in the production build. */
 int dk_prof_read(unsigned long long* out, int nw);
+/* No counterpart in the reference's ABI (its adjoint's DK_PROFILE phases, adjoint.py:101-107,221-232): in a build with
+ * -DG1_PROFILE, copies the last adjoint's per-world phase cycles of the first nw worlds, nw x 27 uint64 (record,
+ * poses, solves, twists, contacts, body sums, body forces, dof terms, then the world's start and end on the 100 MHz
+ * clock; the rest 0); returns -1 in the production build. */
+int dk_prof_read_adj(unsigned long long* out, int nw);
 
 /* Replaces <variant>_adjoint (jax_ffi.py:228-241) for every (clamp_kv, normal) variant at once: the VJP of one control
- * step from its tape. in: tape (nw, nsub * DK_REC_WORDS), fric, com as the forward's, gq_out (nw, 36), gv_out (nw, 35)
- * the output cotangents, ctrl (nw, 29) (clamp_kv 2 only, else may be NULL), clamp_soft (clamp_kv 2); out: gq_in (nw, 36)
- * qpos-form, gv_in (nw, 35), gctrl (nw, 29), info (nw,): the union of the records' flags, 1 << 13 a replayed contact
- * not found (the reference's ADJ_REPLAY_MISMATCH). */
+ * step from its tape. in: tape (nw, nsub * DK_REC_WORDS; 16-byte aligned, else hipErrorInvalidValue), fric, com as
+ * the forward's, gq_out (nw, 36), gv_out (nw, 35) the output cotangents, ctrl (nw, 29) (clamp_kv 2 only, else may be
+ * NULL), clamp_soft (clamp_kv 2); out: gq_in (nw, 36) qpos-form, gv_in (nw, 35), gctrl (nw, 29), info (nw,): the union
+ * of the records' flags, 1 << 13 a replayed contact not found (the reference's ADJ_REPLAY_MISMATCH). */
 int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                const float* ctrl, float clamp_soft, int clamp_kv, int normal);

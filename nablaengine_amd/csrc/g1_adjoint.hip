@@ -89,15 +89,48 @@ struct __align__(16) Adj {
   float tw[NB][NTW][6];              // per-body twists (6 floats each)
   float gx[NGEOM][4], gq[NGEOM][4];
   union {
-    float L[NTRI + 2];         // the taped factor of the solves
+    struct __align__(16) {
+      float q[768], h[768];    // the taped factors L_Q and L_H (630 words each, then the last copy's slack)
+    } lt;
     float fb[NB][NFB][6];      // then the per-body force vectors (6 floats each)
   };
   int ncon, flags;
   unsigned clampm[2], limzone[2], limrow[2], czone[8];
   unsigned short con[MAXCON];
+#ifdef G1_PROFILE
+  unsigned long long prof_t, prof_acc[NPHASE];
+#endif
 };
 // 8 worlds per CU: the LDS of one world must stay within 160 KB / 8
 static_assert(sizeof(Adj) <= 20480, "Adj outgrew the LDS of 8 worlds per CU");
+static_assert(offsetof(Adj, lt) % 16 == 0 && 3 * 256 <= 768 && NTRI <= 3 * 256, "the factors' LDS copies");
+
+// L_Q and L_H of a record copied into LDS by the memory unit (global_load_lds_dwordx4: lane l's 16 bytes land 16 l
+// bytes past the instruction's LDS base), 3 x 1024 bytes each; lanes past the factor's end load its start again into
+// the slack. Issued before the record's other loads, they arrive with them; no registers hold them.
+__device__ __forceinline__ void load_factors(Adj& s, const float* __restrict__ rec, int lane) {
+#pragma unroll
+  for (int c = 0; c < 3; c++) {
+    const int f = 256 * c + 4 * lane;  // the lane's first word (f + 3 <= 631: inside the record for both factors)
+    const int fo = f < NTRI ? f : 0;
+    __builtin_amdgcn_global_load_lds((const void*)(rec + REC_LQ + fo),
+                                     (__attribute__((address_space(3))) void*)(s.lt.q + 256 * c), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(rec + REC_LH + fo),
+                                     (__attribute__((address_space(3))) void*)(s.lt.h + 256 * c), 16, 0, 0);
+  }
+}
+
+// The adjoint's phase profile (a G1_PROFILE build only; g_prof_adj, read by dk_prof_read_adj): s_memtime
+// cycles per phase summed over the substeps, then the world's start and end on the 100 MHz clock.
+enum { AP_RECORD = 0, AP_POSES, AP_SOLVE, AP_TWIST, AP_CONTACT, AP_BODYSUM, AP_FORCES, AP_DOF, AP_T0, AP_T1,
+       AP_SUBTREE, NAPHASE };
+static_assert(NAPHASE <= NPHASE, "the adjoint's phases fit g_prof_adj's rows");
+#ifdef G1_PROFILE
+__device__ unsigned long long g_prof_adj[PROF_WORLDS][NPHASE];
+#define APROF(k) PROF_MARK(s.prof_acc, s.prof_t, k)
+#else
+#define APROF(k) do { } while (0)
+#endif
 
 // impedance and its derivative in the distance (kbimp's curve, solimp power 2; 0 where the curve is clamped)
 __device__ __forceinline__ void imp_d(const float* solimp, float pos, float* imp, float* dimp) {
@@ -319,7 +352,8 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
 // ---------------------------------------------------------------------------------------------- one substep
 __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int clamp_kv, int normal,
                             float clamp_soft) {
-  // the record
+  // the record (the factors first, into LDS directly)
+  load_factors(s, rec, lane);
   if (lane < NQ) s.qpos[lane] = rec[REC_QPOS + lane];
   if (lane < NV) {
     s.qvel[lane] = rec[REC_QVEL + lane];
@@ -340,6 +374,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   }
   if (lane == 0) s.ncon = min((int)(__float_as_uint(rec[REC_HDR]) & 255u), MAXCON);
   wsync();
+  APROF(AP_RECORD);
   // poses: each hinge body's local transform (lane = body), then each body lane walks its chain (the chain table)
   if (lane >= 2 && lane < NB) {
     float sn, cs;
@@ -469,19 +504,19 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     for (int k = 0; k < 3; k++) s.vt[3 + k] += kH * (t[k] + c1 * pt[k] + c2 * ppt[k]);
   }
   wsync();
+  APROF(AP_POSES);
   // y = Q^-1 a_adv bar (L_Q), a* bar = a_adv bar - h kv y; lambda = H^-1 a* bar (L_H)
-  for (int i = lane; i < NTRI; i += WL) s.L[i] = rec[REC_LQ + i];
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the factors' copies have landed in LDS
   wsync();
   const float aab = lane < NV ? kH * s.vt[lane] : 0.f;
-  const float y = ltl_solve(s.L, aab, lane);
+  const float y = ltl_solve(s.lt.q, aab, lane);
   if (lane < NV) s.y[lane] = y;
   wsync();
-  for (int i = lane; i < NTRI; i += WL) s.L[i] = rec[REC_LH + i];
-  wsync();
   const float asb = lane < NV ? aab - kH * cKv[lane] * y : 0.f;
-  const float lam = ltl_solve(s.L, asb, lane);
+  const float lam = ltl_solve(s.lt.h, asb, lane);
   if (lane < NV) s.lam[lane] = lam;
   wsync();
+  APROF(AP_SOLVE);
   // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body
   if (lane >= 1 && lane < NB) {
     Sv V = sv0(), Lm = sv0(), Y = sv0(), Aw = sv0(), A2 = sv0(), Ac = sv0();
@@ -517,6 +552,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   if (lane == 0)
     for (int t = 0; t < NTW; t++) st_sv6(s.tw[0][t], sv0());
   wsync();
+  APROF(AP_TWIST);
   // limit rows (their dof's lane): through the distance only (J constant)
   float lgq = 0.f, lgv = 0.f;
   if (lane >= 6 && lane < NV) {
@@ -629,6 +665,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
       }
     }
   }
+  APROF(AP_CONTACT);
   // per body: the contacts' wrenches and row sums, summed over the contact lanes once per distinct contact body
   // (masked wave sums, a fixed order); body lane B keeps its totals
   Sv EG = sv0(), OL = sv0(), OA = sv0(), OV = sv0();
@@ -654,6 +691,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
         OA.w[k] = x[12 + k]; OA.v[k] = x[15 + k]; OV.w[k] = x[18 + k]; OV.v[k] = x[21 + k];
       }
   }
+  APROF(AP_BODYSUM);
   if (lane >= 1 && lane < NB) {
     const float* I = s.Ib[lane];
     const Sv V = ld_sv6(s.tw[lane][TW_V]), Lm = ld_sv6(s.tw[lane][TW_L]);
@@ -672,24 +710,65 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     st_sv6(s.fb[lane][FB_OV], OV);
   }
   wsync();
+  APROF(AP_FORCES);
+  // per body B: the subtree sums T[B] = sum of fb[b] over the bodies b of B's subtree (54 floats each), as the product
+  // T = A F (32 x 32 x 64, A[B][b] = 1 for b in B's subtree, 0 for the world and the padding) on the matrix cores:
+  // v_mfma_f32_16x16x4f32, lane l giving A[l % 16][l / 16] and F[l / 16][l % 16] and holding C[4 (l / 16) + e][l % 16];
+  // 2 x 4 tiles, 8 steps of k = 4, in two passes over 32 columns each. A pass reads only its own columns of F, every
+  // load before its first store, so T overwrites fb in place.
+  {
+    typedef float mfma4 __attribute__((ext_vector_type(4)));
+    constexpr int NF = NFB * 6;
+    float* F = &s.fb[0][0][0];
+    const int lr = lane & 15, lk = lane >> 4;
+    const unsigned sm[2] = {lr >= 1 ? cTree.submask[lr] : 0u, 16 + lr < NB ? cTree.submask[16 + lr] : 0u};
+#pragma unroll 1
+    for (int half = 0; half < 2; half++) {
+      mfma4 acc[2][2];
+#pragma unroll
+      for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int n = 0; n < 2; n++) acc[m][n] = mfma4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const int kb = 4 * t + lk;  // the body of this lane's k index
+        const bool kin = kb >= 1 && kb < NB;
+        float bv[2];
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+          const int c = 32 * half + 16 * n + lr;
+          const bool ok = kin && c < NF;
+          const float x = F[ok ? kb * NF + c : 0];
+          bv[n] = ok ? x : 0.f;
+        }
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+          const float av = kin && ((sm[m] >> kb) & 1u) ? 1.f : 0.f;
+#pragma unroll
+          for (int n = 0; n < 2; n++)
+            acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[n], acc[m][n], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int B = 16 * m + 4 * lk + e, c = 32 * half + 16 * n + lr;
+            if (B >= 1 && B < NB && c < NF) F[B * NF + c] = acc[m][n][e];
+          }
+    }
+  }
+  wsync();
+  APROF(AP_SUBTREE);
   // per dof: subtree sums and the joint's outside terms
   if (lane < NV) {
     const int j = lane;
     const int bj = j < 6 ? 1 : j - 4;
-    const unsigned sub = cTree.submask[bj];
-    Sv F1 = sv0(), P = sv0(), X1 = sv0(), F2 = sv0(), P2 = sv0(), EGs = sv0(), OLs = sv0(), OAs = sv0(), OVs = sv0();
-    for (int b = 1; b < NB; b++) {
-      if (!((sub >> b) & 1u)) continue;
-      F1 = sv_add(F1, ld_sv6(s.fb[b][FB_F1]));
-      P = sv_add(P, ld_sv6(s.fb[b][FB_P]));
-      X1 = sv_add(X1, ld_sv6(s.fb[b][FB_X1]));
-      F2 = sv_add(F2, ld_sv6(s.fb[b][FB_F2]));
-      P2 = sv_add(P2, ld_sv6(s.fb[b][FB_P2]));
-      EGs = sv_add(EGs, ld_sv6(s.fb[b][FB_EG]));
-      OLs = sv_add(OLs, ld_sv6(s.fb[b][FB_OL]));
-      OAs = sv_add(OAs, ld_sv6(s.fb[b][FB_OA]));
-      OVs = sv_add(OVs, ld_sv6(s.fb[b][FB_OV]));
-    }
+    const Sv F1 = ld_sv6(s.fb[bj][FB_F1]), P = ld_sv6(s.fb[bj][FB_P]), X1 = ld_sv6(s.fb[bj][FB_X1]);  // subtree sums
+    const Sv F2 = ld_sv6(s.fb[bj][FB_F2]), P2 = ld_sv6(s.fb[bj][FB_P2]), EGs = ld_sv6(s.fb[bj][FB_EG]);
+    const Sv OLs = ld_sv6(s.fb[bj][FB_OL]), OAs = ld_sv6(s.fb[bj][FB_OA]), OVs = ld_sv6(s.fb[bj][FB_OV]);
     Sv Vo = sv0(), Lo = sv0(), Yo = sv0(), Awo = sv0(), A1o = sv0(), A2o = sv0();
     for (int k = 0; k < 3; k++) A1o.v[k] = -kGrav[k];
     if (j >= 3 && j < 6) {
@@ -732,6 +811,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     s.vb[j] = s.vt[j] + gv;
   }
   wsync();
+  APROF(AP_DOF);
 }
 
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_adjoint(int nw, int nsub, const float* __restrict__ tape,
@@ -749,6 +829,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
   if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = ctrl ? ctrl[(size_t)w * NU + lane] : 0.f; }
   if (lane == 0) { s.fric = fric[w]; s.flags = 0; }
+#ifdef G1_PROFILE
+  if (lane < NPHASE) s.prof_acc[lane] = 0;
+  if (lane == 0) {
+    s.prof_t = __builtin_amdgcn_s_memtime();
+    s.prof_acc[AP_T0] = __builtin_amdgcn_s_memrealtime();
+  }
+#endif
   chain_table(s.chain, lane);
   // the output cotangents in the tangent space at the output state (its root quaternion: the last substep's
   // integration replayed from the record)
@@ -797,6 +884,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane < NV) gv_in[(size_t)w * NV + lane] = s.vb[lane];
   if (lane < NU) gctrl[(size_t)w * NU + lane] = s.ub[lane];
   if (lane == 0) info[w] = s.flags;
+#ifdef G1_PROFILE
+  wsync();
+  if (lane == 0) s.prof_acc[AP_T1] = __builtin_amdgcn_s_memrealtime();
+  wsync();
+  if (lane < NPHASE && w < PROF_WORLDS) g_prof_adj[w][lane] = s.prof_acc[lane];
+#endif
 }
 
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
@@ -804,6 +897,7 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work) {
   if (nw <= 0) return 0;
+  if (reinterpret_cast<uintptr_t>(tape) & 15u) return (int)hipErrorInvalidValue;  // 16-byte copies of the factors
   const int* perm = nullptr;
   if (work) {  // the dispatch order, heaviest worlds first
     const int rc = launch_order_adj(st, nw, nsub, tape, work);
@@ -815,5 +909,15 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
   return (int)hipGetLastError();
 }
 size_t adjoint_lds_bytes() { return sizeof(Adj); }
+
+int prof_read_adj(unsigned long long* out, int nw) {  // the G1_PROFILE build's adjoint phase cycles (nw x NPHASE)
+#ifdef G1_PROFILE
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof_adj), sizeof(unsigned long long) * NPHASE * (size_t)nw);
+#else
+  (void)out;
+  (void)nw;
+  return -1;
+#endif
+}
 
 }  // namespace g1k

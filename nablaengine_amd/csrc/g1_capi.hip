@@ -12,6 +12,7 @@ size_t order_work_bytes(int nw);
 size_t forward_lds_bytes();
 size_t adjoint_lds_bytes();
 int prof_read(unsigned long long* out, int nw);
+int prof_read_adj(unsigned long long* out, int nw);
 int launch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, int iterations, const int* info,
                     const float* tape);
 int launch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float* gq, const float* gv, const float* gu,
@@ -96,6 +97,7 @@ int dk_fwd_upload(const float* consts, hipStream_t st) {
 
 // the profiling build's per-world phase cycles of the last forward (test and measurement helper; -1 in production)
 int dk_prof_read(unsigned long long* out, int nw) { return g1k::prof_read(out, nw); }
+int dk_prof_read_adj(unsigned long long* out, int nw) { return g1k::prof_read_adj(out, nw); }
 
 void dk_fwd_sizes(long long* o) {
   o[0] = (long long)g1k::forward_lds_bytes(); o[1] = (long long)g1k::adjoint_lds_bytes(); o[2] = 1472; o[3] = 36;
