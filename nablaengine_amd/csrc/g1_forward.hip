@@ -192,19 +192,35 @@ __device__ void smooth(Sim& s, int lane) {
   }
   wsync();
   PROF(PH_SBF);
-  // subtree sums by masks (lane = body): force, moment about O, spatial inertia
-  float Fs[3] = {0.f, 0.f, 0.f}, Ts[3] = {0.f, 0.f, 0.f}, Js[10];
-  for (int k = 0; k < 10; k++) Js[k] = 0.f;
-  const unsigned sub = lane >= 1 && lane < NB ? cTree.submask[lane] : 0u;
-  for (int c = 1; c < NB; c++) {
-    const float m = (float)((sub >> c) & 1u);
-    for (int k = 0; k < 3; k++) { Fs[k] += m * s.u.sm.F[c][k]; Ts[k] += m * s.u.sm.T[c][k]; }
-    for (int k = 0; k < 10; k++) Js[k] += m * s.u.sm.Ic[c][k];
-  }
-  wsync();
-  if (lane >= 1 && lane < NB) {
-    for (int k = 0; k < 3; k++) { s.u.sm.F[lane][k] = Fs[k]; s.u.sm.T[lane][k] = Ts[k]; }
-    for (int k = 0; k < 10; k++) s.u.sm.Ic[lane][k] = Js[k];
+  // subtree sums per body B of the force, the moment about O and the spatial inertia (16 floats), as the product
+  // T = A V (32 x 32 x 16, A[B][b] = 1 for b in B's subtree, 0 for the world and the padding; V[b] = body b's 16
+  // floats) on the matrix cores: v_mfma_f32_16x16x4f32, lane l giving A[l % 16][l / 16] and V[l / 16][l % 16] and
+  // holding C[4 (l / 16) + e][l % 16]; 2 row tiles, 8 steps of k = 4. Every load is issued before the first store, so
+  // the sums overwrite the bodies' own values in place.
+  {
+    typedef float mfma4 __attribute__((ext_vector_type(4)));
+    const int lr = lane & 15, lk = lane >> 4;
+    float* col = lr < 3 ? &s.u.sm.F[0][lr] : (lr < 6 ? &s.u.sm.T[0][lr - 3] : &s.u.sm.Ic[0][lr - 6]);  // column lr
+    const int cs = lr < 6 ? 4 : 12;  // its stride
+    const unsigned sm[2] = {lr >= 1 ? cTree.submask[lr] : 0u, 16 + lr < NB ? cTree.submask[16 + lr] : 0u};
+    mfma4 acc[2] = {mfma4{0.f, 0.f, 0.f, 0.f}, mfma4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const int kb = 4 * t + lk;  // the body of this lane's k index
+      const bool kin = kb >= 1 && kb < NB;
+      const float x = col[(kin ? kb : 1) * cs];
+      const float bv = kin ? x : 0.f;
+#pragma unroll
+      for (int m = 0; m < 2; m++)
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(kin && ((sm[m] >> kb) & 1u) ? 1.f : 0.f, bv, acc[m], 0, 0, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int B = 16 * m + 4 * lk + e;
+        if (B >= 1 && B < NB) col[B * cs] = acc[m][e];
+      }
   }
   PROF(PH_SSUB);
   // motion subspaces
