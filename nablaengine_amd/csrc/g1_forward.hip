@@ -1009,6 +1009,21 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   wsync();
 }
 
+// The wave's issue priority (s_setprio, 0..3; it changes which of a SIMD's two waves issues first, never a result)
+// from the cycles the world is expected still to need: its mean cycles per substep so far (s_memtime, the shader
+// clock) times the substeps left, one level per PRIO_STEP. The longest remaining work goes first, as the dispatch
+// order's heaviest-first does at launch: a world whose cost the launch's estimate missed (a self contact appearing
+// within the step, more Newton iterations) catches up on its co-resident light world instead of finishing last.
+// 4e5 cycles (about 1.4 mean substeps) was the best of 2e5 .. 1e6 at 4096 worlds.
+constexpr float PRIO_STEP = 4e5f;
+__device__ __forceinline__ void set_priority_by_remaining(unsigned long long t_start, int k, int nsub) {
+  const float rem = (float)(__builtin_amdgcn_s_memtime() - t_start) * (float)(nsub - k) / (float)k;
+  if (rem > 3.f * PRIO_STEP) __builtin_amdgcn_s_setprio(3);
+  else if (rem > 2.f * PRIO_STEP) __builtin_amdgcn_s_setprio(2);
+  else if (rem > PRIO_STEP) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // one world per wave64 (one workgroup of 64 lanes)
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_forward(int nw, const float* __restrict__ qpos, const float* __restrict__ qvel,
                                                 const float* __restrict__ warm, const float* __restrict__ ctrl,
@@ -1038,9 +1053,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   }
 #endif
   wsync();
-  for (int k = 0; k < nsub; k++)
+  const unsigned long long t_start = __builtin_amdgcn_s_memtime();
+  for (int k = 0; k < nsub; k++) {
+    if (k > 0) set_priority_by_remaining(t_start, k, nsub);
     substep(s, lane, iterations, tape ? tape + ((size_t)w * nsub + k) * REC_WORDS : nullptr,
             ocon && k == nsub - 1 ? ocon + (size_t)w * MAXCON * 8 : nullptr);
+  }
   if (lane < NQ) oqpos[(size_t)w * NQ + lane] = s.qpos[lane];
   if (lane < NV) { oqvel[(size_t)w * NV + lane] = s.qvel[lane]; owarm[(size_t)w * NV + lane] = s.qacc[lane]; }
 #ifdef G1_PROFILE
