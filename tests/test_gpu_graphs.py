@@ -68,11 +68,12 @@ def _loss_fn(ffi, cq, cv, kin=False, cx=None):
     return f
 
 
-@pytest.mark.parametrize("kin", [False, True])
-def test_compile_fullgraph(ffi, kin):
-    """torch.compile(fullgraph=True) (aot_eager: the graph, the fake implementations and the autograd through the
-    custom ops, without a code generator) of a loss through step: no graph break; the loss and the qpos, qvel, ctrl
-    gradients bitwise eager's."""
+@pytest.mark.parametrize("kin,backend", [(False, "aot_eager"), (True, "aot_eager"), (False, "inductor")])
+def test_compile_fullgraph(ffi, kin, backend):
+    """torch.compile(fullgraph=True) of a loss through step: no graph break; the qpos, qvel, ctrl gradients bitwise
+    eager's (the reference's compile check). aot_eager (the graph, the fake implementations and the autograd through
+    the custom ops, without a code generator) also gives the loss bitwise; inductor generates its own kernels for the
+    loss's products and sums, so its loss agrees to float32 rounding."""
     import torch
     B = 64
     tin = _inputs(B)
@@ -84,7 +85,7 @@ def test_compile_fullgraph(ffi, kin):
     ex = torch._dynamo.explain(f)(*x)
     assert ex.graph_break_count == 0, ex.break_reasons
     torch._dynamo.reset()
-    cf = torch.compile(f, fullgraph=True, backend="aot_eager")
+    cf = torch.compile(f, fullgraph=True, backend=backend)
     x = [t.clone().requires_grad_(i in (0, 1, 3)) for i, t in enumerate(tin)]
     lc = cf(*x)
     lc.backward()
@@ -92,6 +93,6 @@ def test_compile_fullgraph(ffi, kin):
     le = f(*x2)
     le.backward()
     torch.cuda.synchronize()
-    assert torch.equal(lc, le)
+    assert torch.equal(lc, le) if backend == "aot_eager" else torch.allclose(lc, le, rtol=1e-5, atol=0)
     for i in (0, 1, 3):
         assert torch.equal(x[i].grad, x2[i].grad), i
