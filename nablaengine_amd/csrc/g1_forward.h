@@ -28,8 +28,9 @@ struct __align__(16) Sim {
     struct { float gx[NGEOM][4], gq[NGEOM][4]; float stage[MAXCON][16]; unsigned short cand[NPAIR + 2]; } col;
     struct {
       float bw[NB][8];  // body spatial velocity of a dof vector: angular (0..2), velocity of O (4..6)
-      struct { float psi[16][8]; float U[48][16]; } h;  // Hessian: a batch of self-contact rows (<= 16);
-                                                         // U's rows past the dofs zero (MFMA tiles of 16)
+      struct { float psi[16][8]; float U[48][17]; } h;  // Hessian: a batch of self-contact rows (<= 16);
+                                                         // U's rows past the dofs zero (MFMA tiles of 16); rows
+                                                         // padded to 17 floats: no LDS bank conflicts down a column
     } nt;
   } u;
 };
