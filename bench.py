@@ -66,7 +66,14 @@ def cpu_baseline(seconds=10.0):
         oracle.step(**st, **oracle.ENGINE)
         n += 1
     dt = time.perf_counter() - t0
-    return dict(value=64 * n / dt, unit="world-steps/s", cores=1, kind="port",
+    cpu = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return dict(value=64 * n / dt, unit="world-steps/s", cores=1, kind="port", cpu=cpu,
+                host_threads=len(os.sched_getaffinity(0)),
                 sample=f"{n} x 64 config-0 worlds (float64 CPU restatement, not MuJoCo; Newton 10 it, tol 1e-8), "
                        f"{dt:.1f} s, ms per 64-world step {1e3 * dt / n:.2f}")
 
