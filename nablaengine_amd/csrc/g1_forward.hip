@@ -646,14 +646,36 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
       }
     }
     wsync();
-    if (lane < 48) {  // U[i][r] = sigma_r(i) S_i . psi_r; rows past the dofs zero
+    {  // U[i][r] = sigma_r(i) S_i . psi_r (rows past the dofs zero): S Psi' (48 x 8 x 16, S's rows with its two
+       // unused slots 3 and 7 as zero columns) on the matrix cores, 3 row tiles x 2 k-steps, then the signs
+      const int ln = opaque_lane(lane);
+      const int lr = ln & 15, lk = ln >> 4;
+      const float* pr = s.u.nt.h.psi[lr];  // this lane's column r = lr
+      const int b1r = __float_as_int(pr[6]), b2r = __float_as_int(pr[7]);
+      float bv[2];
 #pragma unroll
-      for (int r = 0; r < 4 * SELF_BATCH; r++) {
-        const float* o = s.u.nt.h.psi[r];
-        const int b1 = __float_as_int(o[6]), b2 = __float_as_int(o[7]);
-        const float sg = (float)((int)((dm >> b2) & 1u) - (int)((dm >> b1) & 1u));
-        s.u.nt.h.U[lane][r] =
-            lane < NV ? sg * (w[0] * o[0] + w[1] * o[1] + w[2] * o[2] + v[0] * o[3] + v[1] * o[4] + v[2] * o[5]) : 0.f;
+      for (int kk = 0; kk < 2; kk++) {
+        const int k = 4 * kk + lk;  // S's slot; psi's 0..5 are S's 0..2, 4..6
+        const float x = pr[k < 3 ? k : (k < 7 ? k - 1 : 0)];
+        bv[kk] = (k == 3 || k == 7) ? 0.f : x;
+      }
+#pragma unroll
+      for (int t = 0; t < 3; t++) {
+        const int ia = 16 * t + lr, ic = ia < NV ? ia : 0;
+        mfma4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+          const int k = 4 * kk + lk;
+          const float x = s.S[ic][k];
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ia < NV && k != 3 && k != 7 ? x : 0.f, bv[kk], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int i = 16 * t + 4 * lk + e;
+          const unsigned di = s.dsub[i];  // 0 past the dofs
+          const float sg = (float)((int)((di >> b2r) & 1u) - (int)((di >> b1r) & 1u));
+          s.u.nt.h.U[i][lr] = sg * acc[e];
+        }
       }
     }
     wsync();
