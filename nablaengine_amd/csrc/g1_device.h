@@ -238,8 +238,24 @@ __device__ __forceinline__ float dot3(const float* a, const float* b) { return a
 // lower, TRI layout, followed by the 64-float sink at LSINK). Lane j's registers c[m] for m < j hold other entries of the matrix (loaded from in-bounds
 // addresses, not zeroed): they are updated from one another only, never broadcast (a broadcast reads lane m's c[k],
 // k > m) and never stored, so the valid entries do not depend on them.
-template <bool SPARSE>
+// The fill that contacts between robot bodies of the common kinds add to the tree's sparsity: a leg against the
+// waist or its own arm, or the two legs. H gains entries between the non-shared dofs of the two chains, and
+// eliminating leaf-first spreads them to the rows of the later (higher) chain and of the shared ancestors in
+// between: rows 18-27 gain columns 6-11 (left leg against waist / left arm), rows 18-20 and 28-34 gain 12-17 (right
+// leg against waist / right arm), rows 12-17 gain 6-11 (the legs; also the fill of both arm kinds together, coupled
+// through the waist). Other kinds use the dense routine.
+__host__ __device__ constexpr uint64_t fill_bits(int k) {
+  uint64_t m = 0;
+  if (k >= 18 && k <= 27) m |= 0xFC0ull;                                 // columns 6..11
+  if ((k >= 18 && k <= 20) || (k >= 28 && k <= 34)) m |= 0x3F000ull;     // columns 12..17
+  if (k >= 12 && k <= 17) m |= 0xFC0ull;                                 // columns 6..11
+  return m;
+}
+static_assert(NV == 35, "the fill rows are the G1's dof ranges");
+
+template <int PATTERN>  // 0: the tree's sparsity; 1: with the common self-contact fill; 2: every pair
 __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
+  constexpr bool SPARSE = PATTERN < 2;
   const int lane = opaque_lane(lane_);
   // column j = lane of the lower triangle: A[m][j] = col[tri(m, 0)] for m >= j; every lane's address inside the
   // matrix (lanes past the column select 0), all the loads issued before the elimination
@@ -256,10 +272,10 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
     float bc[NV];
 #pragma unroll
     for (int m = 0; m < k; m++)
-      if (!SPARSE || ((TREE.dofanc[k] >> m) & 1ull)) bc[m] = rdl(c[k], m);  // compile-time ancestor test
+      if (!SPARSE || (((TREE.dofanc[k] | (PATTERN ? fill_bits(k) : 0ull)) >> m) & 1ull)) bc[m] = rdl(c[k], m);
 #pragma unroll
-    for (int m = 0; m < k; m++)
-      if (!SPARSE || ((TREE.dofanc[k] >> m) & 1ull)) c[m] = fmaf(-c[k], bc[m], c[m]);  // A[m][j] -= L[k][j] L[k][m]
+    for (int m = 0; m < k; m++)  // A[m][j] -= L[k][j] L[k][m] (the pattern's test at compile time)
+      if (!SPARSE || (((TREE.dofanc[k] | (PATTERN ? fill_bits(k) : 0ull)) >> m) & 1ull)) c[m] = fmaf(-c[k], bc[m], c[m]);
   }
   // lane j stores column j's entries m >= j; the other lanes store into their sink slot (no branch per store)
 #pragma unroll

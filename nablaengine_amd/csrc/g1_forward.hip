@@ -26,12 +26,14 @@ namespace g1k {
 
 // factor the packed matrix in s.L in place as L' L; dense when a contact couples two robot bodies (cross-branch
 // entries), else with the tree's sparsity
-__device__ __forceinline__ void factor_L(Sim& s, int lane, bool dense = false) {
+// pattern: 0 the tree's sparsity, 1 with the common self-contact fill, 2 dense (hessian()'s classification)
+__device__ __forceinline__ void factor_L(Sim& s, int lane, int pattern = 0) {
 #ifdef G1_PROFILE
-  if (dense && lane == 0) s.prof_acc[PH_DENSE] += 1;
+  if (pattern != 0 && lane == 0) s.prof_acc[PH_DENSE] += 1;
 #endif
-  if (dense) ltl_factor<false>(s.L, lane);
-  else ltl_factor<true>(s.L, lane);
+  if (pattern == 0) ltl_factor<0>(s.L, lane);
+  else if (pattern == 1) ltl_factor<1>(s.L, lane);
+  else ltl_factor<2>(s.L, lane);
   wsync();
 }
 
@@ -554,8 +556,8 @@ __device__ __forceinline__ void contact_stiffness(const Rows& R, const float* dd
   K[15] = Kf[0][0]; K[16] = Kf[1][1]; K[17] = Kf[2][2]; K[18] = Kf[0][1]; K[19] = Kf[0][2]; K[20] = Kf[1][2];
 }
 
-// H = M + J' D J on the rows with x < 0, packed into s.L (lane i writes row i); returns whether a contact between two
-// robot bodies put entries outside the tree's sparsity.
+// H = M + J' D J on the rows with x < 0, packed into s.L (lane i writes row i); returns the factorization pattern its
+// contacts between robot bodies need (factor_L: 0 the tree's sparsity, 1 the common self-contact fill, 2 dense).
 //   Floor contacts: J'CJ of a contact on body B is S_i' K S_j on every pair of dofs moving B, with K = Phi' C Phi its
 //   6x6 stiffness about O. The contacts are summed per body by wave reductions (one pass per distinct body, usually
 //   the two feet); dof i accumulates (n, f) = (sum of K over the bodies it moves) S_i, and H[i][j] = S_j . (n, f) on
@@ -563,7 +565,7 @@ __device__ __forceinline__ void contact_stiffness(const Rows& R, const float* dd
 //   Contacts between two robot bodies: J'CJ = sum over the active pyramid edges t of u_t u_t', u_t = sqrt(D) J' e_t,
 //   u_t[d] = sigma_d S_d . (r x e_t, e_t) with sigma_d = (dof d moves body 2) - (dof d moves body 1); added as
 //   U U' on the matrix cores (fp32 MFMA), SELF_BATCH contacts (4 edges each) a batch.
-__device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool con) {
+__device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con) {
   float d[4];
 #pragma unroll
   for (int t = 0; t < 4; t++) d[t] = (con && t < R.nr && R.jar[t] < 0.f) ? R.D : 0.f;
@@ -705,7 +707,19 @@ __device__ __forceinline__ bool hessian(Sim& s, const Rows& R, int lane, bool co
     wsync();
   }
   wsync();
-  return selfm != 0ull;
+  // the factorization's pattern from the active contacts between robot bodies (body x < y): none when x is y's
+  // ancestor (the coupling stays on y's chain); the common fill for a leg against the waist or its own arm, or the two
+  // legs; else dense
+  int cls = 0;
+  if (act && R.b1 != 0) {
+    const int x = min(R.b1, R.b2), y = max(R.b1, R.b2);
+    const bool anc = x == 1 || ((s.dsub[x + 4] >> y) & 1u);  // body x >= 2 has the one dof x + 4
+    const bool legl = x >= 2 && x <= 7, legr = x >= 8 && x <= 13;
+    const bool common = (legl && y >= 8 && y <= 23) || (legr && ((y >= 14 && y <= 16) || y >= 24));
+    cls = anc ? 0 : common ? 1 : 2;
+  }
+  const unsigned all = wor((unsigned)cls);
+  return all == 0u ? 0 : (all & 2u) ? 2 : 1;
 }
 
 
@@ -739,9 +753,9 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
     if (zsame) {  // no row changed its zone in the last step: H, and so its factor in s.L, are unchanged
       p = ltl_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     } else {
-      const bool dense = hessian(s, R, lane, con);
+      const int pattern = hessian(s, R, lane, con);
       PROF(PH_HESS);
-      factor_L(s, lane, dense);
+      factor_L(s, lane, pattern);
       PROF(PH_FACTOR);
       p = ltl_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     }
@@ -969,8 +983,8 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   if (lane == 0) s.niter = no.it;
   if (rec) {  // the final zones, and H's factor at them (assembled again when the last step changed a zone)
     if (!no.fresh) {
-      const bool dense = hessian(s, R, lane, con);
-      factor_L(s, lane, dense);
+      const int pattern = hessian(s, R, lane, con);
+      factor_L(s, lane, pattern);
     }
     tape_put(rec + REC_LH, s.L, NTRI, REC_LQ - REC_LH, lane);
     unsigned cz = 0u;
