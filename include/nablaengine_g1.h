@@ -58,6 +58,10 @@ int dk_torch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float
 /* Replaces <unit>_upload (jax_ffi.py:214-225): the model constants are compiled into this library, so the call only
  * checks that the current device can run the kernels; consts may be NULL. */
 int dk_fwd_upload(const float* consts, hipStream_t st);
+/* Replaces <unit>_launch (jax_ffi.py:243-254): the adjoint's launch on device dev, o[0] the LDS bytes k_adjoint
+ * takes per world (static: the kernel needs no dynamic LDS and no opt-in), o[1] its resident worlds per CU
+ * (hipOccupancyMaxActiveBlocksPerMultiprocessor); the current device is restored. Returns 0 or a hipError_t. */
+int dk_fwd_launch(int dev, long long* o);
 /* Replaces <unit>_sizes (jax_ffi.py:255-258): o[0..8] = LDS bytes of the forward, of the adjoint, tape words per
  * world and substep, nq, nv, max contacts, clamp_kv, normal, the tape's flags word offset (o[6], o[7] -1: runtime). */
 void dk_fwd_sizes(long long* o);
@@ -94,12 +98,14 @@ int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const f
 long long dk_adjoint_work_bytes(int nw);
 
 /* The reference's per-variant unit names (jax_ffi.py:180,845-846: dk_kv{0,1,2}_n{0..3}), each the entry above with
- * its (clamp_kv, normal) fixed; _upload and _sizes as dk_fwd_upload / dk_fwd_sizes (o[6], o[7] the variant). */
+ * its (clamp_kv, normal) fixed; _upload, _launch and _sizes as dk_fwd_upload / dk_fwd_launch / dk_fwd_sizes (o[6],
+ * o[7] the variant). */
 #define DK_VARIANT_DECL(KV, N)                                                                                       \
   int dk_kv##KV##_n##N##_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric,            \
                                   const float* com, const float* gq_out, const float* gv_out, float* gq_in,          \
                                   float* gv_in, float* gctrl, int* info, const float* ctrl, float clamp_soft);       \
   int dk_kv##KV##_n##N##_upload(const float* consts, hipStream_t st);                                                \
+  int dk_kv##KV##_n##N##_launch(int dev, long long* o);                                                              \
   void dk_kv##KV##_n##N##_sizes(long long* o);
 DK_VARIANT_DECL(0, 0) DK_VARIANT_DECL(0, 1) DK_VARIANT_DECL(0, 2) DK_VARIANT_DECL(0, 3)
 DK_VARIANT_DECL(1, 0) DK_VARIANT_DECL(1, 1) DK_VARIANT_DECL(1, 2) DK_VARIANT_DECL(1, 3)

@@ -798,8 +798,11 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
         if (clamp_kv == 0) { wq = 0.f; wv = 1.f; }
         else if (clamp_kv == 1) { wq = wv = 0.f; }
         else {
+          // w = exp(-o / delta), o = max((|f| - tau) / tau, 0) the relative overshoot of the unclamped PD force
+          // (adjoint.py:811-829): a dof the tape marks clamped whose recomputed f rounds to inside its bound gets
+          // o = 0, w = 1, never w > 1
           const float raw = cKp[j] * (s.ctrl[j - 6] - s.qpos[j + 1]) - cKv[j] * s.qvel[j];
-          const float ov = (fabsf(raw) - cFrclim[j]) / cFrclim[j];
+          const float ov = fmaxf((fabsf(raw) - cFrclim[j]) / cFrclim[j], 0.f);
           wq = wv = clamp_soft > 0.f ? expf(-ov / clamp_soft) : 0.f;
         }
       }
@@ -909,6 +912,17 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
   return (int)hipGetLastError();
 }
 size_t adjoint_lds_bytes() { return sizeof(Adj); }
+
+// k_adjoint's resident workgroups (worlds) per CU on device dev, the current device restored afterwards
+int adjoint_occupancy(int dev, int* n) {
+  int old = -1;
+  hipError_t e = hipGetDevice(&old);
+  if (e != hipSuccess) return (int)e;
+  if ((e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(n, k_adjoint, 64, 0);
+  const hipError_t e2 = hipSetDevice(old);
+  return (int)(e != hipSuccess ? e : e2);
+}
 
 int prof_read_adj(unsigned long long* out, int nw) {  // the G1_PROFILE build's adjoint phase cycles (nw x NPHASE)
 #ifdef G1_PROFILE

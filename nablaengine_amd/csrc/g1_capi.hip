@@ -11,6 +11,7 @@ int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work);
 size_t order_work_bytes(int nw);
 size_t forward_lds_bytes();
 size_t adjoint_lds_bytes();
+int adjoint_occupancy(int dev, int* n);
 int prof_read(unsigned long long* out, int nw);
 int prof_read_adj(unsigned long long* out, int nw);
 int launch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, int iterations, const int* info,
@@ -99,6 +100,15 @@ int dk_fwd_upload(const float* consts, hipStream_t st) {
 int dk_prof_read(unsigned long long* out, int nw) { return g1k::prof_read(out, nw); }
 int dk_prof_read_adj(unsigned long long* out, int nw) { return g1k::prof_read_adj(out, nw); }
 
+int dk_fwd_launch(int dev, long long* o) {
+  o[0] = (long long)g1k::adjoint_lds_bytes();
+  o[1] = 0;
+  int n = 0;
+  const int rc = g1k::adjoint_occupancy(dev, &n);
+  o[1] = rc ? 0 : n;
+  return rc;
+}
+
 void dk_fwd_sizes(long long* o) {
   o[0] = (long long)g1k::forward_lds_bytes(); o[1] = (long long)g1k::adjoint_lds_bytes(); o[2] = 1472; o[3] = 36;
   o[4] = 35; o[5] = 64; o[6] = -1; o[7] = -1; o[8] = 1;
@@ -131,6 +141,7 @@ int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float*
                       N);                                                                                            \
   }                                                                                                                  \
   int dk_kv##KV##_n##N##_upload(const float* consts, hipStream_t st) { return dk_fwd_upload(consts, st); }          \
+  int dk_kv##KV##_n##N##_launch(int dev, long long* o) { return dk_fwd_launch(dev, o); }                             \
   void dk_kv##KV##_n##N##_sizes(long long* o) {                                                                      \
     dk_fwd_sizes(o);                                                                                                 \
     o[6] = KV;                                                                                                       \

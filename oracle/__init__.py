@@ -47,10 +47,14 @@ def lib():
         ip = ctypes.POINTER(ctypes.c_int)
         L.g1o_step.argtypes = [ctypes.c_int, dp, dp, dp, dp, dp, dp, ctypes.c_int, ctypes.c_double, ctypes.c_int,
                                ctypes.c_double, ctypes.c_int, dp, dp, dp, ip, dp]
+        L.g1o_step_ex.argtypes = L.g1o_step.argtypes + [dp, dp, ctypes.c_int]
+        L.g1o_step_mt.argtypes = [ctypes.c_int] + L.g1o_step.argtypes[:-1]
         L.g1o_smooth.argtypes = [dp] * 9
         L.g1o_vjp.argtypes = [ctypes.c_int, dp, dp, dp, dp, dp, dp, ctypes.c_int, ctypes.c_double, ctypes.c_int,
                               ctypes.c_double, ctypes.c_int, dp, dp, ctypes.c_int, ctypes.c_int, ctypes.c_double, dp, dp,
                               dp]
+        L.g1o_vjp_ex.argtypes = (L.g1o_vjp.argtypes[:17] + [ctypes.c_double, ctypes.c_double]
+                                 + L.g1o_vjp.argtypes[17:])
         L.g1o_contacts.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp]
         L.g1o_kinematics.argtypes = [ctypes.c_int] + [dp] * 8
         _lib = L
@@ -72,9 +76,13 @@ TRUTH = dict(iterations=2000, tol=1e-13, ls_max=100, ls_tol=1e-12)
 
 
 def step(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4,
-         flops=False):
+         flops=False, qfrc=None, freeze=None, freeze_mode=0):
     """One control step of B worlds in float64: (qpos' (B, 36), qvel' (B, 35), warm' (B, 35), info (B, 4) int32),
-    and with flops=True the algorithmic flops of each world-step (B,) last."""
+    and with flops=True the algorithmic flops of each world-step (B,) last.
+
+    The checker's hooks (inert by default): qfrc (B, 35) a generalized force added to qfrc_smooth in every substep;
+    freeze (npair, 3) float64 array and freeze_mode 1 / 2: record / replay the segment parameters of the
+    capsule-capsule pairs whose both parameters are free (one world per call)."""
     qpos = _c(qpos, (-1, NQ))
     B = qpos.shape[0]
     qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
@@ -82,25 +90,49 @@ def step(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=
     oq, ov, ow = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NV))
     info = np.empty((B, 4), np.int32)
     fl = np.empty(B)
-    lib().g1o_step(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
-                   int(ls_max), float(ls_tol), int(nsub), _p(oq), _p(ov), _p(ow),
-                   info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), _p(fl))
+    qf = None if qfrc is None else _c(qfrc, (B, NV))
+    if freeze is not None:
+        assert B == 1 and freeze.dtype == np.float64 and freeze.flags.c_contiguous
+    lib().g1o_step_ex(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
+                      int(ls_max), float(ls_tol), int(nsub), _p(oq), _p(ov), _p(ow),
+                      info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), _p(fl), None if qf is None else _p(qf),
+                      None if freeze is None else _p(freeze), int(freeze_mode))
     return (oq, ov, ow, info, fl) if flops else (oq, ov, ow, info)
 
 
+def step_mt(threads, qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7,
+            nsub=4):
+    """``step`` on ``threads`` host threads (contiguous shares of the worlds; the same results)."""
+    qpos = _c(qpos, (-1, NQ))
+    B = qpos.shape[0]
+    qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
+    friction, com = _c(friction, (B,)), _c(com, (B, 3))
+    oq, ov, ow = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NV))
+    info = np.empty((B, 4), np.int32)
+    lib().g1o_step_mt(int(threads), B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations),
+                      float(tol), int(ls_max), float(ls_tol), int(nsub), _p(oq), _p(ov), _p(ow),
+                      info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    return oq, ov, ow, info
+
+
+NPAIR = 502  # the model's collision pairs (the freeze hook's table rows)
+
+
 def vjp(qpos, qvel, warm, ctrl, friction, com, g_qpos, g_qvel, clamp_kv=1, normal=0, clamp_soft=0.2, iterations=10,
-        tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4):
+        tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4, normal_eps=1e-3, parallel_eps=1.2e-3):
     """Analytic VJP of one control step in float64 (the oracle's adjoint): (g_qpos (B, 36) qpos form, g_qvel (B, 35),
-    g_ctrl (B, 29)) from the output cotangents (g_qpos' (B, 36) qpos form, g_qvel' (B, 35))."""
+    g_ctrl (B, 29)) from the output cotangents (g_qpos' (B, 36) qpos form, g_qvel' (B, 35)). normal_eps and
+    parallel_eps are the eps of the normal options 2 / 3 and the near-parallel rule's sin^2 threshold (the reference's
+    compile-time 1e-3 m and 1.2e-3, which the GPU library uses); the checker varies them to pin the options."""
     qpos = _c(qpos, (-1, NQ))
     B = qpos.shape[0]
     qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
     friction, com = _c(friction, (B,)), _c(com, (B, 3))
     gq, gv = _c(g_qpos, (B, NQ)), _c(g_qvel, (B, NV))
     oq, ov, ou = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NU))
-    lib().g1o_vjp(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
-                  int(ls_max), float(ls_tol), int(nsub), _p(gq), _p(gv), int(clamp_kv), int(normal), float(clamp_soft),
-                  _p(oq), _p(ov), _p(ou))
+    lib().g1o_vjp_ex(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
+                     int(ls_max), float(ls_tol), int(nsub), _p(gq), _p(gv), int(clamp_kv), int(normal),
+                     float(clamp_soft), float(normal_eps), float(parallel_eps), _p(oq), _p(ov), _p(ou))
     return oq, ov, ou
 
 
@@ -127,6 +159,39 @@ def fd_jacobian(qpos, qvel, warm, ctrl, friction, com, h=1e-6, **kw):
                         np.tile(com, (n, 1)), **kw)
     out = np.concatenate([oq, ov], 1).reshape(2 * NV + NU, 2, NQ + NV)
     return (out[:, 0] - out[:, 1]).T / (2 * h)
+
+
+def fd_vjp(qpos, qvel, warm, ctrl, friction, com, g_qpos, g_qvel, h=1e-6, threads=None, **kw):
+    """Central-difference VJPs of B states' control steps, (B, 99) in the columns (qpos tangent 35 | qvel 35 |
+    ctrl 29): the cotangents (g_qpos (B, 36) qpos form | g_qvel (B, 35)) times ``fd_jacobian``'s columns, all
+    198 B perturbed steps in one ``step_mt`` call on ``threads`` host threads (default: the usable cores, at most 16)."""
+    import os
+    qpos = _c(qpos, (-1, NQ))
+    B = qpos.shape[0]
+    qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
+    friction, com = _c(friction, (B,)), _c(com, (B, 3))
+    n = 2 * NV + NU
+    Q = np.repeat(qpos, 2 * n, axis=0).reshape(B, n, 2, NQ)
+    V = np.repeat(qvel, 2 * n, axis=0).reshape(B, n, 2, NV)
+    U = np.repeat(ctrl, 2 * n, axis=0).reshape(B, n, 2, NU)
+    for j in range(NV):
+        for s, sg in ((0, 1.0), (1, -1.0)):
+            d = np.zeros((B, NV))
+            d[:, j] = sg * h
+            Q[:, j, s] = integrate_pos(qpos, d)
+            V[:, NV + j, s, j] += sg * h
+    for j in range(NU):
+        U[:, 2 * NV + j, 0, j] += h
+        U[:, 2 * NV + j, 1, j] -= h
+    if threads is None:
+        threads = min(16, len(os.sched_getaffinity(0)))
+    rep = lambda a: np.repeat(a, 2 * n, axis=0)
+    oq, ov, _, _ = step_mt(threads, Q.reshape(-1, NQ), V.reshape(-1, NV), rep(warm), U.reshape(-1, NU), rep(friction),
+                           rep(com), **kw)
+    out = np.concatenate([oq, ov], 1).reshape(B, n, 2, NQ + NV)
+    J = (out[:, :, 0] - out[:, :, 1]) / (2 * h)  # (B, 99, 71): d output / d input column
+    c = np.concatenate([_c(g_qpos, (B, NQ)), _c(g_qvel, (B, NV))], 1)
+    return np.einsum("bio,bo->bi", J, c)
 
 
 def smooth(qpos, qvel, ctrl, com):

@@ -20,6 +20,8 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <thread>
+#include <vector>
 
 #include "../nablaengine_amd/csrc/g1_model.h"
 
@@ -51,7 +53,26 @@ struct World {
   double aadv[NV];    // implicitfast's a_adv of the last substep
   bool clamped[NV];   // dofs whose actuator force is at its limit
   double flops;  // algorithmic flops of the world-step so far (the closed-form phase counts, see count_* below)
+  // The checker's own hooks, inert at their defaults (no part of the reference's step): qfrc, a generalized force
+  // added to qfrc_smooth (NV, or NULL), so that finite differences in it measure the adjoint's lambda; freeze, per
+  // capsule-capsule pair (flag, x1, x2): with freeze_mode 1 the forward records the segment parameters of every pair
+  // whose both parameters are free, with 2 it uses the recorded ones instead of solving for them (the forward in
+  // which the near-parallel rule's held parameters are exact); normal_eps, parallel_eps: the eps of the normal
+  // options 2 and 3 (1e-3 m) and the near-parallel rule's sin^2 threshold (1.2e-3), the reference's
+  // DK_ADJ_NORMAL_EPS / DK_ADJ_PARALLEL_EPS (adjoint_contact.py:76-95).
+  const double* qfrc;
+  double (*freeze)[3];
+  int freeze_mode;
+  double normal_eps, parallel_eps;
 };
+
+void init_hooks(World& s) {
+  s.qfrc = nullptr;
+  s.freeze = nullptr;
+  s.freeze_mode = 0;
+  s.normal_eps = 1e-3;
+  s.parallel_eps = 1.2e-3;
+}
 
 inline void qmul(const double* a, const double* b, double* o) {
   double w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];
@@ -268,7 +289,7 @@ void smooth(World& s, const double* ctrl) {
     } else {
       s.clamped[i] = false;
     }
-    s.qsm[i] = act - bias[i];
+    s.qsm[i] = act - bias[i] + (s.qfrc ? s.qfrc[i] : 0.0);
   }
   chol_solve(s.M, s.qsm, s.qacc0);
 }
@@ -394,6 +415,11 @@ void collide_pair(World& s, int pair) {
   };
   if (std::fabs(det) >= 1e-15) {
     double x1 = (mc * u - mb * v) / det, x2 = (ma * v - mb * u) / det;
+    if (s.freeze && x1 >= -1 && x1 <= 1 && x2 >= -1 && x2 <= 1) {  // both free: the checker's freeze hook
+      double* fz = s.freeze[pair];
+      if (s.freeze_mode == 1) { fz[0] = 1; fz[1] = x1; fz[2] = x2; }
+      else if (s.freeze_mode == 2 && fz[0] != 0) { x1 = fz[1]; x2 = fz[2]; }
+    }
     if (x1 > 1) { x1 = 1; x2 = (v - mb) / mc; }
     else if (x1 < -1) { x1 = -1; x2 = (v + mb) / mc; }
     if (x2 > 1 || x2 < -1) {
@@ -772,9 +798,8 @@ void imp_d(const double* solimp, double pos, double* imp, double* dimp) {
 }
 
 // the normal derivative's factor kappa(nu) (1 / nu exact; the reference's options 1-3: frozen, regularized, frozen
-// below 1e-3 m)
-double kappa(double nu, int normal) {
-  const double eps = 1e-3;
+// below eps = 1e-3 m; adjoint_contact.py:239-249 adj_kappa)
+double kappa(double nu, int normal, double eps) {
   if (normal == 0) return 1.0 / nu;
   if (normal == 1) return 0.0;
   if (normal == 2) return 1.0 / std::fmax(nu, eps);
@@ -803,7 +828,7 @@ void make_frame_vjp(const double* n, const double* frb, double* nb) {
 
 // sphere core VJP: (dist, pos, n) = sphere_sphere(p1, r1, p2, r2) with cotangents db, posb, nb -> p1b, p2b
 void sphere_core_vjp(const double* p1, double r1, const double* p2, double r2, double db, const double* posb,
-                     const double* nb, int normal, double* p1b, double* p2b) {
+                     const double* nb, int normal, double eps, double* p1b, double* p2b) {
   double dl[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
   double l = std::sqrt(dot3(dl, dl));
   double dlb[3] = {0, 0, 0};
@@ -811,7 +836,7 @@ void sphere_core_vjp(const double* p1, double r1, const double* p2, double r2, d
   if (l > 0) {
     double n[3] = {dl[0] / l, dl[1] / l, dl[2] / l}, nt[3];
     for (int k = 0; k < 3; k++) nt[k] = nb[k] + 0.5 * (r1 - r2) * posb[k];
-    double nn = dot3(n, nt), kap = kappa(l, normal);
+    double nn = dot3(n, nt), kap = kappa(l, normal, eps);
     for (int k = 0; k < 3; k++) dlb[k] += kap * (nt[k] - n[k] * nn) + n[k] * db;
   }
   for (int k = 0; k < 3; k++) { p1b[k] -= dlb[k]; p2b[k] += dlb[k]; }
@@ -857,7 +882,7 @@ void contact_geom_vjp(const World& s, const Contact& c, double db, const double*
   double nb[3] = {0, 0, 0};
   make_frame_vjp(c.frame, frb, nb);
   if (ty1 == 2 && ty2 == 2) {
-    sphere_core_vjp(p1, sz1[0], p2, sz2[0], db, posb, nb, normal, x1b, x2b);
+    sphere_core_vjp(p1, sz1[0], p2, sz2[0], db, posb, nb, normal, s.normal_eps, x1b, x2b);
     return;
   }
   if (ty1 == 2 && ty2 == 3) {
@@ -867,7 +892,7 @@ void contact_geom_vjp(const World& s, const Contact& c, double db, const double*
     double gam = dot3(ab, ab) + 1e-6, raw = dot3(ap, ab) / gam, t = std::fmin(std::fmax(raw, 0.0), 1.0);
     for (int k = 0; k < 3; k++) pt[k] = a[k] + t * ab[k];
     double ptb[3] = {0, 0, 0};
-    sphere_core_vjp(p1, sz1[0], pt, sz2[0], db, posb, nb, normal, x1b, ptb);
+    sphere_core_vjp(p1, sz1[0], pt, sz2[0], db, posb, nb, normal, s.normal_eps, x1b, ptb);
     double abb[3], apb[3] = {0, 0, 0}, axb[3], tb = dot3(ptb, ab);
     for (int k = 0; k < 3; k++) abb[k] = t * ptb[k];
     double ab_a[3];
@@ -918,15 +943,16 @@ void contact_geom_vjp(const World& s, const Contact& c, double db, const double*
   }
   double v1[3], v2[3], v1b[3] = {0, 0, 0}, v2b[3] = {0, 0, 0};
   for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
-  sphere_core_vjp(v1, sz1[0], v2, sz2[0], db, posb, nb, normal, v1b, v2b);
+  sphere_core_vjp(v1, sz1[0], v2, sz2[0], db, posb, nb, normal, s.normal_eps, v1b, v2b);
   double a1b[3], a2b[3], db3[3] = {0, 0, 0};
   for (int k = 0; k < 3; k++) { x1b[k] += v1b[k]; x2b[k] += v2b[k]; a1b[k] = x1 * v1b[k]; a2b[k] = x2 * v2b[k]; }
   double x1bar = dot3(a1, v1b), x2bar = dot3(a2, v2b);
-  // near-parallel rule (normal options != 0): both parameters held where sin^2(theta) < 1.2e-3
+  // near-parallel rule (normal options != 0; adjoint_contact.py:436-448): both parameters held where
+  // sin^2(theta) < 1.2e-3
   if (mode == 0 && normal != 0) {
     double cr[3];
     cross(a1, a2, cr);
-    if (dot3(cr, cr) < 1.2e-3 * ma * mc) { x1bar = 0; x2bar = 0; }
+    if (dot3(cr, cr) < s.parallel_eps * ma * mc) { x1bar = 0; x2bar = 0; }
   }
   double mab = 0, mbb = 0, mcb = 0, ub = 0, vb = 0;
   if (mode == 0) {
@@ -1170,7 +1196,8 @@ void substep_vjp(World& s, const Rec& rec, const double* ctrl, double* qb, doubl
       else if (clamp_kv == 1) { wq = wv = 0; }
       else {
         double raw = DOF_KP[i] * (ctrl[i - 6] - s.qpos[i + 1]) - DOF_KV[i] * s.qvel[i];
-        double o = (std::fabs(raw) - DOF_FRCLIM[i]) / DOF_FRCLIM[i];
+        // the relative overshoot, floored at 0 (adjoint.py:822-829 lam_soft): w <= 1
+        double o = std::fmax((std::fabs(raw) - DOF_FRCLIM[i]) / DOF_FRCLIM[i], 0.0);
         wq = wv = clamp_soft > 0 ? std::exp(-o / clamp_soft) : 0.0;
       }
     }
@@ -1194,10 +1221,14 @@ extern "C" {
 // per Newton iteration the Hessian assembly 6 k (k + 1) / 2 + 12 k over the contacts with a quadratic row and a
 // factorization 2.86e4, or 2.45e3 for a re-solve, plus 12 sum k + 2.45e3 and 6 R per line-search evaluation), k the
 // contact's support size and R the rows. Returns 0.
-int g1o_step(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
-             const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
-             double* oqpos, double* oqvel, double* owarm, int* info, double* flops) {
+int g1o_step_ex(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
+                const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
+                double* oqpos, double* oqvel, double* owarm, int* info, double* flops, const double* qfrc,
+                double* freeze, int freeze_mode) {
   World* s = new World;
+  init_hooks(*s);
+  s->freeze = reinterpret_cast<double (*)[3]>(freeze);
+  s->freeze_mode = freeze ? freeze_mode : 0;
   for (int w = 0; w < nw; w++) {
     std::memcpy(s->qpos, qpos + (size_t)w * NQ, sizeof(double) * NQ);
     std::memcpy(s->qvel, qvel + (size_t)w * NV, sizeof(double) * NV);
@@ -1206,6 +1237,7 @@ int g1o_step(int nw, const double* qpos, const double* qvel, const double* warm,
     s->fric = fric[w];
     s->flags = 0;
     s->flops = 0;
+    s->qfrc = qfrc ? qfrc + (size_t)w * NV : nullptr;
     for (int k = 0; k < nsub; k++) {
       // smooth dynamics 2.5e4, qacc_smooth factor + solve 3.1e4, implicitfast factor + solve 3.1e4, broadphase 5e3
       s->flops += 2.5e4 + 3.1e4 + 3.1e4 + 5e3;
@@ -1227,11 +1259,39 @@ int g1o_step(int nw, const double* qpos, const double* qvel, const double* warm,
   return 0;
 }
 
+int g1o_step(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
+             const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
+             double* oqpos, double* oqvel, double* owarm, int* info, double* flops) {
+  return g1o_step_ex(nw, qpos, qvel, warm, ctrl, fric, com, iterations, tol, ls_max, ls_tol, nsub, oqpos, oqvel, owarm,
+                     info, flops, nullptr, nullptr, 0);
+}
+
+// g1o_step on nthreads host threads, each taking a contiguous share of the worlds (the CPU baseline's all-threads
+// leg; results identical to g1o_step's, every world being independent).
+int g1o_step_mt(int nthreads, int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
+                const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
+                double* oqpos, double* oqvel, double* owarm, int* info) {
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > nw) nthreads = nw > 0 ? nw : 1;
+  std::vector<std::thread> pool;
+  for (int t = 0; t < nthreads; t++) {
+    const int a = (int)((long long)nw * t / nthreads), b = (int)((long long)nw * (t + 1) / nthreads);
+    pool.emplace_back([=] {
+      g1o_step(b - a, qpos + (size_t)a * NQ, qvel + (size_t)a * NV, warm + (size_t)a * NV, ctrl + (size_t)a * NU,
+               fric + a, com + (size_t)a * 3, iterations, tol, ls_max, ls_tol, nsub, oqpos + (size_t)a * NQ,
+               oqvel + (size_t)a * NV, owarm + (size_t)a * NV, info ? info + 4 * (size_t)a : nullptr, nullptr);
+    });
+  }
+  for (auto& th : pool) th.join();
+  return 0;
+}
+
 // Smooth dynamics of one state (tests): M (NV x NV dense), qfrc_smooth (NV), qacc_smooth (NV), body poses
 // (xpos (NB, 3), xquat (NB, 4)).
 int g1o_smooth(const double* qpos, const double* qvel, const double* ctrl, const double* com, double* M, double* qsm,
                double* qacc0, double* xpos, double* xquat) {
   World* s = new World;
+  init_hooks(*s);
   std::memcpy(s->qpos, qpos, sizeof(double) * NQ);
   std::memcpy(s->qvel, qvel, sizeof(double) * NV);
   std::memcpy(s->com, com, sizeof(double) * 3);
@@ -1257,6 +1317,7 @@ int g1o_smooth(const double* qpos, const double* qvel, const double* ctrl, const
 int g1o_kinematics(int nw, const double* qpos, const double* qvel, const double* com, double* qn, double* xpos,
                    double* xquat, double* cvel, double* sc) {
   World* s = new World;
+  init_hooks(*s);
   const double zero[NV] = {0};
   for (int w = 0; w < nw; w++) {
     std::memcpy(s->qpos, qpos + (size_t)w * NQ, sizeof(double) * NQ);
@@ -1309,6 +1370,7 @@ int g1o_kinematics(int nw, const double* qpos, const double* qvel, const double*
 int g1o_contacts(const double* qpos, const double* qvel, const double* ctrl, const double* com, double fric,
                  double* out) {
   World* s = new World;
+  init_hooks(*s);
   std::memcpy(s->qpos, qpos, sizeof(double) * NQ);
   std::memcpy(s->qvel, qvel, sizeof(double) * NV);
   std::memcpy(s->com, com, sizeof(double) * 3);
@@ -1332,11 +1394,14 @@ int g1o_contacts(const double* qpos, const double* qvel, const double* ctrl, con
 // outputs gq_out (nw, 36) qpos form, gv_out (nw, 35); gradients gq_in (nw, 36) qpos form (its quaternion part
 // 2 q (x) (0, t) of the tangent cotangent t), gv_in (nw, 35), gu (nw, 29). clamp_kv 0 / 1 / 2, normal 0..3 as the
 // reference's adjoint options; clamp_soft the soft clamp's delta.
-int g1o_vjp(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl, const double* fric,
-            const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub, const double* gq_out,
-            const double* gv_out, int clamp_kv, int normal, double clamp_soft, double* gq_in, double* gv_in,
-            double* gu) {
+int g1o_vjp_ex(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
+               const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
+               const double* gq_out, const double* gv_out, int clamp_kv, int normal, double clamp_soft,
+               double normal_eps, double parallel_eps, double* gq_in, double* gv_in, double* gu) {
   World* s = new World;
+  init_hooks(*s);
+  s->normal_eps = normal_eps;
+  s->parallel_eps = parallel_eps;
   Rec* rec = new Rec[nsub];
   for (int w = 0; w < nw; w++) {
     std::memcpy(s->qpos, qpos + (size_t)w * NQ, sizeof(double) * NQ);
@@ -1387,6 +1452,14 @@ int g1o_vjp(int nw, const double* qpos, const double* qvel, const double* warm, 
   delete[] rec;
   delete s;
   return 0;
+}
+
+int g1o_vjp(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl, const double* fric,
+            const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub, const double* gq_out,
+            const double* gv_out, int clamp_kv, int normal, double clamp_soft, double* gq_in, double* gv_in,
+            double* gu) {
+  return g1o_vjp_ex(nw, qpos, qvel, warm, ctrl, fric, com, iterations, tol, ls_max, ls_tol, nsub, gq_out, gv_out,
+                    clamp_kv, normal, clamp_soft, 1e-3, 1.2e-3, gq_in, gv_in, gu);
 }
 
 }  // extern "C"

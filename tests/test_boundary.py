@@ -22,7 +22,8 @@ def _declared():
     names = {n for n in names if "##" not in n and not n.startswith("dk_kv##")}
     for kv in (0, 1, 2):
         for n in (0, 1, 2, 3):
-            names |= {f"dk_kv{kv}_n{n}_adjoint", f"dk_kv{kv}_n{n}_upload", f"dk_kv{kv}_n{n}_sizes"}
+            names |= {f"dk_kv{kv}_n{n}_adjoint", f"dk_kv{kv}_n{n}_upload", f"dk_kv{kv}_n{n}_sizes",
+                      f"dk_kv{kv}_n{n}_launch"}
     return names
 
 

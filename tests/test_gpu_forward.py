@@ -93,22 +93,29 @@ def test_forward_vs_mujoco_warp_reference_gates(ffi):
     assert np.median(eq) <= 5e-7 and np.percentile(eq, 99) <= 5e-6
 
 
-def test_forward_vs_oracle_synthetic(ffi):
-    """Config-1 states (1024 of them) against the float64 oracle at MuJoCo's truth settings: median relative error of
-    qvel <= 2e-6; and every world finite."""
+@pytest.mark.parametrize("iterations", [10, 50])
+def test_forward_vs_oracle_synthetic(ffi, iterations):
+    """Config-1 states (1024) against the float64 oracle at matched settings: the engine's 10 Newton iterations
+    against the oracle at 10 (oracle.ENGINE), and 50 against the converged oracle (MuJoCo's truth settings). At 10
+    iterations about 6% of these worlds stop at the cap in some substep, so both precisions' unconverged iterates are
+    compared there (the oracle's own 10-iteration result differs from its converged one by p99 1.7e-3 on these
+    states: the tail of a 10-iteration step against the converged one is the cap, tests/test_oracle.py). Gates: qvel
+    median <= 2e-6 and p99 <= 2e-5, qpos median <= 2e-7 and p99 <= 2e-6; every world finite."""
     import torch
     st = synthetic.states(1024, config=1)
-    q1, v1, w1, info = ffi.forward(*_gpu(st))
+    q1, v1, w1, info = ffi.forward(*_gpu(st), iterations=iterations)
     torch.cuda.synchronize()
-    oq, ov, ow, oinfo = oracle.step(**{k: st[k].astype(np.float64) for k in st}, **oracle.TRUTH)
+    ref = oracle.ENGINE if iterations == 10 else oracle.TRUTH
+    oq, ov, ow, oinfo = oracle.step(**{k: st[k].astype(np.float64) for k in st}, **ref)
     v1 = v1.cpu().numpy().astype(np.float64)
     q1 = q1.cpu().numpy().astype(np.float64)
     assert np.isfinite(v1).all() and np.isfinite(q1).all()
     ev, eq = _rel(v1, ov), _rel(q1, oq)
-    print(f"synthetic: qvel median {np.median(ev):.3g} p99 {np.percentile(ev, 99):.3g}; qpos median {np.median(eq):.3g}"
-          f"; contacts max {info[:, 1].max().item()} rows max {info[:, 2].max().item()}")
-    assert np.median(ev) <= 2e-6
-    assert np.median(eq) <= 2e-6
+    print(f"synthetic, {iterations} iterations: qvel median {np.median(ev):.3g} p99 {np.percentile(ev, 99):.3g} max "
+          f"{ev.max():.3g}; qpos median {np.median(eq):.3g} p99 {np.percentile(eq, 99):.3g}; contacts max "
+          f"{info[:, 1].max().item()} rows max {info[:, 2].max().item()}")
+    assert np.median(ev) <= 2e-6 and np.percentile(ev, 99) <= 2e-5
+    assert np.median(eq) <= 2e-7 and np.percentile(eq, 99) <= 2e-6
 
 
 def test_forward_bitwise_deterministic(ffi):

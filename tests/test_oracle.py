@@ -184,20 +184,182 @@ def test_gradient_gate_self_test():
     assert not bad, stats_bad
 
 
-def test_adjoint_variants_differ_where_they_should():
-    """clamp_kv 0 / 1 agree on states without a clamped actuator and differ on clamped ones (G4); the normal options
-    agree on G0 states (no self contact below 1e-3 m)."""
-    g = np.load(os.path.join(GOLD, "grad_mf_s0.npz"))
-    for grp, same in (("G0", True), ("G4", False)):
-        s = int(np.nonzero(g[grp])[0][0])
-        args = [g[k][s:s + 1].astype(np.float64) for k in ("qpos", "qvel", "qacc_warmstart", "ctrl", "friction", "com")]
-        cq, cv = g["cot_qpos"][s, :1].astype(np.float64), g["cot_qvel"][s, :1].astype(np.float64)
-        a = oracle.vjp(*args, cq, cv, clamp_kv=0, normal=0)
-        b = oracle.vjp(*args, cq, cv, clamp_kv=1, normal=0)
-        assert np.allclose(a[1], b[1], rtol=1e-12, atol=1e-12) == same
-        c = oracle.vjp(*args, cq, cv, clamp_kv=1, normal=3)
-        if grp == "G0":
-            assert np.allclose(b[0], c[0], rtol=1e-9, atol=1e-12)
+KP, KV, FRCLIM = (np.asarray(MODEL[k]) for k in ("dof_kp", "dof_kv", "dof_frclim"))
+ONE_SUBSTEP = dict(oracle.TRUTH, nsub=1)
+
+
+def _lam_by_fd(s64, cq, cv, h=1e-6):
+    """lambda of a one-substep step by central differences: the output loss's derivative with respect to a generalized
+    force added to qfrc_smooth (the oracle's qfrc hook). lambda = H^-1 a* bar is that derivative, since qfrc_smooth
+    enters the step only through the constrained solve (its IFT gives d a* / d qfrc = H^-1)."""
+    B = len(cq)
+    rep = {k: np.repeat(v, 2 * oracle.NV, axis=0) for k, v in s64.items()}
+    Q = np.zeros((B, oracle.NV, 2, oracle.NV))
+    for j in range(oracle.NV):
+        Q[:, j, 0, j], Q[:, j, 1, j] = h, -h
+    oq, ov, _, _ = oracle.step(**rep, qfrc=Q.reshape(-1, oracle.NV), **ONE_SUBSTEP)
+    L = ((oq * np.repeat(cq, 2 * oracle.NV, 0)).sum(1) + (ov * np.repeat(cv, 2 * oracle.NV, 0)).sum(1))
+    L = L.reshape(B, oracle.NV, 2)
+    return (L[:, :, 0] - L[:, :, 1]) / (2 * h)
+
+
+@pytest.mark.parametrize("config", [1, 4])
+def test_clamp_variants_against_lambda_by_fd(config):
+    """The three clamp_kv modes pinned through lambda measured by finite differences (one substep, so one lambda; 64
+    states with clamped actuators on about half of them). With the PD force f = kp (u - q) - kv v clamped at +-tau
+    (clamped: |f| >= tau, computed here in numpy), the reference's definitions (adjoint.py:43-56,811-846) are:
+    clamp_kv=1 (exact): g_ctrl = kp lambda on unclamped dofs and 0 on clamped ones; clamp_kv=0 (MuJoCo Warp's): the
+    same except g_qvel gets -kv lambda more on the clamped dofs, nothing else changes; clamp_kv=2 (soft, delta): on a
+    clamped dof all three actuator paths take w lambda, w = exp(-max((|f| - tau) / tau, 0) / delta), so
+    g_ctrl = w kp lambda and g_qpos / g_qvel differ from clamp_kv=1 by -w kp lambda / -w kv lambda; delta -> 0 gives
+    clamp_kv=1. A dropped term, a wrong sign or a weight on the wrong path fails one of these."""
+    st = synthetic.states(64, config=config, dtype=np.float64)
+    cq, cv = synthetic.cotangents(64, dtype=np.float64)
+    lam = _lam_by_fd(st, cq, cv)
+    raw = KP[6:] * (st["ctrl"] - st["qpos"][:, 7:]) - KV[6:] * st["qvel"][:, 6:]
+    cl = np.abs(raw) >= FRCLIM[6:]
+    assert cl.any(1).sum() >= 30
+    V = lambda kv, **kw: oracle.vjp(**st, g_qpos=cq, g_qvel=cv, clamp_kv=kv, normal=0, **ONE_SUBSTEP, **kw)
+    g1, g0 = V(1), V(0)
+    klam = KP[6:] * lam[:, 6:]
+    sc = np.abs(klam).max()
+    assert np.abs(g1[2] - np.where(cl, 0.0, klam)).max() < 1e-5 * sc
+    assert np.array_equal(g0[0], g1[0]) and np.array_equal(g0[2], g1[2])
+    d = g0[1] - g1[1]
+    assert np.abs(d[:, :6]).max() == 0
+    assert np.abs(d[:, 6:] - np.where(cl, -KV[6:] * lam[:, 6:], 0.0)).max() < 1e-5 * sc
+    o = np.maximum((np.abs(raw) - FRCLIM[6:]) / FRCLIM[6:], 0.0)
+    for delta in (0.05, 0.2, 1.0):
+        g2 = V(2, clamp_soft=delta)
+        w = np.where(cl, np.exp(-o / delta), 1.0)
+        assert np.abs(g2[2] - w * klam).max() < 1e-5 * sc
+        assert np.abs(g2[1][:, 6:] - g1[1][:, 6:] - np.where(cl, -w * KV[6:] * lam[:, 6:], 0.0)).max() < 1e-5 * sc
+        assert np.abs(g2[0][:, 7:] - g1[0][:, 7:] - np.where(cl, -w * klam, 0.0)).max() < 1e-5 * sc
+        assert np.array_equal(g2[1][:, :6], g1[1][:, :6])
+    g2 = V(2, clamp_soft=1e-12)
+    assert all(np.array_equal(a, b) for a, b in zip(g2, g1))
+
+
+def _one_self_contact_worlds(st, n):
+    """Indices of states with exactly one self contact (a pair of robot geoms) at the input pose, with its pair and
+    nu = dist + r1 + r2 (the sphere core's centre distance)."""
+    pg1, pg2 = np.asarray(MODEL["pair_g1"]), np.asarray(MODEL["pair_g2"])
+    gt, gs = np.asarray(MODEL["geom_type"]), np.asarray(MODEL["geom_size"]).reshape(-1, 3)
+    out = []
+    for w in range(len(st["qpos"])):
+        c = oracle.contacts(st["qpos"][w], st["qvel"][w], st["ctrl"][w], st["com"][w], st["friction"][w])
+        sc = [r for r in c if gt[pg1[int(r[0])]] != 0]
+        if len(sc) == 1:
+            p = int(sc[0][0])
+            out.append((w, p, sc[0][2] + gs[pg1[p], 0] + gs[pg2[p], 0]))
+        if len(out) == n:
+            break
+    return out
+
+
+def test_normal_options_through_kappa():
+    """The normal options pinned against the exact mode (normal 0, pinned by FD) on contact-heavy states with exactly
+    one self contact (one substep, the near-parallel rule off: parallel_eps 0). The options differ only in kappa(nu),
+    the factor of the sphere core's normal derivative kappa (I - n n') (adjoint_contact.py:239-262): 0 exact 1 / nu,
+    1 frozen 0, 2 1 / max(nu, eps), 3 nu < eps ? 0 : 1 / nu. The VJP is affine in kappa, g(kappa) = g1 + kappa nu
+    (g0 - g1) with g1 normal 1's, so: option 2 and 3 with eps below nu equal option 0 bitwise; option 3 with eps above
+    nu equals option 1; option 2 with eps above nu is linear in 1 / eps, and its slope fits nu = dist + r1 + r2 of
+    the contact's geometry to 1e-9 (on the states whose self contact has a quadratic row, where g0 != g1)."""
+    st = synthetic.states(768, config=4, dtype=np.float64)
+    one = _one_self_contact_worlds(st, 32)
+    assert len(one) >= 24
+    sel = np.array([w for w, _, _ in one])
+    nus = np.array([nu for _, _, nu in one])
+    sub = {k: v[sel] for k, v in st.items()}
+    cq, cv = synthetic.cotangents(len(sel), dtype=np.float64)
+    G = lambda n, **kw: np.concatenate(oracle.vjp(**sub, g_qpos=cq, g_qvel=cv, clamp_kv=1, normal=n, parallel_eps=0.0,
+                                                  **ONE_SUBSTEP, **kw), 1)
+    g0, g1 = G(0), G(1)
+    assert np.array_equal(G(2, normal_eps=1e-9), g0) and np.array_equal(G(3, normal_eps=1e-9), g0)
+    assert np.array_equal(G(3, normal_eps=1.0), g1)
+    ga, gb = G(2, normal_eps=1.0), G(2, normal_eps=0.5)
+    sc = np.abs(g0).max(1, keepdims=True)
+    assert (np.abs((gb - g1) - 2 * (ga - g1)) / sc).max() < 1e-12
+    d = g0 - g1
+    row = np.abs(d).max(1) > 1e-9 * sc[:, 0]
+    assert row.sum() >= 12
+    nufit = (d * (ga - g1)).sum(1)[row] / (d * d).sum(1)[row]
+    assert np.abs(nufit / nus[row] - 1).max() < 1e-9
+    assert np.median(np.abs(d[row]).max(1) / sc[row, 0]) > 1e-2  # the frame's derivative matters
+
+
+def _fd_vjp(s1, cq, cv, h, **kw):
+    J = oracle.fd_jacobian(*(s1[k][0] for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")), h=h, **kw)
+    return np.concatenate([cq[0], cv[0]]) @ J
+
+
+def test_near_parallel_rule_is_the_frozen_parameter_gradient():
+    """The near-parallel rule (normal options != 0, adjoint_contact.py:436-448): a capsule-capsule contact whose two
+    segment parameters are both free has them held constant in the VJP where sin^2(theta) < 1.2e-3. With the
+    threshold raised to 1 (every both-free pair held) and kappa exact (option 2 at eps 1e-9), the VJP must be the
+    exact gradient of the forward in which those parameters are frozen at their values (the oracle's freeze hook:
+    recorded on the nominal run, replayed in every finite-difference run), and on two states where the held contact
+    has a row that matters it must differ from the unfrozen exact VJP. One substep, contact-heavy states with such a
+    contact, where the finite differences are smooth (h and h / 10 agree)."""
+    st = synthetic.states(256, config=4, dtype=np.float64)
+    pg1, gt = np.asarray(MODEL["pair_g1"]), np.asarray(MODEL["geom_type"])
+    pg2 = np.asarray(MODEL["pair_g2"])
+    done = 0
+    for w in range(len(st["qpos"])):
+        s1 = {k: v[w:w + 1] for k, v in st.items()}
+        c = oracle.contacts(s1["qpos"][0], s1["qvel"][0], s1["ctrl"][0], s1["com"][0], s1["friction"][0])
+        fz = np.zeros((oracle.NPAIR, 3))
+        oracle.step(**s1, freeze=fz, freeze_mode=1, **ONE_SUBSTEP)
+        if not any(fz[int(r[0]), 0] and gt[pg1[int(r[0])]] == 3 and gt[pg2[int(r[0])]] == 3 for r in c):
+            continue
+        cq, cv = synthetic.cotangents(1, seed=w, dtype=np.float64)
+        plain = _fd_vjp(s1, cq, cv, 1e-6, **ONE_SUBSTEP)
+        if np.linalg.norm(plain - _fd_vjp(s1, cq, cv, 1e-7, **ONE_SUBSTEP)) > 1e-4 * np.linalg.norm(plain):
+            continue  # a row switching on within +-h (the step is not smooth here)
+        fd = np.zeros(99)
+        J = []
+        for j in range(99):
+            out = []
+            for sg in (1.0, -1.0):
+                q, v, u = s1["qpos"].copy(), s1["qvel"].copy(), s1["ctrl"].copy()
+                if j < 35:
+                    dq = np.zeros(35)
+                    dq[j] = sg * 1e-6
+                    q = oracle.integrate_pos(q, dq)
+                elif j < 70:
+                    v[0, j - 35] += sg * 1e-6
+                else:
+                    u[0, j - 70] += sg * 1e-6
+                oq, ov, _, _ = oracle.step(q, v, s1["warm"], u, s1["friction"], s1["com"], freeze=fz, freeze_mode=2,
+                                           **ONE_SUBSTEP)
+                out.append(np.concatenate([oq[0], ov[0]]))
+            J.append((out[0] - out[1]) / 2e-6)
+        fd = np.concatenate([cq[0], cv[0]]) @ np.array(J).T
+        tang = lambda g: np.concatenate([oracle.qpos_tangent(s1["qpos"][0], g[0][0]), g[1][0], g[2][0]])
+        held = tang(oracle.vjp(**s1, g_qpos=cq, g_qvel=cv, clamp_kv=1, normal=2, normal_eps=1e-9, parallel_eps=1.0,
+                               **ONE_SUBSTEP))
+        exact = tang(oracle.vjp(**s1, g_qpos=cq, g_qvel=cv, clamp_kv=1, normal=0, **ONE_SUBSTEP))
+        assert np.linalg.norm(held - fd) < 1e-6 * np.linalg.norm(fd), w
+        if np.linalg.norm(exact - fd) > 1e-3 * np.linalg.norm(fd):  # the held contact has a row that matters
+            done += 1
+            if done == 2:
+                break
+    assert done == 2
+
+
+def test_ten_iteration_tail_is_the_iteration_cap():
+    """On 1024 config-1 states the 10-iteration step differs from the converged one (MuJoCo's truth settings: 2000
+    iterations, tolerance 1e-13) by p99 > 1e-3 in qvel, while 20 iterations already give the converged result to
+    1e-13 on every world: the tail of the engine's default step against converged references is its iteration cap,
+    not an error of the solver (an exact Newton method on a piecewise quadratic stops on the minimiser once its
+    zones are right)."""
+    st = synthetic.states(1024, config=1, dtype=np.float64)
+    _, ov, _, _ = oracle.step(**st, **oracle.TRUTH)
+    rel = lambda a: np.linalg.norm(a - ov, axis=1) / np.linalg.norm(ov, axis=1)
+    e10 = rel(oracle.step(**st, **oracle.ENGINE)[1])
+    e20 = rel(oracle.step(**st, **dict(oracle.ENGINE, iterations=20))[1])
+    assert np.percentile(e10, 99) > 1e-3 and np.median(e10) < 1e-13
+    assert e20.max() < 1e-13
 
 
 def test_flop_count_closed_form():
