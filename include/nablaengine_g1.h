@@ -1,8 +1,8 @@
 /* C ABI of the MI355X G1 control-step library (libnablaengine_g1.so): the entry points the reference's FFI binds
  * (ctypes in src/nablaengine/torch_ffi.py:333-366 _bind, XLA FFI in src/nablaengine/jax_ffi.py:486-797), with
  * cudaStream_t -> hipStream_t. Plain pointers and sizes: float32 arrays world-major and row-contiguous, int32 info.
- * Every entry returns 0 on success, else a hipError_t (or -1: the device cannot take the launch); nothing is
- * allocated per call (the caller owns every output, the tape and the work buffer); launches go on the given stream. */
+ * Every entry returns 0 on success, else a hipError_t (or -1: the device cannot take the launch; -2: more worlds
+ * than dk_fwd_forward_static's scratch holds); nothing is allocated per call (the caller owns every output, the tape and the work buffer); launches go on the given stream. */
 #ifndef NABLAENGINE_G1_H
 #define NABLAENGINE_G1_H
 #include <hip/hip_runtime_api.h>
@@ -28,6 +28,18 @@ int dk_fwd_order(hipStream_t st, int nw, const float* qpos, void* work);
 int dk_fwd_forward_ordered(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm,
                            const float* ctrl, const float* fric, const float* com, int iterations, int nsub, float* oq,
                            float* ov, float* ow, int* info, float* ocon, float* tape, const void* work);
+/* No counterpart in the reference (its forward takes the caller's work memory): dk_fwd_forward for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same
+ * arguments without work, and the same results; the dispatch order lives in a static device array of the library
+ * (1 MiB per GPU, held until the process ends) whose address dk_fwd_upload takes once per device (else the first
+ * call on the device does). At most DK_STATIC_MAX_WORLDS worlds: more returns DK_ERR_STATIC_CAPACITY without a
+ * launch. Nothing is allocated. Every call on one GPU shares that array, so calls that overlap on one GPU (two
+ * streams at once) race; calls in one stream's order do not. */
+#define DK_STATIC_MAX_WORLDS 131072
+#define DK_ERR_STATIC_CAPACITY (-2)
+int dk_fwd_forward_static(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm,
+                          const float* ctrl, const float* fric, const float* com, int iterations, int nsub, float* oq,
+                          float* ov, float* ow, int* info, float* ocon, float* tape);
 /* Replaces <fwd>_work_bytes (jax_ffi.py:265): scratch bytes the forward's work buffer takes for nw worlds (the
  * dispatch order, heaviest worlds first: 8 bytes per world). work = NULL runs the worlds in index order instead; the
  * results are the same either way. */

@@ -3,6 +3,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 namespace g1k {
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
@@ -29,6 +31,33 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
 }  // namespace g1k
 
 namespace {
+// The allocation-free forward's scratch (dk_fwd_forward_static): the dispatch order of up to DK_STATIC_MAX_WORLDS
+// worlds (a permutation and a cost, 4 bytes each per world) in a file-scope device array, one copy per GPU held until
+// the process ends. Host code never passes the array's name to a kernel (on the host it is a stand-in, not a device
+// address): each device's address is taken once by hipGetSymbolAddress with that device current and kept in
+// g_scratch. The kernels write every word they read (costs, then the permutation), so nothing is cleared.
+__device__ __align__(256) unsigned char scratch[8 * (size_t)DK_STATIC_MAX_WORLDS];
+constexpr int MAX_DEVICES = 64;
+void* g_scratch[MAX_DEVICES];
+std::mutex g_scratch_mu;
+
+// the scratch's address on the current device (taken on the first call for that device)
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= MAX_DEVICES) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return 0;
+}
+
 int check_device() {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -93,7 +122,23 @@ long long dk_fwd_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work
 int dk_fwd_upload(const float* consts, hipStream_t st) {
   (void)consts;
   (void)st;
-  return check_device();
+  const int rc = check_device();
+  if (rc) return rc;
+  void* p = nullptr;  // the allocation-free forward's scratch address on this device, taken at set-up
+  return scratch_ptr(&p);
+}
+
+int dk_fwd_forward_static(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm,
+                          const float* ctrl, const float* fric, const float* com, int iterations, int nsub, float* oq,
+                          float* ov, float* ow, int* info, float* ocon, float* tape) {
+  if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0) return (int)hipErrorInvalidValue;
+  if (nw > DK_STATIC_MAX_WORLDS) return DK_ERR_STATIC_CAPACITY;
+  if (nw == 0) return 0;
+  void* work = nullptr;
+  const int rc = scratch_ptr(&work);
+  if (rc) return rc;
+  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
+                             work, 1);
 }
 
 // the profiling build's per-world phase cycles of the last forward (test and measurement helper; -1 in production)
