@@ -2,12 +2,21 @@
 and forward+VJP, at 4096 worlds (and 16384), on one GPU.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu] [--no-16k] [--no-configs]
+                    [--no-corpus] [--no-rounds]
 
 A step is one control step (4 substeps of 5 ms, Newton 10 iterations) of B worlds of BASELINE config 1 (seeded
 synthetic states, inputs resident in HBM before the timed region), exactly what torch_ffi.forward runs: the dispatch
-order pre-pass and the forward kernel. K steps are timed back to back between two synchronizations with HIP events on
-the launch stream; rank 0 prints one JSON line. Forward+VJP is the taped forward plus the adjoint (torch_ffi.forward
-(tape=True) + torch_ffi.backward), timed the same way.
+order pre-pass and the forward kernel. The headline (`ms_per_step`, `value`): W untimed calls, then K calls back to
+back between two synchronizations, timed with HIP events on the launch stream; rank 0 prints one JSON line.
+Forward+VJP is the taped forward plus the adjoint (torch_ffi.forward(tape=True) + torch_ffi.backward), timed the same
+way.
+
+`rounds` restates the reference's timing protocol (scripts/paper_bench/common.py:1-10,154-187): a warm-up of at least
+5 calls and 1 s, then 6 rounds of n back-to-back calls with one synchronization each (n chosen so that a round lasts
+about 0.25 s, at most 200 calls), round 0 dropped; ms per call median / p10 / p90 / min / max over the 5 kept rounds.
+It covers the forward and forward+VJP at 4096 and 16384 synthetic worlds and at the 4096 states of the reference's
+corpus mf_s0 (`corpus_mf_s0`: the inputs its published 1.214 / 1.784 ms are measured on,
+docs/results/paper_rtx6000/paper_bench.md:91-92; a committed fixture, tests/golden/corpus_mf_s0.npz).
 
 Also reported: config 3 (`config3_jacobian`: full 71 x 99 step Jacobians of the 4096 worlds from one taped forward
 and 71 VJPs, us per world-Jacobian) and config 4 (`config4_bptt`: a 32-step rollout of 16384 contact-heavy worlds with
@@ -18,7 +27,9 @@ closed-form phase counts on the same inputs, counted once before timing, per wor
 mean duration, timed live here with HIP events around K back-to-back launches of the forward alone (the order
 computed once before, dk_fwd_forward_ordered); peak is MI355X's FP32 (157.3 TFLOP/s). `traffic` is k_forward's HBM
 bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (the committed summary). `cpu_baseline` is the float64 CPU
-restatement ("port", one thread) on 64 config-0 worlds for about 10 s.
+restatement ("port"), timed with the same round protocol: one thread on the 64 worlds of config 0 (the reference's
+single-thread CPU case) and, in `all_threads`, the host's usable cores (len(os.sched_getaffinity(0)), at most 16: the
+GPU box's CPU share) on 4096 config-0 worlds (the reference's batched CPU case).
 """
 import argparse
 import ctypes
@@ -41,7 +52,9 @@ IO_BYTES_FWD = (36 + 35 + 35 + 29 + 1 + 3) * 4 + (36 + 35 + 35) * 4 + 16
 # HBM bytes per k_forward launch at 4096 worlds, measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (two runs,
 # each scaled by the same counter's reading on a copy of known size, `--copy-mib`); the summary holds the command
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_forward_4096_traffic.md")
+CORPUS = os.path.join(ROOT, "tests", "golden", "corpus_mf_s0.npz")
 KEYS = ("qpos", "qvel", "warm", "ctrl", "friction", "com")
+ROUNDS, WARM_CALLS, WARM_S, ROUND_S, MAX_CALLS = 5, 5, 1.0, 0.25, 200
 
 
 def measured_traffic(worlds):
@@ -55,27 +68,82 @@ def measured_traffic(worlds):
     return None
 
 
-def cpu_baseline(seconds=10.0):
-    """The float64 CPU restatement (test oracle, one thread) on 64 worlds of config 0: world-steps/s."""
+def _stats(per_call_ms, n, warm_calls, warm_s):
+    a = np.asarray(per_call_ms)
+    return {"median_ms": float(np.median(a)), "p10_ms": float(np.percentile(a, 10)),
+            "p90_ms": float(np.percentile(a, 90)), "min_ms": float(a.min()), "max_ms": float(a.max()),
+            "calls_per_round": n, "kept_rounds": len(a), "warmup_calls": warm_calls, "warmup_s": round(warm_s, 3)}
+
+
+def protocol_cpu(call):
+    """The reference's round protocol (common.py:154-187) for a host call: ms per call over the kept rounds."""
+    t0, k = time.perf_counter(), 0
+    while k < WARM_CALLS or time.perf_counter() - t0 < WARM_S:
+        call()
+        k += 1
+    warm = time.perf_counter() - t0
+    n = int(min(MAX_CALLS, max(1, round(ROUND_S * 6 / (warm / k)))))  # CPU rounds of about 1.5 s
+    per = []
+    for _ in range(ROUNDS + 1):
+        t = time.perf_counter()
+        for _ in range(n):
+            call()
+        per.append(1e3 * (time.perf_counter() - t) / n)
+    return _stats(per[1:], n, k, warm)
+
+
+def protocol_gpu(fn, stream):
+    """The reference's round protocol for a GPU call: warm-up >= 5 calls and >= 1 s (synchronized), then 6 rounds of
+    n back-to-back calls, each timed with HIP events on `stream` and one synchronization, round 0 dropped."""
+    import torch
+    t0, k = time.perf_counter(), 0
+    while k < WARM_CALLS or time.perf_counter() - t0 < WARM_S:
+        fn()
+        torch.cuda.synchronize()
+        k += 1
+    warm = time.perf_counter() - t0
+    n = int(min(MAX_CALLS, max(1, round(ROUND_S / (warm / k)))))
+    per = []
+    for _ in range(ROUNDS + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / n)
+    return _stats(per[1:], n, k, warm)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        return "unknown CPU"
+
+
+def cpu_baseline():
+    """The float64 CPU restatement (test oracle) on config-0 states with the round protocol: one thread on 64 worlds,
+    and the host's usable cores (at most 16) on 4096 worlds. world-steps/s from the median round."""
     import oracle
     from nablaengine_amd import synthetic
     st = synthetic.states(64, config=0, dtype=np.float64)
-    oracle.step(**st, **oracle.ENGINE)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        oracle.step(**st, **oracle.ENGINE)
-        n += 1
-    dt = time.perf_counter() - t0
-    cpu = "unknown CPU"
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
-    except (OSError, StopIteration):
-        pass
-    return dict(value=64 * n / dt, unit="world-steps/s", cores=1, kind="port", cpu=cpu,
+    one = protocol_cpu(lambda: oracle.step(**st, **oracle.ENGINE))
+    threads = min(16, len(os.sched_getaffinity(0)))
+    big = synthetic.states(4096, config=0, dtype=np.float64)
+    many = protocol_cpu(lambda: oracle.step_mt(threads, **big, **oracle.ENGINE))
+    settings = "float64 CPU restatement, not MuJoCo; Newton 10 it, tol 1e-8, line search 40 / 1e-7 (the engine's)"
+    return dict(value=64e3 / one["median_ms"], unit="world-steps/s", cores=1, kind="port", cpu=_cpu_model(),
                 host_threads=len(os.sched_getaffinity(0)),
-                sample=f"{n} x 64 config-0 worlds (float64 CPU restatement, not MuJoCo; Newton 10 it, tol 1e-8), "
-                       f"{dt:.1f} s, ms per 64-world step {1e3 * dt / n:.2f}")
+                sample=f"64 config-0 worlds per call, {one['calls_per_round']} calls per round, 5 kept rounds "
+                       f"({settings}); ms per 64-world step median {one['median_ms']:.2f}",
+                rounds=one,
+                all_threads=dict(value=4096e3 / many["median_ms"], unit="world-steps/s", cores=threads,
+                                 sample=f"4096 config-0 worlds per call on {threads} threads (contiguous shares), "
+                                        f"{many['calls_per_round']} calls per round, 5 kept rounds; ms per "
+                                        f"4096-world step median {many['median_ms']:.1f}",
+                                 rounds=many))
 
 
 def algorithmic_flops(st):
@@ -100,24 +168,34 @@ def timed(fn, steps, warmup, stream):
     return e0.elapsed_time(e1) / steps
 
 
-def measure(B, steps, warmup, kernel=False):
-    """(forward ms, fwd+VJP ms, k_forward ms or None, info of the last forward) at B worlds of config 1."""
+def _calls(st):
+    """(forward call, forward+VJP call, the output holder) on states st, inputs resident on the GPU."""
     import torch
     from nablaengine_amd import synthetic, torch_ffi
-    st = synthetic.states(B, config=1)
-    args = [torch.from_numpy(st[k]).cuda() for k in KEYS]
-    stream = torch.cuda.current_stream()
+    B = len(st["qpos"])
+    args = [torch.from_numpy(np.ascontiguousarray(st[k], np.float32)).cuda() for k in KEYS]
+    gq, gv = (torch.from_numpy(x).cuda() for x in synthetic.cotangents(B))
     out = {}
 
     def fwd():
         out["r"] = torch_ffi.forward(*args)
-    ms = timed(fwd, steps, warmup, stream)
-    info = out["r"][3].cpu().numpy()
-    gq, gv = (torch.from_numpy(x).cuda() for x in synthetic.cotangents(B))
 
     def vjp():
         r = torch_ffi.forward(*args, tape=True)
         torch_ffi.backward(r[4], args[4], args[5], gq, gv)
+    return fwd, vjp, out, args
+
+
+def measure(B, steps, warmup, kernel=False, rounds=True):
+    """(forward ms, fwd+VJP ms, k_forward ms or None, info of the last forward, round-protocol stats or None) at B
+    worlds of config 1."""
+    import torch
+    from nablaengine_amd import synthetic, torch_ffi
+    st = synthetic.states(B, config=1)
+    fwd, vjp, out, args = _calls(st)
+    stream = torch.cuda.current_stream()
+    ms = timed(fwd, steps, warmup, stream)
+    info = out["r"][3].cpu().numpy()
     vjp_ms = timed(vjp, steps, warmup, stream)
     kms = None
     if kernel:  # k_forward alone: the order once, then the ordered launches back to back
@@ -134,7 +212,28 @@ def measure(B, steps, warmup, kernel=False):
             assert lib.dk_fwd_forward_ordered(st_, B, *map(p, args), 10, 4, p(q1), p(v1), p(w1), p(inf), None, None,
                                               p(work)) == 0
         kms = timed(kern, steps, warmup, stream)
-    return ms, vjp_ms, kms, info
+    rs = {"forward": protocol_gpu(fwd, stream), "fwd_vjp": protocol_gpu(vjp, stream)} if rounds else None
+    return ms, vjp_ms, kms, info, rs
+
+
+def measure_corpus():
+    """The forward and forward+VJP of the reference corpus mf_s0's 4096 states (warm start as stored), with the
+    round protocol."""
+    import torch
+    z = np.load(CORPUS)
+    st = {k: z["qacc_warmstart" if k == "warm" else k] for k in KEYS}
+    fwd, vjp, out, _ = _calls(st)
+    stream = torch.cuda.current_stream()
+    rf, rv = protocol_gpu(fwd, stream), protocol_gpu(vjp, stream)
+    info = out["r"][3].cpu().numpy()
+    return {"worlds": len(st["qpos"]), "inputs": "benchmarks/data/mf_s0.npz (4096 corpus states: qpos, qvel, "
+                                                  "qacc_warmstart, ctrl, friction, com; cotangents N(0, 1))",
+            "ms_per_step": rf["median_ms"], "ms_per_step_fwd_vjp": rv["median_ms"],
+            "world_steps_per_s": 4096e3 / rf["median_ms"], "world_steps_per_s_fwd_vjp": 4096e3 / rv["median_ms"],
+            "reference_rtx_pro_6000_ms": {"forward": 1.214, "fwd_vjp": 1.784},
+            "forward": rf, "fwd_vjp": rv,
+            "capacity": {"contacts_max": int(info[:, 1].max()), "rows_max": int(info[:, 2].max()),
+                         "overflow_worlds": int(((info[:, 3] & 20) != 0).sum())}}
 
 
 def measure_jacobian(B, reps=2):
@@ -189,6 +288,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-16k", action="store_true", help="skip the 16384-world forward and fwd+VJP lines")
     ap.add_argument("--no-configs", action="store_true", help="skip the config 3 (Jacobian) and 4 (BPTT) lines")
+    ap.add_argument("--no-corpus", action="store_true", help="skip the mf_s0 corpus line")
+    ap.add_argument("--no-rounds", action="store_true", help="skip the round-protocol statistics")
     ap.add_argument("--flop-sample", type=int, default=512, help="worlds the flop count is taken on")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="before the timed steps, copy a buffer of this many MiB 3 times (a kernel of known HBM "
@@ -209,12 +310,14 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     B = a.worlds
-    ms, vjp_ms, kms, info = measure(B, a.steps, a.warmup, kernel=True)
+    ms, vjp_ms, kms, info, rs = measure(B, a.steps, a.warmup, kernel=True, rounds=not a.no_rounds)
     big = None
     if not a.no_16k and B != 16384:
-        bms, bvjp, _, binfo = measure(16384, max(a.steps // 4, 3), max(a.warmup // 4, 2))
+        bms, bvjp, _, binfo, brs = measure(16384, max(a.steps // 4, 3), max(a.warmup // 4, 2), rounds=not a.no_rounds)
         big = {"worlds": 16384, "ms_per_step": bms, "ms_per_step_fwd_vjp": bvjp,
                "world_steps_per_s": 16384e3 / bms, "world_steps_per_s_fwd_vjp": 16384e3 / bvjp}
+        if brs:
+            big["rounds"] = brs
     st = synthetic.states(B, config=1)
     sub = {k: v[: a.flop_sample] for k, v in st.items()}
     fl = algorithmic_flops(sub)
@@ -241,8 +344,13 @@ def main():
         "capacity": {"contacts_max": int(info[:, 1].max()), "rows_max": int(info[:, 2].max()),
                      "overflow_worlds": int(((info[:, 3] & 20) != 0).sum())},
     }
+    if rs:
+        res["rounds"] = dict(rs, protocol="scripts/paper_bench/common.py:154-187: warm-up >= 5 calls and >= 1 s, "
+                                          "6 rounds of n calls (one synchronization each), round 0 dropped")
     if big:
         res["worlds_16384"] = big
+    if not a.no_corpus and os.path.exists(CORPUS):
+        res["corpus_mf_s0"] = measure_corpus()
     if not a.no_configs:
         res["config3_jacobian"] = measure_jacobian(B)
         res["config4_bptt"] = measure_bptt(16384)

@@ -9,7 +9,10 @@ Every array is data the reference's own checks hold (MuJoCo C float64 truth and 
   FD VJPs `fd_vjp` (h = 1e-6) and `fd_vjp_floor` (h = 1e-7), validity bits `bad`, groups G0/G4/G5/G6, outputs `out`;
   the first 16 G0 states' full 71 x 99 step Jacobian `jacobian` with `jac_index`;
 - mjw_<corpus>.npz (mf_s0): MuJoCo Warp 3.17 float32 contacts at the input state (`con`: pair, dist, pos[3],
-  normal[3]) and per-substep counts for the first 512 states (fixtures/mjlab/mjw317_mf_s0.npz).
+  normal[3]) and per-substep counts for the first 512 states (fixtures/mjlab/mjw317_mf_s0.npz);
+- corpus_mf_s0.npz: the inputs of all 4096 states of the benchmark corpus mf_s0 (benchmarks/data/mf_s0.npz), the
+  states the reference's published timings are measured on (docs/results/paper_rtx6000/paper_bench.md:91-92), for
+  bench.py's corpus line.
 """
 import os
 import sys
@@ -40,6 +43,8 @@ def main():
                                 **{g: t["group_" + g] for g in ("G0", "G4", "G5", "G6")},
                                 **{k: c[k][gi] for k in INPUTS}, **extra,
                                 **{"jac_" + k: c[k][gi[ji]] for k in INPUTS})  # jac_index: positions into index
+    c = np.load(os.path.join(data, "mf_s0.npz"))
+    np.savez_compressed(os.path.join(OUT, "corpus_mf_s0.npz"), **{k: c[k] for k in INPUTS})
     m = np.load(os.path.join(REF, "fixtures", "mjlab", "mjw317_mf_s0.npz"))
     c = np.load(os.path.join(data, "mf_s0.npz"))
     n = 512
