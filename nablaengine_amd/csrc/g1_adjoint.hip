@@ -717,7 +717,6 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   // 2 x 4 tiles, 8 steps of k = 4, in two passes over 32 columns each. A pass reads only its own columns of F, every
   // load before its first store, so T overwrites fb in place.
   {
-    typedef float mfma4 __attribute__((ext_vector_type(4)));
     constexpr int NF = NFB * 6;
     float* F = &s.fb[0][0][0];
     const int lr = lane & 15, lk = lane >> 4;

@@ -253,6 +253,16 @@ __host__ __device__ constexpr uint64_t fill_bits(int k) {
 }
 static_assert(NV == 35, "the fill rows are the G1's dof ranges");
 
+typedef float mfma4 __attribute__((ext_vector_type(4)));
+constexpr int NROOT = 6;  // the free joint's dofs: every other dof's ancestors
+
+// The hinge dofs are eliminated first; each would update the 6 x 6 root block (rows and columns 0..5) by the outer
+// product of its row's root part, 6 broadcasts and FMAs a step that only lanes 0..5 use (174 of the tree pattern's 306
+// pairs). These updates are summed instead as one product on the matrix cores, the Schur complement
+// D = X' X with X[k][r] = L[k][r] (hinge rows k = 6..34, root columns r < 6; 29 rows padded to 32): 8 steps of
+// v_mfma_f32_16x16x4f32, lane l giving A[l % 16][k'] = B[k'][l % 16] = X[6 + k'][l % 16] for k' = 4 t + l / 16 (read
+// back from the factor's hinge rows, stored first), lane l holding D[4 (l / 16) + e][l % 16]. Then the root block is
+// eliminated as before.
 template <int PATTERN>  // 0: the tree's sparsity; 1: with the common self-contact fill; 2: every pair
 __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
   constexpr bool SPARSE = PATTERN < 2;
@@ -265,21 +275,43 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
   for (int m = 0; m < NV; m++) c[m] = col[tri(m, 0)];
 #pragma unroll
   for (int k = NV - 1; k >= 0; k--) {
+    if (k == NROOT - 1) {
+      // the hinge rows are final: store them (lane j column j, rows m >= j; other lanes into their sink slot), then
+      // the root block's Schur complement on the matrix cores
+#pragma unroll
+      for (int m = NROOT; m < NV; m++) Lp[m >= lane && lane < NV ? tri(m, lane) : LSINK + lane] = c[m];
+      __syncthreads();
+      const int r = lane & 15, q = lane >> 4;
+      mfma4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const int kk = NROOT + 4 * t + q;
+        const bool in = r < NROOT && kk < NV;
+        const float x = Lp[tri(in ? kk : NV - 1, in ? r : 0)];
+        const float xv = in ? x : 0.f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv, xv, acc, 0, 0, 0);
+      }
+      // lane j < 6: D[0..3][j] in its own acc, D[4][j] and D[5][j] in lane j + 16's acc[0], acc[1]
+      const float d4 = __shfl(acc[0], lane + 16, 64), d5 = __shfl(acc[1], lane + 16, 64);
+      c[0] -= acc[0]; c[1] -= acc[1]; c[2] -= acc[2]; c[3] -= acc[3]; c[4] -= d4; c[5] -= d5;
+    }
     const float d = fmaxf(rdl(c[k], k), 1e-30f);
     // L[k][j] = A[k][j] / sqrt(d) on lane j; on lane k itself d / sqrt(d) = L[k][k] (the hardware 1/sqrt, 1 ulp)
     c[k] *= __builtin_amdgcn_rsqf(d);
-    // every broadcast of the step first, then the updates: a v_readlane's SGPR is not read by the next instruction
+    // every broadcast of the step first, then the updates: a v_readlane's SGPR is not read by the next instruction;
+    // a hinge step's updates of the root rows are left to the Schur complement above
+    const int m0 = k >= NROOT ? NROOT : 0;
     float bc[NV];
 #pragma unroll
-    for (int m = 0; m < k; m++)
+    for (int m = m0; m < k; m++)
       if (!SPARSE || (((TREE.dofanc[k] | (PATTERN ? fill_bits(k) : 0ull)) >> m) & 1ull)) bc[m] = rdl(c[k], m);
 #pragma unroll
-    for (int m = 0; m < k; m++)  // A[m][j] -= L[k][j] L[k][m] (the pattern's test at compile time)
+    for (int m = m0; m < k; m++)  // A[m][j] -= L[k][j] L[k][m] (the pattern's test at compile time)
       if (!SPARSE || (((TREE.dofanc[k] | (PATTERN ? fill_bits(k) : 0ull)) >> m) & 1ull)) c[m] = fmaf(-c[k], bc[m], c[m]);
   }
-  // lane j stores column j's entries m >= j; the other lanes store into their sink slot (no branch per store)
+  // lane j stores column j's root rows m >= j; the other lanes store into their sink slot (no branch per store)
 #pragma unroll
-  for (int m = 0; m < NV; m++) Lp[m >= lane && lane < NV ? tri(m, lane) : LSINK + lane] = c[m];
+  for (int m = 0; m < NROOT; m++) Lp[m >= lane && lane < NV ? tri(m, lane) : LSINK + lane] = c[m];
 }
 
 // x = A^-1 b for A = L' L (ltl_factor), b and x on lane i < NV: L' y = b leaf-first (reads row i of L: lane k takes

@@ -200,7 +200,6 @@ __device__ void smooth(Sim& s, int lane) {
   // holding C[4 (l / 16) + e][l % 16]; 2 row tiles, 8 steps of k = 4. Every load is issued before the first store, so
   // the sums overwrite the bodies' own values in place.
   {
-    typedef float mfma4 __attribute__((ext_vector_type(4)));
     const int lr = lane & 15, lk = lane >> 4;
     float* col = lr < 3 ? &s.u.sm.F[0][lr] : (lr < 6 ? &s.u.sm.T[0][lr - 3] : &s.u.sm.Ic[0][lr - 6]);  // column lr
     const int cs = lr < 6 ? 4 : 12;  // its stride
@@ -521,7 +520,6 @@ __device__ void refresh(Sim& s, Rows& R, int lane, bool con, bool smooth = false
 }
 
 constexpr int SELF_BATCH = 4;  // contacts between two robot bodies per outer-product batch (4 edge rows each)
-typedef float mfma4 __attribute__((ext_vector_type(4)));
 
 // a floor contact's 6x6 stiffness K = Phi' C Phi about O (21 floats: Kaa 6, Kal 9, Kf 6), C from the curvatures d of
 // its pyramid rows in the frame basis; zero where !on
