@@ -192,6 +192,15 @@ __device__ __forceinline__ void make_frame_vjp(const float* n, const float* frb,
 }
 
 // sphere core VJP: (dist, pos, n) of two spheres with cotangents db, posb, nb -> p1b, p2b (added)
+// kappa(nu) nu, the factor of the normal's derivative where it is written without 1 / nu (capsule-capsule with both
+// parameters free): exactly 1 for the exact derivative
+__device__ __forceinline__ float kappa_nu(float nu, int normal) {
+  const float eps = 1e-3f;
+  if (normal == 0) return 1.f;
+  if (normal == 1) return 0.f;
+  if (normal == 2) return nu / fmaxf(nu, eps);
+  return nu < eps ? 0.f : 1.f;
+}
 __device__ __forceinline__ void sphere_core_vjp(const float* p1, float r1, const float* p2, float r2, float db,
                                                 const float* posb, const float* nb, int normal, float* p1b, float* p2b) {
   const float dl[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
@@ -314,20 +323,48 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
     x1 = fminf(fmaxf(raw, -1.f), 1.f);
     mode = (raw >= -1.f && raw < 1.f) ? 2 : 3;
   }
-  float v1[3], v2[3], v1b[3] = {0.f, 0.f, 0.f}, v2b[3] = {0.f, 0.f, 0.f};
-  for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
-  sphere_core_vjp(v1, r1, v2, r2, db, posb, nb, normal, v1b, v2b);
-  float a1b[3], a2b[3];
-  for (int k = 0; k < 3; k++) { x1b[k] += v1b[k]; x2b[k] += v2b[k]; a1b[k] = x1 * v1b[k]; a2b[k] = x2 * v2b[k]; }
-  float x1bar = dot3(a1, v1b), x2bar = dot3(a2, v2b);
-  if (mode == 0 && normal != 0) {  // near-parallel capsules: both parameters held where sin^2(theta) < 1.2e-3
-    float cr[3];
-    cross(a1, a2, cr);
-    if (dot3(cr, cr) < 1.2e-3f * ma * mc) { x1bar = 0.f; x2bar = 0.f; }
+  float v1[3], v2[3], v1b[3] = {0.f, 0.f, 0.f}, v2b[3] = {0.f, 0.f, 0.f}, dl[3], wv[3], a1b[3], a2b[3], x1bar, x2bar;
+  for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; dl[k] = v2[k] - v1[k]; }
+  cross(a1, a2, wv);
+  const float ww = dot3(wv, wv);  // ma mc - mb^2 without its cancellation
+  const bool wok = ww > 1e-12f * ma * mc;
+  // near-parallel capsules (normal options != 0): both parameters held where sin^2(theta) < 1.2e-3
+  const bool held = mode == 0 && normal != 0 && ww < 1.2e-3f * ma * mc;
+  const float nu = sqrtf(dot3(dl, dl));
+  if (mode == 0 && !held && wok && nu > 0.f) {
+    // both parameters free: v2 - v1 is normal to both axes at the optimum, so n = sg w / |w| depends on the axes
+    // alone (w = a1 x a2: dn = sg (I - n n') dw / |w|, dw = da1 x a2 + a1 x da2) and the distance is stationary in x1, x2; pos =
+    // v1 + n (r1 + dist / 2) moves with x1 through v1 only. No term of order 1 / nu appears (the general chain below
+    // sums such terms that cancel to order 1, losing up to 1e-3 relative in float32 at nu = 5 mm). The normal path is
+    // scaled by kappa(nu) nu (1 for the exact derivative).
+    float n[3], t[3], tau[3], u1[3], u2[3];
+    const float inu = 1.f / nu;
+    for (int k = 0; k < 3; k++) n[k] = dl[k] * inu;
+    const float dist = nu - r1 - r2, hp = r1 + 0.5f * dist, dt = db + 0.5f * dot3(n, posb);
+    for (int k = 0; k < 3; k++) t[k] = nb[k] + hp * posb[k];
+    const float nt = dot3(n, t);
+    float f = kappa_nu(nu, normal) * rsqrtf(ww);
+    if (dot3(n, wv) < 0.f) f = -f;
+    for (int k = 0; k < 3; k++) tau[k] = f * (t[k] - n[k] * nt);
+    cross(a2, tau, u1);
+    cross(tau, a1, u2);
+    for (int k = 0; k < 3; k++) { v2b[k] = n[k] * dt; v1b[k] = posb[k] - v2b[k]; }
+    for (int k = 0; k < 3; k++) {
+      x1b[k] += v1b[k]; x2b[k] += v2b[k];
+      a1b[k] = x1 * v1b[k] + u1[k]; a2b[k] = x2 * v2b[k] + u2[k];
+    }
+    x1bar = dot3(a1, posb);
+    x2bar = 0.f;
+  } else {
+    sphere_core_vjp(v1, r1, v2, r2, db, posb, nb, normal, v1b, v2b);
+    for (int k = 0; k < 3; k++) { x1b[k] += v1b[k]; x2b[k] += v2b[k]; a1b[k] = x1 * v1b[k]; a2b[k] = x2 * v2b[k]; }
+    x1bar = held ? 0.f : dot3(a1, v1b);
+    x2bar = held ? 0.f : dot3(a2, v2b);
   }
   float mab = 0.f, mbb = 0.f, mcb = 0.f, ub = 0.f, vb = 0.f;
-  if (mode == 0) {
-    const float N1b = x1bar * idet, N2b = x2bar * idet, detb = -(x1bar * x1 + x2bar * x2) * idet;
+  if (mode == 0) {  // G's determinant as |a1 x a2|^2 where that is not rounding noise (the forward's det otherwise)
+    const float ig = wok ? 1.f / ww : idet;
+    const float N1b = x1bar * ig, N2b = x2bar * ig, detb = -(x1bar * x1 + x2bar * x2) * ig;
     mcb += N1b * u; ub += N1b * mc; mbb -= N1b * v; vb -= N1b * mb;
     mab += N2b * v; vb += N2b * ma; mbb -= N2b * u; ub -= N2b * mb;
     mab += detb * mc; mcb += detb * ma; mbb -= 2.f * mb * detb;

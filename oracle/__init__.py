@@ -57,6 +57,8 @@ def lib():
                                  + L.g1o_vjp.argtypes[17:])
         L.g1o_contacts.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp]
         L.g1o_kinematics.argtypes = [ctypes.c_int] + [dp] * 8
+        L.g1o_substep_hessian.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp, ctypes.c_int, ctypes.c_double,
+                                          ctypes.c_int, ctypes.c_double, dp, dp]
         _lib = L
     return _lib
 
@@ -192,6 +194,28 @@ def fd_vjp(qpos, qvel, warm, ctrl, friction, com, g_qpos, g_qvel, h=1e-6, thread
     J = (out[:, :, 0] - out[:, :, 1]) / (2 * h)  # (B, 99, 71): d output / d input column
     c = np.concatenate([_c(g_qpos, (B, NQ)), _c(g_qvel, (B, NV))], 1)
     return np.einsum("bio,bo->bi", J, c)
+
+
+def substep_hessian(qpos, qvel, warm, ctrl, friction, com, iterations=2000, tol=1e-13, ls_max=100, ls_tol=1e-12):
+    """One substep of one state: (M (35, 35) at the input state, H (35, 35) = M + J'DJ on the rows in the quadratic
+    zone at Newton's final a*), float64 (the checker of a tape record's factors)."""
+    M, H = np.empty((NV, NV)), np.empty((NV, NV))
+    lib().g1o_substep_hessian(_p(_c(qpos, NQ)), _p(_c(qvel, NV)), _p(_c(warm, NV)), _p(_c(ctrl, NU)), float(friction),
+                              _p(_c(com, 3)), int(iterations), float(tol), int(ls_max), float(ls_tol), _p(M), _p(H))
+    return M, H
+
+
+def ltl(A):
+    """The leaf-first factor A = L' L (L lower triangular, positive diagonal; eliminated from the last row up, as the
+    engine and MuJoCo factor M) of a symmetric positive definite A, float64."""
+    A = np.array(A, np.float64, copy=True)
+    n = len(A)
+    L = np.zeros_like(A)
+    for k in range(n - 1, -1, -1):
+        L[k, k] = np.sqrt(A[k, k])
+        L[k, :k] = A[k, :k] / L[k, k]
+        A[:k, :k] -= np.outer(L[k, :k], L[k, :k])
+    return L
 
 
 def smooth(qpos, qvel, ctrl, com):

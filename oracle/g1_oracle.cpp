@@ -61,6 +61,7 @@ struct World {
   // options 2 and 3 (1e-3 m) and the near-parallel rule's sin^2 threshold (1.2e-3), the reference's
   // DK_ADJ_NORMAL_EPS / DK_ADJ_PARALLEL_EPS (adjoint_contact.py:76-95).
   const double* qfrc;
+  double (*hfinal)[NV];  // the checker's hook: newton() writes H at its final zones here (or NULL)
   double (*freeze)[3];
   int freeze_mode;
   double normal_eps, parallel_eps;
@@ -68,6 +69,7 @@ struct World {
 
 void init_hooks(World& s) {
   s.qfrc = nullptr;
+  s.hfinal = nullptr;
   s.freeze = nullptr;
   s.freeze_mode = 0;
   s.normal_eps = 1e-3;
@@ -689,6 +691,15 @@ void newton(World& s, int iterations, double tol, int ls_max, double ls_tol) {
     if (improvement < tol || scale * gn < tol) break;
   }
   s.niter = it;
+  if (s.hfinal) {  // the checker's hook: H = M + J' D J on the rows in the quadratic zone at the final a*
+    for (int i = 0; i < NV; i++)
+      for (int j = 0; j < NV; j++) s.hfinal[i][j] = s.M[i][j];
+    for (int r = 0; r < s.nefc; r++) {
+      if (!(v.jar[r] < 0)) continue;
+      for (int i = 0; i < NV; i++)
+        for (int j = 0; j < NV; j++) s.hfinal[i][j] += s.efcJ[r][i] * s.efcD[r] * s.efcJ[r][j];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------- integration
@@ -941,22 +952,49 @@ void contact_geom_vjp(const World& s, const Contact& c, double db, const double*
       mode = (raw >= -1 && raw < 1) ? 2 : 3;
     }
   }
-  double v1[3], v2[3], v1b[3] = {0, 0, 0}, v2b[3] = {0, 0, 0};
-  for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; }
-  sphere_core_vjp(v1, sz1[0], v2, sz2[0], db, posb, nb, normal, s.normal_eps, v1b, v2b);
-  double a1b[3], a2b[3], db3[3] = {0, 0, 0};
-  for (int k = 0; k < 3; k++) { x1b[k] += v1b[k]; x2b[k] += v2b[k]; a1b[k] = x1 * v1b[k]; a2b[k] = x2 * v2b[k]; }
-  double x1bar = dot3(a1, v1b), x2bar = dot3(a2, v2b);
+  double v1[3], v2[3], v1b[3] = {0, 0, 0}, v2b[3] = {0, 0, 0}, dl[3], w[3], a1b[3], a2b[3], x1bar, x2bar;
+  for (int k = 0; k < 3; k++) { v1[k] = p1[k] + a1[k] * x1; v2[k] = p2[k] + a2[k] * x2; dl[k] = v2[k] - v1[k]; }
+  cross(a1, a2, w);
+  const double ww = dot3(w, w);  // = det without its cancellation
+  const bool wok = ww > 1e-12 * ma * mc;
   // near-parallel rule (normal options != 0; adjoint_contact.py:436-448): both parameters held where
   // sin^2(theta) < 1.2e-3
-  if (mode == 0 && normal != 0) {
-    double cr[3];
-    cross(a1, a2, cr);
-    if (dot3(cr, cr) < s.parallel_eps * ma * mc) { x1bar = 0; x2bar = 0; }
+  const bool held = mode == 0 && normal != 0 && ww < s.parallel_eps * ma * mc;
+  const double nu = std::sqrt(dot3(dl, dl));
+  if (mode == 0 && !held && wok && nu > 0) {
+    // both parameters free (adjoint_contact.py:449-465): v2 - v1 is normal to both axes, so the normal is
+    // n = sg w / |w| of the axes alone (dn = sg (I - n n') dw / |w|), the distance is stationary in x1, x2, and
+    // pos = v1 + n (r1 + dist / 2) moves with x1 through v1 only; the normal options scale this normal path by
+    // kappa(nu) nu (the exact derivative: 1). For the exact derivative this equals the general chain below; for the
+    // options it is the reference's definition
+    double n[3], t[3], tau[3], u1[3], u2[3];
+    for (int k = 0; k < 3; k++) n[k] = dl[k] / nu;
+    const double dist = nu - sz1[0] - sz2[0], hp = sz1[0] + 0.5 * dist, dt = db + 0.5 * dot3(n, posb);
+    for (int k = 0; k < 3; k++) t[k] = nb[k] + hp * posb[k];
+    const double nt = dot3(n, t);
+    const double knu = normal == 0 ? 1.0 : kappa(nu, normal, s.normal_eps) * nu;
+    double f = knu / std::sqrt(ww);
+    if (dot3(n, w) < 0) f = -f;
+    for (int k = 0; k < 3; k++) tau[k] = f * (t[k] - n[k] * nt);
+    cross(a2, tau, u1);
+    cross(tau, a1, u2);
+    for (int k = 0; k < 3; k++) { v2b[k] = n[k] * dt; v1b[k] = posb[k] - v2b[k]; }
+    for (int k = 0; k < 3; k++) {
+      x1b[k] += v1b[k]; x2b[k] += v2b[k];
+      a1b[k] = x1 * v1b[k] + u1[k]; a2b[k] = x2 * v2b[k] + u2[k];
+    }
+    x1bar = dot3(a1, posb);
+    x2bar = 0;
+  } else {
+    sphere_core_vjp(v1, sz1[0], v2, sz2[0], db, posb, nb, normal, s.normal_eps, v1b, v2b);
+    for (int k = 0; k < 3; k++) { x1b[k] += v1b[k]; x2b[k] += v2b[k]; a1b[k] = x1 * v1b[k]; a2b[k] = x2 * v2b[k]; }
+    x1bar = held ? 0 : dot3(a1, v1b);
+    x2bar = held ? 0 : dot3(a2, v2b);
   }
-  double mab = 0, mbb = 0, mcb = 0, ub = 0, vb = 0;
-  if (mode == 0) {
-    double N1b = x1bar / det, N2b = x2bar / det, detb = -x1bar * x1 / det - x2bar * x2 / det;
+  double mab = 0, mbb = 0, mcb = 0, ub = 0, vb = 0, db3[3] = {0, 0, 0};
+  if (mode == 0) {  // G's determinant as |a1 x a2|^2 where that is not rounding noise (adjoint_contact.py:472)
+    const double g = wok ? ww : det;
+    double N1b = x1bar / g, N2b = x2bar / g, detb = -x1bar * x1 / g - x2bar * x2 / g;
     mcb += N1b * u; ub += N1b * mc; mbb -= N1b * v; vb -= N1b * mb;
     mab += N2b * v; vb += N2b * ma; mbb -= N2b * u; ub -= N2b * mb;
     mab += detb * mc; mcb += detb * ma; mbb -= 2 * mb * detb;
@@ -1283,6 +1321,30 @@ int g1o_step_mt(int nthreads, int nw, const double* qpos, const double* qvel, co
     });
   }
   for (auto& th : pool) th.join();
+  return 0;
+}
+
+// One substep of one world (the checker's view of a tape record): M (NV x NV) at the input state, and H = M + J'DJ at
+// Newton's final zones (NV x NV), with the given warm start and solver settings.
+int g1o_substep_hessian(const double* qpos, const double* qvel, const double* warm, const double* ctrl, double fric,
+                        const double* com, int iterations, double tol, int ls_max, double ls_tol, double* M,
+                        double* H) {
+  World* s = new World;
+  init_hooks(*s);
+  std::memcpy(s->qpos, qpos, sizeof(double) * NQ);
+  std::memcpy(s->qvel, qvel, sizeof(double) * NV);
+  std::memcpy(s->qacc, warm, sizeof(double) * NV);
+  std::memcpy(s->com, com, sizeof(double) * 3);
+  s->fric = fric;
+  s->flags = 0;
+  s->flops = 0;
+  s->hfinal = reinterpret_cast<double (*)[NV]>(H);
+  smooth(*s, ctrl);
+  std::memcpy(M, s->M, sizeof(s->M));
+  collision(*s);
+  rows(*s);
+  newton(*s, iterations, tol, ls_max, ls_tol);
+  delete s;
   return 0;
 }
 

@@ -294,6 +294,54 @@ def test_variant_entries_bound_as_the_reference(ffi):
             assert torch.equal(a, b), (kv, n)
 
 
+# 65 config-4 states (synthetic.states(4096, config=4, seed=1000 + s), world w) with capsule-capsule self contacts at
+# the input state whose two segment parameters are both free, found among 163,840 such states: every one of the 39
+# contacts at nu < 2 cm with sin^2(theta) < 0.01 (near parallel, above the near-parallel rule's 1.2e-3), and 48
+# contacts drawn from those at nu < 1 cm (nu: the segments' distance), as (s, w)
+CAPSULE_STATES = [
+    (0, 613), (0, 882), (0, 1502), (0, 2914), (0, 3474), (1, 1071), (1, 1723), (1, 1762), (1, 2914),
+    (3, 620), (3, 1366), (3, 2392), (4, 3218), (4, 3877), (6, 1623), (6, 1652), (6, 1819), (8, 1064),
+    (8, 4000), (9, 1352), (10, 705), (10, 1400), (10, 2408), (11, 1814), (11, 2470), (11, 3345), (15, 1662),
+    (15, 2025), (15, 3524), (16, 1636), (16, 2619), (18, 3187), (19, 161), (19, 515), (19, 3009), (20, 28),
+    (20, 572), (20, 2034), (20, 2218), (21, 88), (21, 215), (21, 1880), (21, 2554), (23, 1945), (24, 2435),
+    (24, 2891), (25, 421), (25, 4056), (26, 235), (27, 1466), (28, 2894), (28, 2935), (29, 4014), (31, 3474),
+    (31, 3665), (32, 47), (33, 859), (33, 1660), (33, 1755), (33, 3275), (34, 336), (36, 358), (36, 2004),
+    (37, 1200), (38, 3240),
+]
+
+
+def test_capsule_both_free_vjp(ffi):
+    """The capsule-capsule contact VJP with both segment parameters free, written without 1 / nu
+    (adjoint_contact.py:436-465: the normal n = sg (a1 x a2) / |a1 x a2| of the axes alone; the general chain sums
+    terms of order 1 / nu that cancel, losing up to 1e-3 relative in float32 at nu = 5 mm), on the CAPSULE_STATES:
+    one substep at 50 iterations against the float64 oracle's analytic VJP of the same variant, exact mode and the
+    interface default: per world relative error median <= 1e-4, p90 <= 1e-3, max <= 1e-2 (the general chain's max
+    here was 70)."""
+    import torch
+    cache, st = {}, {k: [] for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")}
+    for s_, w in CAPSULE_STATES:
+        if s_ not in cache:
+            cache[s_] = synthetic.states(4096, config=4, seed=1000 + s_)
+        for k in st:
+            st[k].append(cache[s_][k][w])
+    st = {k: np.array(v) for k, v in st.items()}
+    n = len(CAPSULE_STATES)
+    cq, cv = synthetic.cotangents(n, seed=7)
+    s64 = {k: v.astype(np.float64) for k, v in st.items()}
+    args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    r = ffi.forward(*args, iterations=50, substeps=1, tape=True)
+    for kv, nm in ((1, 0), (0, 3)):
+        gq, gv, gu, _ = ffi.backward(r[4], args[4], args[5], _t(cq), _t(cv), substeps=1, clamp_kv=kv, normal=nm)
+        torch.cuda.synchronize()
+        g = _blocks(s64, *(x.cpu().numpy().astype(np.float64) for x in (gq, gv, gu)))
+        ref = _blocks(s64, *oracle.vjp(**s64, g_qpos=cq, g_qvel=cv, clamp_kv=kv, normal=nm,
+                                       **dict(oracle.TRUTH, nsub=1)))
+        e = _rel_rows(g, ref)
+        print(f"capsule both-free ({n} states) clamp_kv={kv} normal={nm}: median {np.median(e):.3g} p90 "
+              f"{np.percentile(e, 90):.3g} max {e.max():.3g}")
+        assert np.median(e) <= 1e-4 and np.percentile(e, 90) <= 1e-3 and e.max() <= 1e-2
+
+
 def test_dispatch_order_does_not_change_results(ffi):
     """The C entries with a work buffer dispatch the worlds heaviest first; without one (NULL) in index order. The
     outputs, the tape and the gradients are bitwise the same both ways (contact-heavy config-4 states, where the

@@ -2,13 +2,14 @@
 the contact check of scripts/engine_step_check.py): the contacts of a substep (ocon) against MuJoCo Warp 3.17's on the
 corpus states; the tape's state chain (record k holds the state after k substeps, bitwise the k-substep forward's
 outputs); its contact table against the substep's contacts; and record coverage (a buffer prefilled with 0xA5 bytes
-gives bitwise the tape of a zeroed one)."""
+gives bitwise the tape of a zeroed one); the taped factors L_Q and L_H against float64 (T4 / T5)."""
 import ctypes
 import os
 
 import numpy as np
 import pytest
 
+import oracle
 from nablaengine_amd import synthetic
 
 pytestmark = pytest.mark.gpu
@@ -124,3 +125,54 @@ def test_tape_record_coverage(ffi):
     *_, t0 = _forward(ffi, args, 4, tape_fill=0)
     *_, t1 = _forward(ffi, args, 4, tape_fill=int(np.int32(np.uint32(0xA5A5A5A5))))
     assert torch.equal(t0.view(torch.int32), t1.view(torch.int32))
+
+
+REC_FLAGS, REC_LH, REC_LQ = 1, 200, 832
+NTRI = 35 * 36 // 2
+
+
+def _unpack(words):
+    """A packed lower triangle (row i, column j <= i at i (i + 1) / 2 + j) as a dense (35, 35) float64 matrix."""
+    L = np.zeros((35, 35))
+    L[np.tril_indices(35)] = words[:NTRI]
+    return L
+
+
+@pytest.mark.parametrize("config", [1, 4])
+def test_taped_factors_vs_oracle(ffi, config):
+    """The reference's tape checks T4 / T5 (docs/verification.md:131-132) at 50 Newton iterations: every record's L_Q
+    against the float64 leaf-first factor of M + h diag(kv) at the record's input state (oracle.smooth's M,
+    oracle.ltl), relative max-norm error <= 1e-5; and L_H' L_H against the float64 Hessian M + J'DJ at Newton's final
+    zones of that substep (oracle.substep_hessian from the record's state and warm start: the previous record's a*),
+    median <= 1e-5 and p95 <= 1e-4 over the records without overflow or non-convergence flags (a record whose float32
+    and float64 solves end in different zones differs by a row's D J J')."""
+    import torch
+    B = 128
+    st = synthetic.states(B, config=config)
+    args = [_t(st[k]) for k in KEYS]
+    r = ffi.forward(*args, iterations=50, tape=True)
+    torch.cuda.synchronize()
+    tape = r[4].cpu().numpy().reshape(B, 4, -1)
+    flags = tape[:, :, REC_FLAGS].view(np.uint32)
+    m = synthetic.model()
+    hkv = m["timestep"] * np.diag(np.asarray(m["dof_kv"]))
+    eq, eh = [], []
+    for w in range(B):
+        warm = st["warm"][w].astype(np.float64)
+        for k in range(4):
+            rec = tape[w, k].astype(np.float64)
+            q, v = rec[REC_QPOS:REC_QPOS + 36], rec[REC_QVEL:REC_QVEL + 35]
+            u, f, c = st["ctrl"][w].astype(np.float64), float(st["friction"][w]), st["com"][w].astype(np.float64)
+            M, H = oracle.substep_hessian(q, v, warm, u, f, c)
+            LQ, LH = _unpack(rec[REC_LQ:]), _unpack(rec[REC_LH:])
+            ref = oracle.ltl(M + hkv)
+            eq.append(np.abs(LQ - ref).max() / np.abs(ref).max())
+            if not flags[w, k] & (4 | 16 | (1 << 9)):
+                eh.append(np.abs(LH.T @ LH - H).max() / np.abs(H).max())
+            warm = rec[REC_ASTAR:REC_ASTAR + 35]
+    eq, eh = np.array(eq), np.array(eh)
+    print(f"config {config}: L_Q vs float64 ({len(eq)} records) median {np.median(eq):.3g} max {eq.max():.3g}; "
+          f"L_H'L_H vs float64 H ({len(eh)} records) median {np.median(eh):.3g} p95 {np.percentile(eh, 95):.3g} "
+          f"max {eh.max():.3g}")
+    assert eq.max() <= 1e-5
+    assert len(eh) >= 3 * B and np.median(eh) <= 1e-5 and np.percentile(eh, 95) <= 1e-4

@@ -362,6 +362,42 @@ def test_ten_iteration_tail_is_the_iteration_cap():
     assert e20.max() < 1e-13
 
 
+def test_ltl_is_the_reversed_cholesky():
+    """oracle.ltl (the leaf-first factor A = L' L) against a textbook routine: with J the order reversal, J A J = C C'
+    (numpy's Cholesky), so L = J C' J; on random SPD matrices and on M + h kv of a state."""
+    rng = np.random.default_rng(3)
+    mats = [X @ X.T + 35 * np.eye(35) for X in rng.normal(size=(4, 35, 35))]
+    st = synthetic.states(2, config=1, dtype=np.float64)
+    M = oracle.smooth(st["qpos"][0], st["qvel"][0], st["ctrl"][0], st["com"][0])[0]
+    mats.append(M + MODEL["timestep"] * np.diag(KV))
+    for A in mats:
+        C = np.linalg.cholesky(A[::-1, ::-1])
+        assert np.allclose(oracle.ltl(A), C.T[::-1, ::-1], rtol=1e-12, atol=1e-12 * np.abs(A).max())
+
+
+def test_substep_hessian_against_fd():
+    """oracle.substep_hessian's H (M + J'DJ at Newton's final zones) against finite differences of the step: at one
+    substep the step's warm' output is a*, and within the final zones a* moves with a generalized force f added to
+    qfrc_smooth as d a* / d f = H^-1 (the optimality condition M a - qfrc_smooth - f - J' f_c(a) = 0 is linear there).
+    H^-1 from central differences (oracle qfrc hook) agrees to 1e-6 relative, on 8 config-1 states with active
+    constraint rows; H is symmetric."""
+    st = synthetic.states(8, config=1, dtype=np.float64)
+    fd = 1e-5
+    for w in range(8):
+        s1 = {k: v[w:w + 1] for k, v in st.items()}
+        M, H = oracle.substep_hessian(*(s1[k][0] for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")))
+        Q = np.zeros((2 * oracle.NV, oracle.NV))
+        for j in range(oracle.NV):
+            Q[2 * j, j], Q[2 * j + 1, j] = fd, -fd
+        rep = {k: np.repeat(v, 2 * oracle.NV, axis=0) for k, v in s1.items()}
+        _, _, ow, _ = oracle.step(**rep, qfrc=Q, **ONE_SUBSTEP)
+        Jw = ((ow[0::2] - ow[1::2]) / (2 * fd)).T  # d a* / d f, column j: f_j
+        Hi = np.linalg.inv(H)
+        assert np.abs(Jw - Hi).max() < 1e-6 * np.abs(Hi).max(), w
+        assert np.abs(H - H.T).max() <= 1e-14 * np.abs(H).max()
+        assert np.abs(H - M).max() > 1e-3 * np.abs(M).max()  # the states have active constraint rows
+
+
 def test_flop_count_closed_form():
     """The algorithmic flop count: per world-step 4 x (smooth 2.5e4 + 2 x 3.1e4 factor-solves + 5e3 broadphase) plus
     the contact and Newton terms, so between 4.6e5 (no contacts, no iteration) and 1e7 on config-1 states."""
