@@ -17,6 +17,13 @@ Parity status of each function (how it is pinned; the tests that pin it are name
   ``smooth`` (each joint's torque from the weight of its subtree at its subtree COM) in
   ``tests/test_oracle_kinematics.py``.
 - ``kinematics_vjp``: central differences of ``kinematics`` (float64, h = 1e-6), brute force.
+- ``vjp``: exact mode by central differences of ``step`` and MuJoCo's ``fd_vjp`` (``tests/test_oracle.py``); clamp_kv 0 / 2
+  through lambda measured by central differences in an applied generalized force (the ``qfrc`` hook), normal 1 / 2 / 3
+  through the VJP's affine dependence on kappa(nu) (the ``normal_eps`` argument), the near-parallel rule by central
+  differences of the forward with frozen segment parameters (the ``freeze`` hook, ``parallel_eps``).
+- ``fd_vjp``, ``step_mt``: against ``fd_jacobian`` / ``step`` (the same arithmetic, batched / threaded).
+- ``substep_hessian``: H^-1 against central differences of a* in an applied generalized force; ``ltl`` against numpy's
+  Cholesky of the order-reversed matrix.
 """
 
 import ctypes
