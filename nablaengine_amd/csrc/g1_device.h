@@ -6,6 +6,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "g1_tables.h"
 
 namespace g1k {
@@ -169,6 +171,21 @@ __device__ __forceinline__ int wscan_excl(int v, int lane) {
 }
 __device__ __forceinline__ void wsync() { __syncthreads(); }
 
+// x with lane L's value replaced by 0 (v_writelane_b32 with the lane an inline constant: one instruction, no compare)
+template <int L>
+__device__ __forceinline__ float zero_lane(float x) {
+  asm("v_writelane_b32 %0, 0, %1" : "+v"(x) : "n"(L));
+  return x;
+}
+// f(std::integral_constant<int, I>) for I = A, A + S, ... while I != B (unrolled, I a compile-time constant)
+template <int A, int B, int S, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (A != B) {
+    f(std::integral_constant<int, A>{});
+    static_for<A + S, B, S>(f);
+  }
+}
+
 // Phase profile (a G1_PROFILE build only): per world, s_memtime cycles of the forward's phases summed over the substeps
 // (lane 0's clock at phase ends, after a barrier), written to g_prof[world][phase] for the first PROF_WORLDS worlds
 // and read by dk_prof_read. The production build compiles every mark to nothing.
@@ -252,6 +269,7 @@ __host__ __device__ constexpr uint64_t fill_bits(int k) {
   return m;
 }
 static_assert(NV == 35, "the fill rows are the G1's dof ranges");
+static_assert(NV * (NV - 1) / 2 + 63 < LSINK + 64, "the unmasked row stores of the last row stay in the factor buffer");
 
 typedef float mfma4 __attribute__((ext_vector_type(4)));
 constexpr int NROOT = 6;  // the free joint's dofs: every other dof's ancestors
@@ -276,10 +294,14 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
 #pragma unroll
   for (int k = NV - 1; k >= 0; k--) {
     if (k == NROOT - 1) {
-      // the hinge rows are final: store them (lane j column j, rows m >= j; other lanes into their sink slot), then
-      // the root block's Schur complement on the matrix cores
+      // the hinge rows are final: store them, row m at tri(m, 0) + lane on every lane, rows in increasing order. A
+      // lane past the row (lane > m, or no column) writes into a later row's slots, which that row's own store
+      // overwrites afterwards (a wave's LDS stores land in program order), or for the last row into the padding and
+      // the sink (tri(34, 0) + 63 < LSINK + 64): no address arithmetic per store. Then the root block's Schur
+      // complement on the matrix cores
+      float* rowbase = Lp + lane;
 #pragma unroll
-      for (int m = NROOT; m < NV; m++) Lp[m >= lane && lane < NV ? tri(m, lane) : LSINK + lane] = c[m];
+      for (int m = NROOT; m < NV; m++) rowbase[tri(m, 0)] = c[m];
       __syncthreads();
       const int r = lane & 15, q = lane >> 4;
       mfma4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -309,7 +331,8 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
     for (int m = m0; m < k; m++)  // A[m][j] -= L[k][j] L[k][m] (the pattern's test at compile time)
       if (!SPARSE || (((TREE.dofanc[k] | (PATTERN ? fill_bits(k) : 0ull)) >> m) & 1ull)) c[m] = fmaf(-c[k], bc[m], c[m]);
   }
-  // lane j stores column j's root rows m >= j; the other lanes store into their sink slot (no branch per store)
+  // lane j stores column j's root rows m >= j; the other lanes store into their sink slot (the hinge rows are stored
+  // already: no write past a root row may reach them)
 #pragma unroll
   for (int m = 0; m < NROOT; m++) Lp[m >= lane && lane < NV ? tri(m, lane) : LSINK + lane] = c[m];
 }
@@ -326,31 +349,32 @@ __device__ __forceinline__ float ltl_solve(const float* Lp, float b, int lane_) 
   const int r = lane < NV ? lane : NV - 1;
   const float dself = lane < NV ? 1.f / Lp[tri(r, r)] : 0.f;
   float z = b * dself;  // (b - sum of the solved descendants' terms) / L[lane][lane]
-  // pass 1, step i: lanes r < i take L[i][r] = col[tri(i, 0)] (every lane's address inside L)
+  // pass 1, step i: lanes r < i take L[i][r] = col[tri(i, 0)] (every lane's address inside L); the lanes at or past
+  // i take 0 through dm, their copy of dself zeroed one lane a step (v_writelane: no compare and select per step)
   const float* col = Lp + r;
   float lv[NV];
 #pragma unroll
   for (int i = NV - 1; i >= 1; i--) lv[i] = col[tri(i, 0)];
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the chain
-#pragma unroll
-  for (int i = NV - 1; i >= 1; i--) {
-    const float l = lv[i] * dself;
-    const float lik = lane < i ? l : 0.f;
-    z = fmaf(-lik, rdl(z, i), z);
-  }
+  float dm = dself;
+  static_for<NV - 1, 0, -1>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    dm = zero_lane<i>(dm);  // lane i solves at this step
+    z = fmaf(-(lv[i] * dm), rdl(z, i), z);
+  });
   // z = y; root-first: x[lane] = (y[lane] - sum_{k < lane} L[lane][k] x[k]) / L[lane][lane]
-  // pass 2, step k: lanes r > k take L[r][k] = row[k] (every lane's address inside L)
+  // pass 2, step k: lanes r > k take L[r][k] = row[k] (every lane's address inside L); lanes up to k take 0 (dm)
   z *= dself;
   const float* row = Lp + tri(r, 0);
 #pragma unroll
   for (int k = 0; k < NV - 1; k++) lv[k] = row[k];
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int k = 0; k < NV - 1; k++) {
-    const float l = lv[k] * dself;
-    const float lkj = lane > k ? l : 0.f;
-    z = fmaf(-lkj, rdl(z, k), z);
-  }
+  dm = dself;
+  static_for<0, NV - 1, 1>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    dm = zero_lane<k>(dm);  // lane k is solved at this step
+    z = fmaf(-(lv[k] * dm), rdl(z, k), z);
+  });
   return z;
 }
 
