@@ -386,21 +386,26 @@ __constant__ inline Arr<float, 2> cPSolref = to_float(PAIR_SOLREF);
 __constant__ inline Arr<float, 5> cPSolimp = to_float(PAIR_SOLIMP);
 static_assert(JNT_SOLIMP[4] == 2.0 && PAIR_SOLIMP[4] == 2.0, "kbimp assumes the solimp power 2");
 
-// body spatial velocities of the dof vector v (LDS, NV): bw[b] = sum over b's chain of S_d v_d. The chain comes from
-// the LDS table in one load; every step's loads are independent of the others, so they are all in flight at once.
+// body spatial velocities of the dof vector v (LDS, NV + 1 entries, v[NV] = 0): bw[b] = sum over b's chain of S_d v_d.
+// Every body's chain starts with the root's 6 dofs, whose subspaces are S_0..2 = (0; e_k) and S_3..5 = (S_k's
+// angular part; 0): their part is v[0..2] and 3 columns, the same on every lane (broadcast loads). The hinge dofs
+// follow (chain entries 6..15); the table's padding byte 255 clamps to dof NV, whose S row and v entry are zero, so
+// every step is unconditional and needs no mask. The world body (lane 0) gets 0.
 __device__ __forceinline__ void body_vel(Sim& s, const float* v, int lane) {
   if (lane < NB) {
     unsigned ch[4];
     for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
-    float w[3] = {0.f, 0.f, 0.f}, u[3] = {0.f, 0.f, 0.f};
+    float w[3], u[3] = {v[0], v[1], v[2]};
+    for (int k = 0; k < 3; k++) w[k] = s.S[3][k] * v[3] + s.S[4][k] * v[4] + s.S[5][k] * v[5];
 #pragma unroll
-    for (int t = 0; t < MAXCHAIN; t++) {
-      bool on;
-      const int d = chain_dof(ch, t, &on);
-      const float vd = v[d] * (on ? 1.f : 0.f);  // d is a valid dof past the chain's end: every load unconditional
+    for (int t = NROOT; t < MAXCHAIN; t++) {
+      const unsigned b = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
+      const int d = (int)min(b, (unsigned)NV);
+      const float vd = v[d];
       for (int k = 0; k < 3; k++) { w[k] = fmaf(s.S[d][k], vd, w[k]); u[k] = fmaf(s.S[d][4 + k], vd, u[k]); }
     }
-    for (int k = 0; k < 3; k++) { s.u.nt.bw[lane][k] = w[k]; s.u.nt.bw[lane][4 + k] = u[k]; }
+    const float z = lane > 0 ? 1.f : 0.f;
+    for (int k = 0; k < 3; k++) { s.u.nt.bw[lane][k] = z * w[k]; s.u.nt.bw[lane][4 + k] = z * u[k]; }
   }
   wsync();
 }
@@ -1077,6 +1082,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane == 0) { s.fric = fric[w]; s.flags = 0; s.niter = 0; }
   s.dsub[lane] = lane < NV ? cTree.dofmask32[lane] : 0u;
   chain_table(s.chain, lane);
+  if (lane < 8) s.S[NV][lane] = 0.f;  // body_vel's zero padding row and entries
+  if (lane == 0) { s.qvel[NV] = 0.f; s.qacc[NV] = 0.f; s.p[NV] = 0.f; }
 #ifdef G1_PROFILE
   if (lane < NPHASE) s.prof_acc[lane] = 0;
   if (lane == 0) {
