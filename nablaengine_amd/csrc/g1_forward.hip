@@ -56,6 +56,14 @@ __device__ __forceinline__ void dof_motion(const Sim& s, int i, float* w, float*
   }
 }
 
+// Entry t of a chain-table row (the dofs moving a body, ascending; padding 255) for the row of dof `lane`, clamped to
+// lane: a chain's entries are lane's ancestor dofs and lane itself, so the clamp maps the padding and a root dof past
+// lane (the root rows' chains hold all 6 root dofs) to the diagonal. A row assembly then stores every entry
+// unconditionally: the clamped ones store the diagonal's value again.
+__device__ __forceinline__ int chain_dof_row(const unsigned* ch, int t, int lane) {
+  return (int)min((ch[t >> 2] >> (8 * (t & 3))) & 255u, (unsigned)lane);
+}
+
 // (n, f) = I (w, v) for a packed spatial inertia about O: n = J w + h x v, f = m v - h x w (source.py:305-313)
 __device__ __forceinline__ void apply_inertia(const float* J, const float* w, const float* v, float* n, float* f) {
   float hv[3], hw[3];
@@ -75,14 +83,13 @@ __device__ __forceinline__ void m_to_L(Sim& s, int lane, float dg) {
     const int bi = lane < 6 ? 1 : lane - 4;
     unsigned ch[4];
     for (int k = 0; k < 4; k++) ch[k] = s.chain[bi][k];
-    const float dd = dg * cKv[lane];
+    float* row = s.L + tri(lane, 0);
 #pragma unroll
     for (int t = 0; t < MAXCHAIN; t++) {
-      bool on;
-      const int j = chain_dof(ch, t, &on);
-      const float m = s.M[lane][j] + (j == lane ? dd : 0.f);
-      s.L[on && j <= lane ? tri(lane, j) : LSINK + lane] = m;
+      const int j = chain_dof_row(ch, t, lane);
+      row[j] = s.M[lane][j];
     }
+    row[lane] = s.M[lane][lane] + dg * cKv[lane];  // after the entries (same wave, program order)
   }
   wsync();
 }
@@ -246,19 +253,18 @@ __device__ void smooth(Sim& s, int lane) {
     for (int k = 0; k < 10; k++) Jb[k] = s.u.sm.Ic[bi][k];
     apply_inertia(Jb, w, v, n, f);
     // M[i][j] = S_j . I_c(body i) S_i on the chain of dof i's body (its ancestor dofs j <= i), both halves; the
-    // rest of M is zero (zero-filled above, earlier in this wave's LDS order)
+    // rest of M is zero (zero-filled above, earlier in this wave's LDS order). Two lanes never store the same entry:
+    // lane i writes row i and column i at j <= i (the entry (i, i) twice)
     unsigned ch[4];
     for (int k = 0; k < 4; k++) ch[k] = s.chain[bi][k];
     const float arm = cArm[lane];
 #pragma unroll
     for (int t = 0; t < MAXCHAIN; t++) {
-      bool on;
-      const int j = chain_dof(ch, t, &on);
+      const int j = chain_dof_row(ch, t, lane);
       const float mij = s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0] + s.S[j][5] * f[1]
                         + s.S[j][6] * f[2] + (j == lane ? arm : 0.f);
-      const bool st = on && j <= lane;  // else both stores go to the row's unused column 35 (no branch)
-      s.M[lane][st ? j : MSTRIDE - 1] = mij;
-      s.M[st ? j : lane][st ? lane : MSTRIDE - 1] = mij;
+      s.M[lane][j] = mij;  // j <= lane: both halves (the clamped entries store the diagonal again)
+      s.M[j][lane] = mij;
     }
     float act = 0.f;
     if (lane >= 6) {
@@ -608,21 +614,20 @@ __device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con
     // independent of the stores into L), then the stores of the chain's entries
     unsigned ch[4];
     for (int k = 0; k < 4; k++) ch[k] = s.chain[bi][k];
+    float* row = s.L + tri(lane, 0);
 #pragma unroll
     for (int t0 = 0; t0 < MAXCHAIN; t0 += 8) {  // 8 entries a batch
       float hv[8];
-      int ha[8];
-      bool hon[8];
+      int hj[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const int j = chain_dof(ch, t0 + e, &hon[e]);
-        hon[e] = hon[e] && j <= lane;
-        ha[e] = tri(lane, j <= lane ? j : lane);
+        const int j = chain_dof_row(ch, t0 + e, lane);
+        hj[e] = j;
         hv[e] = s.M[lane][j] + (s.S[j][0] * n[0] + s.S[j][1] * n[1] + s.S[j][2] * n[2] + s.S[j][4] * f[0]
                                 + s.S[j][5] * f[1] + s.S[j][6] * f[2]);
       }
 #pragma unroll
-      for (int e = 0; e < 8; e++) s.L[hon[e] ? ha[e] : LSINK + lane] = hv[e];
+      for (int e = 0; e < 8; e++) row[hj[e]] = hv[e];  // the clamped entries store the diagonal's value again
     }
     if (R.lsg != 0.f && R.ljar < 0.f) s.L[tri(lane, lane)] += R.lD;
   }
