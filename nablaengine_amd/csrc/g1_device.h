@@ -78,7 +78,14 @@ __device__ __forceinline__ int prefix_count(unsigned long long m, int lane) {  /
 // scalar. A fixed order on every call (bitwise deterministic); lanes without a DPP source add +0.
 #define G1_DPP(x, ctrl, rmask) \
   __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), (ctrl), (rmask), 0xf, false))
+// A reduction's input as an opaque value: its first step then stays one v_add_f32_dpp, where otherwise a product
+// input is contracted with the first add into an FMA of the DPP-moved value (a zero move, a v_mov_b32_dpp and the FMA)
+__device__ __forceinline__ float opaque(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 __device__ __forceinline__ float wsum(float v) {
+  v = opaque(v);
   v += G1_DPP(v, 0x111, 0xf);  // row_shr:1
   v += G1_DPP(v, 0x112, 0xf);  // row_shr:2
   v += G1_DPP(v, 0x114, 0xf);  // row_shr:4
@@ -88,6 +95,8 @@ __device__ __forceinline__ float wsum(float v) {
   return rdl(v, 63);
 }
 __device__ __forceinline__ float2 wsum2(float a, float b) {
+  a = opaque(a);
+  b = opaque(b);
   a += G1_DPP(a, 0x111, 0xf); b += G1_DPP(b, 0x111, 0xf);
   a += G1_DPP(a, 0x112, 0xf); b += G1_DPP(b, 0x112, 0xf);
   a += G1_DPP(a, 0x114, 0xf); b += G1_DPP(b, 0x114, 0xf);
@@ -100,6 +109,8 @@ __device__ __forceinline__ float2 wsum2(float a, float b) {
 // the n chains interleaved, so every step's n instructions are independent of each other
 template <int N>
 __device__ __forceinline__ void wsum_n(float* x) {
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] = opaque(x[e]);
 #pragma unroll
   for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x111, 0xf);
 #pragma unroll
@@ -131,6 +142,8 @@ __device__ __forceinline__ unsigned wor(unsigned v) {
 // 32, 6 for 64; width uniform. The same fixed order on every call with the same width.
 template <int N>
 __device__ __forceinline__ void wsum_nw(float* x, int width) {
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] = opaque(x[e]);
 #pragma unroll
   for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x111, 0xf);
 #pragma unroll
@@ -271,8 +284,48 @@ __host__ __device__ constexpr uint64_t fill_bits(int k) {
 static_assert(NV == 35, "the fill rows are the G1's dof ranges");
 static_assert(NV * (NV - 1) / 2 + 63 < LSINK + 64, "the unmasked row stores of the last row stay in the factor buffer");
 
+// The hinge dofs are eliminated first; each would update the 6 x 6 root block (rows and columns 0..5) by the outer
+// product of its row's root part, 6 broadcasts and FMAs a step that only lanes 0..5 use (174 of the tree pattern's 306
+// pairs). These updates are summed instead as one product on the matrix cores, the Schur complement
+// D = X' X with X[k][r] = L[k][r] (hinge rows k = 6..34, root columns r < 6; 29 rows padded to 32): 8 steps of
+// v_mfma_f32_16x16x4f32, lane l giving A[l % 16][k'] = B[k'][l % 16] = X[6 + k'][l % 16] for k' = 4 t + l / 16 (read
+// back from the factor's hinge rows, stored first), lane l holding D[4 (l / 16) + e][l % 16]. Then the root block is
+// eliminated as before.
+// The elimination order. Any order that eliminates a dof after all its descendants gives the same factor; for the
+// tree's pattern the four branches below the root and waist (right arm 34..28, left arm 27..21, right leg 17..12, left
+// leg 11..6) are independent chains, interleaved two at a time so that consecutive steps do not wait on each other;
+// then the waist (20..18) and the root (5..0). With the self-contact fill (rows 18..27 and 12..17 gain leg columns) and
+// dense, the descending order.
 typedef float mfma4 __attribute__((ext_vector_type(4)));
 constexpr int NROOT = 6;  // the free joint's dofs: every other dof's ancestors
+struct Order { int v[NV]; };
+constexpr Order elim_order(bool tree) {
+  Order o{};
+  int n = 0;
+  if (tree) {
+    for (int t = 0; t < 7; t++) { o.v[n++] = 34 - t; o.v[n++] = 27 - t; }
+    for (int t = 0; t < 6; t++) { o.v[n++] = 17 - t; o.v[n++] = 11 - t; }
+    for (int k = 20; k >= 18; k--) o.v[n++] = k;
+    for (int k = NROOT - 1; k >= 0; k--) o.v[n++] = k;
+  } else {
+    for (int k = NV - 1; k >= 0; k--) o.v[n++] = k;
+  }
+  return o;
+}
+constexpr bool order_ok(const Order& o) {  // a permutation, each dof after all of its descendants (tree pattern)
+  bool seen[NV] = {};
+  for (int s = 0; s < NV; s++) {
+    const int k = o.v[s];
+    if (k < 0 || k >= NV || seen[k]) return false;
+    for (int d = k + 1; d < NV; d++)
+      if (((TREE.dofanc[d] >> k) & 1ull) && !seen[d]) return false;
+    seen[k] = true;
+  }
+  return true;
+}
+static_assert(order_ok(elim_order(true)) && order_ok(elim_order(false)), "elimination orders");
+static_assert(TREE.dofanc[34] >> 18 & 1 && TREE.dofanc[27] >> 18 & 1 && !(TREE.dofanc[27] >> 28 & 1) &&
+              !(TREE.dofanc[17] >> 6 & 1), "the G1's branches: arms 21..27 / 28..34 below the waist, legs 6..11 / 12..17");
 
 // The hinge dofs are eliminated first; each would update the 6 x 6 root block (rows and columns 0..5) by the outer
 // product of its row's root part, 6 broadcasts and FMAs a step that only lanes 0..5 use (174 of the tree pattern's 306
@@ -284,6 +337,7 @@ constexpr int NROOT = 6;  // the free joint's dofs: every other dof's ancestors
 template <int PATTERN>  // 0: the tree's sparsity; 1: with the common self-contact fill; 2: every pair
 __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
   constexpr bool SPARSE = PATTERN < 2;
+  constexpr Order ORD = elim_order(PATTERN == 0);
   const int lane = opaque_lane(lane_);
   // column j = lane of the lower triangle: A[m][j] = col[tri(m, 0)] for m >= j; every lane's address inside the
   // matrix (lanes past the column select 0), all the loads issued before the elimination
@@ -291,9 +345,9 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
   float c[NV];
 #pragma unroll
   for (int m = 0; m < NV; m++) c[m] = col[tri(m, 0)];
-#pragma unroll
-  for (int k = NV - 1; k >= 0; k--) {
-    if (k == NROOT - 1) {
+  static_for<0, NV, 1>([&](auto sc) {
+    constexpr int k = ORD.v[decltype(sc)::value];
+    if constexpr (k == NROOT - 1) {
       // the hinge rows are final: store them, row m at tri(m, 0) + lane on every lane, rows in increasing order. A
       // lane past the row (lane > m, or no column) writes into a later row's slots, which that row's own store
       // overwrites afterwards (a wave's LDS stores land in program order), or for the last row into the padding and
@@ -322,7 +376,7 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
     c[k] *= __builtin_amdgcn_rsqf(d);
     // every broadcast of the step first, then the updates: a v_readlane's SGPR is not read by the next instruction;
     // a hinge step's updates of the root rows are left to the Schur complement above
-    const int m0 = k >= NROOT ? NROOT : 0;
+    constexpr int m0 = k >= NROOT ? NROOT : 0;
     float bc[NV];
 #pragma unroll
     for (int m = m0; m < k; m++)
@@ -330,7 +384,7 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
 #pragma unroll
     for (int m = m0; m < k; m++)  // A[m][j] -= L[k][j] L[k][m] (the pattern's test at compile time)
       if (!SPARSE || (((TREE.dofanc[k] | (PATTERN ? fill_bits(k) : 0ull)) >> m) & 1ull)) c[m] = fmaf(-c[k], bc[m], c[m]);
-  }
+  });
   // lane j stores column j's root rows m >= j; the other lanes store into their sink slot (the hinge rows are stored
   // already: no write past a root row may reach them)
 #pragma unroll
