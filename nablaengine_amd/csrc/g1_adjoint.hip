@@ -79,7 +79,7 @@ __device__ __forceinline__ void st_sv6(float* p, const Sv& x) {
 struct __align__(16) Adj {
   float qpos[40], qvel[36], astar[36], aadv[36], at[36];
   float qb[36], vb[36], vt[36], qn[36], y[36], lam[36], ub[32], ctrl[32], com[4];
-  float S[NV][8];
+  float S[NV + 1][8];                 // row NV is zero, as the dof vectors' entry NV (the chain padding's target)
   float Q[NB][4], X[NB][4];
   float hl[NB][12];                  // each hinge body's local transform: q_l, p_b, a_l (as the forward's FK)
   unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
@@ -554,28 +554,36 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   if (lane < NV) s.lam[lane] = lam;
   wsync();
   APROF(AP_SOLVE);
-  // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body
+  // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body. Every
+  // body's chain starts with the root's 6 dofs, S_0..2 = (0; e_k) and S_3..5 = (w_k; 0): their part of a twist is
+  // (sum_k w_k x_{3+k}; x_0..2), the same on every lane, and their RNE term, V x (S_r v_r) summed over r = 3..5 with
+  // V = (w; u) the root's velocity twist, is (w x w; u x w) = (0; u x w). The hinge dofs follow (chain entries 6..15);
+  // the padding byte 255 clamps to dof NV, whose S row and entries are zero, so every step is unconditional.
   if (lane >= 1 && lane < NB) {
-    Sv V = sv0(), Lm = sv0(), Y = sv0(), Aw = sv0(), A2 = sv0(), Ac = sv0();
     unsigned ch[4];
     for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
-    for (int t = 0; t < MAXCHAIN; t++) {
-      bool on;
-      const int d = chain_dof(ch, t, &on);
-      if (on) {
-        const Sv Sd = ld_sv(s.S[d]);
-        const float vd = s.qvel[d];
-        V = sv_add(V, Sd, vd);
-        Lm = sv_add(Lm, Sd, s.lam[d]);
-        Y = sv_add(Y, Sd, s.y[d]);
-        Aw = sv_add(Aw, Sd, s.astar[d]);
-        A2 = sv_add(A2, Sd, s.at[d]);
-        if (d == 5) {
-          for (int r = 3; r < 6; r++) Ac = sv_add(Ac, cross_mm(V, ld_sv(s.S[r])), s.qvel[r]);
-        } else if (d >= 6) {
-          Ac = sv_add(Ac, cross_mm(V, Sd), vd);
-        }
+    const auto root = [&](const float* x) {
+      Sv r;
+      for (int k = 0; k < 3; k++) {
+        r.w[k] = s.S[3][k] * x[3] + s.S[4][k] * x[4] + s.S[5][k] * x[5];
+        r.v[k] = x[k];
       }
+      return r;
+    };
+    Sv V = root(s.qvel), Lm = root(s.lam), Y = root(s.y), Aw = root(s.astar), A2 = root(s.at), Ac = sv0();
+    cross(V.v, V.w, Ac.v);
+#pragma unroll
+    for (int t = NROOT; t < MAXCHAIN; t++) {
+      const unsigned b = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
+      const int d = (int)min(b, (unsigned)NV);
+      const Sv Sd = ld_sv(s.S[d]);
+      const float vd = s.qvel[d];
+      V = sv_add(V, Sd, vd);
+      Lm = sv_add(Lm, Sd, s.lam[d]);
+      Y = sv_add(Y, Sd, s.y[d]);
+      Aw = sv_add(Aw, Sd, s.astar[d]);
+      A2 = sv_add(A2, Sd, s.at[d]);
+      Ac = sv_add(Ac, cross_mm(V, Sd), vd);
     }
     Sv A1 = sv_add(Aw, Ac);
     for (int k = 0; k < 3; k++) A1.v[k] -= kGrav[k];
@@ -876,6 +884,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   }
 #endif
   chain_table(s.chain, lane);
+  if (lane < 8) s.S[NV][lane] = 0.f;  // the twists' zero padding row and entries (nothing else writes them)
+  if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
   // the output cotangents in the tangent space at the output state (its root quaternion: the last substep's
   // integration replayed from the record)
   if (lane < NV) s.vb[lane] = gv_out[(size_t)w * NV + lane];
