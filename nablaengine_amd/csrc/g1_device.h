@@ -169,6 +169,31 @@ __device__ __forceinline__ void wsum_nw(float* x, int width) {
 #pragma unroll
   for (int e = 0; e < N; e++) x[e] = rdl(x[e], 63);
 }
+// inclusive prefix sums of n values over the first `width` lanes (wsum_nw's DPP steps without the broadcast): lane
+// l < width holds the sum over lanes 0..l; lanes past width hold partial sums of their own rows
+template <int N>
+__device__ __forceinline__ void wscan_nw(float* x, int width) {
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] = opaque(x[e]);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x111, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x112, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x114, 0xf);
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x118, 0xf);
+  if (width <= 16) return;
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x142, 0xa);
+  if (width <= 32) return;
+#pragma unroll
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x143, 0xc);
+}
+// lane src's x (src per lane; ds_bpermute: the LDS unit's crossbar, no memory access)
+__device__ __forceinline__ float lane_of(float x, int src) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(x)));
+}
 __device__ __forceinline__ int wsumi(int v) {  // small counts: exact in float
   return (int)wsum((float)v);
 }
@@ -324,8 +349,9 @@ constexpr bool order_ok(const Order& o) {  // a permutation, each dof after all 
   return true;
 }
 static_assert(order_ok(elim_order(true)) && order_ok(elim_order(false)), "elimination orders");
-static_assert(TREE.dofanc[34] >> 18 & 1 && TREE.dofanc[27] >> 18 & 1 && !(TREE.dofanc[27] >> 28 & 1) &&
-              !(TREE.dofanc[17] >> 6 & 1), "the G1's branches: arms 21..27 / 28..34 below the waist, legs 6..11 / 12..17");
+static_assert(((TREE.dofanc[34] >> 18) & 1) != 0 && ((TREE.dofanc[27] >> 18) & 1) != 0 &&
+              ((TREE.dofanc[27] >> 28) & 1) == 0 && ((TREE.dofanc[17] >> 6) & 1) == 0,
+              "the G1's branches: arms 21..27 / 28..34 below the waist, legs 6..11 / 12..17");
 
 // The hinge dofs are eliminated first; each would update the 6 x 6 root block (rows and columns 0..5) by the outer
 // product of its row's root part, 6 broadcasts and FMAs a step that only lanes 0..5 use (174 of the tree pattern's 306

@@ -587,23 +587,37 @@ __device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con
   const float w[3] = {s.S[il][0], s.S[il][1], s.S[il][2]}, v[3] = {s.S[il][4], s.S[il][5], s.S[il][6]};
   float n[3] = {0.f, 0.f, 0.f}, f[3] = {0.f, 0.f, 0.f};
   float K[21];
-  contact_stiffness(R, d, floorc, K);
-  for (unsigned long long rem = ballot(floorc); rem;) {  // one distinct contact body B a pass
-    const int B = rdli(R.b2, __builtin_ctzll(rem));
-    const bool in = floorc && R.b2 == B;
-    rem &= ~ballot(in);
+  contact_stiffness(R, d, floorc, K);  // exactly 0 off the active floor contacts (Rows are zero past the contacts)
+  const bool floorl = lane < s.ncon && R.b1 == 0;
+  const unsigned long long fl = ballot(floorl);
+  if (fl) {
+    // The floor contacts are the lanes [0, nf) sorted by body, and dof i's subtree is the body range
+    // [ctz(dm), 32 - clz(dm)) (both by the tables' order, checked at compile time), so the floor contacts on the
+    // bodies dof i moves are the lanes [lo, hi): their stiffness sum is P[hi - 1] - P[lo - 1] with P the prefix sums
+    // of K over the lanes. lo and hi come from the last lane of each contact body's run; P[-1] reads lane 63 and is
+    // multiplied by 0 (for hi = 0 both reads are lane 63 and cancel).
+    const int nf = __popcll(fl);
+    wscan_nw<21>(K, nf);
+    const int bnext = __shfl_down(R.b2, 1, WL);
+    const unsigned long long ends = ballot(floorl && (lane == nf - 1 || bnext != R.b2));
+    const int bs = dm ? __builtin_ctz(dm) : NB, be = dm ? 32 - __builtin_clz(dm) : NB;
+    int lo = 0, hi = 0;
+    for (unsigned long long m = ends; m; m &= m - 1ull) {  // one contact body a step, in body order (all lanes)
+      const int e = __builtin_ctzll(m), B = rdli(R.b2, e);
+      lo = B < bs ? e + 1 : lo;
+      hi = B < be ? e + 1 : hi;
+    }
+    const float cl = (lo > 0 || hi == 0) ? 1.f : 0.f;
     float k[21];
 #pragma unroll
-    for (int e = 0; e < 21; e++) k[e] = in ? K[e] : 0.f;
-    wsum_nw<21>(k, s.ncon);  // contact lanes only
-    if ((dm >> B) & 1u) {  // n += Kaa w + Kal v, f += Kal' w + Kll v
-      n[0] += k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
-      n[1] += k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
-      n[2] += k[4] * w[0] + k[5] * w[1] + k[2] * w[2] + k[12] * v[0] + k[13] * v[1] + k[14] * v[2];
-      f[0] += k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
-      f[1] += k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
-      f[2] += k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
-    }
+    for (int e = 0; e < 21; e++) k[e] = fmaf(-lane_of(K[e], (lo - 1) & (WL - 1)), cl, lane_of(K[e], (hi - 1) & (WL - 1)));
+    // n = Kaa w + Kal v, f = Kal' w + Kll v
+    n[0] = k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
+    n[1] = k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
+    n[2] = k[4] * w[0] + k[5] * w[1] + k[2] * w[2] + k[12] * v[0] + k[13] * v[1] + k[14] * v[2];
+    f[0] = k[6] * w[0] + k[9] * w[1] + k[12] * w[2] + k[15] * v[0] + k[18] * v[1] + k[19] * v[2];
+    f[1] = k[7] * w[0] + k[10] * w[1] + k[13] * w[2] + k[18] * v[0] + k[16] * v[1] + k[20] * v[2];
+    f[2] = k[8] * w[0] + k[11] * w[1] + k[14] * w[2] + k[19] * v[0] + k[20] * v[1] + k[17] * v[2];
   }
   PROF(PH_HCOMP);
   // rows of H: zero, then M[i][j] + S_j . (n, f) on the ancestor dofs j of i (M's nonzeros are on these chains)

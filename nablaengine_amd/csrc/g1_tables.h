@@ -82,6 +82,28 @@ constexpr bool check_tree() {
 }
 static_assert(check_tree(), "the kernels assume <= 64 dofs, <= 32 bodies, <= 16 dofs per chain");
 
+// The Hessian's floor-contact prefix sums rely on two orders: each dof's bodies (its body's subtree) are one run of
+// body ids (bodies in depth-first order), and the floor pairs (g1 on the world body) come first in pair order,
+// sorted by g2's body, so the contacts, compacted in pair order, put the floor contacts in lanes [0, nf) by body.
+constexpr bool check_orders() {
+  for (int i = 0; i < NV; i++) {
+    const uint64_t m = TREE.dofmask32[i];
+    if (m == 0 || ((m + (m & (~m + 1))) & m) != 0) return false;
+  }
+  bool other = false;
+  int last = 0;
+  for (int p = 0; p < NPAIR; p++) {
+    if (GEOM_BODY[PAIR_G1[p]] == 0) {
+      if (other || GEOM_BODY[PAIR_G2[p]] < last || GEOM_BODY[PAIR_G2[p]] == 0) return false;
+      last = GEOM_BODY[PAIR_G2[p]];
+    } else {
+      other = true;
+    }
+  }
+  return true;
+}
+static_assert(check_orders(), "dofs' subtrees as body-id runs; floor pairs first, sorted by body");
+
 // geom type codes (mjtGeom): plane 0, sphere 2, capsule 3
 constexpr int GPLANE = 0, GSPHERE = 2, GCAPSULE = 3;
 
