@@ -47,6 +47,10 @@ struct Rows {
   int b1, b2, nr, dim;       // bodies, kept rows (0..4), condim
   float aref[4], jar[4];     // per pyramid edge (or the normal row)
   float lsg, lD, laref, ljar;  // the limit row of this lane's dof (active when lsg != 0)
+  // the floor contacts are the lanes [0, nf) sorted by body; those on the bodies this lane's dof moves are the lanes
+  // [flo, fhi), and fcl = (flo > 0 || fhi == 0) weights the prefix sum below the run (floor_run)
+  int nf, flo, fhi;
+  float fcl;
 };
 
 }  // namespace g1k

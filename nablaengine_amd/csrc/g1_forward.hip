@@ -470,10 +470,41 @@ __device__ __forceinline__ float matvec(const Sim& s, const float* v, int lane_)
 // ============================================================================================== Newton
 struct NewtonOut { int it; bool conv, fresh; };  // fresh: s.L holds H's factor at the final zones
 
+// The floor contacts are the contact lanes [0, nf) sorted by body (the floor pairs come first in pair order, sorted by
+// body, and contacts are compacted in pair order), and the bodies a dof moves are one run of body ids
+// [ctz(dsub), 32 - clz(dsub)) (bodies in depth-first order); both orders are checked at compile time. So the floor
+// contacts on the bodies dof i moves are one lane run [flo, fhi): from the last lane of each contact body's run, the
+// lanes up to the last body below the dof's first body, and up to the last body inside its range.
+__device__ __forceinline__ void floor_run(const Sim& s, Rows& R, int lane) {
+  const bool floorl = lane < s.ncon && R.b1 == 0;
+  const unsigned long long fl = ballot(floorl);
+  const int nf = __popcll(fl);
+  const int bnext = __shfl_down(R.b2, 1, WL);
+  const unsigned long long ends = ballot(floorl && (lane == nf - 1 || bnext != R.b2));
+  const unsigned dm = s.dsub[lane];
+  const int bs = dm ? __builtin_ctz(dm) : NB, be = dm ? 32 - __builtin_clz(dm) : NB;
+  int lo = 0, hi = 0;
+  for (unsigned long long m = ends; m; m &= m - 1ull) {  // one contact body a step, in body order (all lanes)
+    const int e = __builtin_ctzll(m), B = rdli(R.b2, e);
+    lo = B < bs ? e + 1 : lo;
+    hi = B < be ? e + 1 : hi;
+  }
+  R.nf = nf;
+  R.flo = lo;
+  R.fhi = hi;
+  R.fcl = (lo > 0 || hi == 0) ? 1.f : 0.f;
+}
+// the sum of x over the lanes [flo, fhi) of this lane's dof, from x's inclusive prefix sums over the floor lanes:
+// P[fhi - 1] - P[flo - 1], both read by ds_bpermute; P[-1] reads lane 63 and is weighted by 0 (for fhi = 0 both reads
+// are lane 63 and cancel)
+__device__ __forceinline__ float run_sum(float p, const Rows& R) {
+  return fmaf(-lane_of(p, (R.flo - 1) & (WL - 1)), R.fcl, lane_of(p, (R.fhi - 1) & (WL - 1)));
+}
+
 // gradient at the current jar: grad = M a - qfrc_smooth - J' f, f = -D x on the rows with x < 0; returns |grad|
 __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
-  // J' f: the contact's frame force f = -D x (rows with x < 0) as a world force F and its moment T about O, summed per
-  // distinct contact body by masked wave sums (body 2 +, body 1 -); dof i adds S_i . (T, F) of the bodies it moves
+  // J' f: the contact's frame force f = -D x (rows with x < 0) as a world force F and its moment T about O; dof i adds
+  // S_i . (T, F) summed over the contacts on the bodies it moves
   float T[3] = {0.f, 0.f, 0.f}, F[3] = {0.f, 0.f, 0.f};
   bool act = false;
   if (con) {
@@ -491,9 +522,18 @@ __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
   const int il = lane < NV ? lane : 0;
   const float w[3] = {s.S[il][0], s.S[il][1], s.S[il][2]}, v[3] = {s.S[il][4], s.S[il][5], s.S[il][6]};
   float tau = 0.f;
-  for (unsigned m = wor(act ? (1u << R.b1) | (1u << R.b2) : 0u) & ~1u; m; m &= m - 1u) {
+  if (R.nf) {  // floor contacts: the run of the bodies dof i moves (floor_run), from prefix sums over the lanes
+    float x[6] = {T[0], T[1], T[2], F[0], F[1], F[2]};
+    wscan_nw<6>(x, R.nf);
+#pragma unroll
+    for (int e = 0; e < 6; e++) x[e] = run_sum(x[e], R);
+    tau = w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
+  }
+  // contacts between two robot bodies: per distinct body (body 2 +, body 1 -)
+  for (unsigned m = wor(act && R.b1 != 0 ? (1u << R.b1) | (1u << R.b2) : 0u); m; m &= m - 1u) {
     const int B = __builtin_ctz(m);
-    const float sd = (act && R.b2 == B) ? 1.f : ((act && R.b1 == B) ? -1.f : 0.f);
+    const bool self = act && R.b1 != 0;
+    const float sd = (self && R.b2 == B) ? 1.f : ((self && R.b1 == B) ? -1.f : 0.f);
     float x[6] = {sd * T[0], sd * T[1], sd * T[2], sd * F[0], sd * F[1], sd * F[2]};
     wsum_nw<6>(x, s.ncon);  // contact lanes only
     if ((dm >> B) & 1u) tau += w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
@@ -588,29 +628,13 @@ __device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con
   float n[3] = {0.f, 0.f, 0.f}, f[3] = {0.f, 0.f, 0.f};
   float K[21];
   contact_stiffness(R, d, floorc, K);  // exactly 0 off the active floor contacts (Rows are zero past the contacts)
-  const bool floorl = lane < s.ncon && R.b1 == 0;
-  const unsigned long long fl = ballot(floorl);
-  if (fl) {
-    // The floor contacts are the lanes [0, nf) sorted by body, and dof i's subtree is the body range
-    // [ctz(dm), 32 - clz(dm)) (both by the tables' order, checked at compile time), so the floor contacts on the
-    // bodies dof i moves are the lanes [lo, hi): their stiffness sum is P[hi - 1] - P[lo - 1] with P the prefix sums
-    // of K over the lanes. lo and hi come from the last lane of each contact body's run; P[-1] reads lane 63 and is
-    // multiplied by 0 (for hi = 0 both reads are lane 63 and cancel).
-    const int nf = __popcll(fl);
-    wscan_nw<21>(K, nf);
-    const int bnext = __shfl_down(R.b2, 1, WL);
-    const unsigned long long ends = ballot(floorl && (lane == nf - 1 || bnext != R.b2));
-    const int bs = dm ? __builtin_ctz(dm) : NB, be = dm ? 32 - __builtin_clz(dm) : NB;
-    int lo = 0, hi = 0;
-    for (unsigned long long m = ends; m; m &= m - 1ull) {  // one contact body a step, in body order (all lanes)
-      const int e = __builtin_ctzll(m), B = rdli(R.b2, e);
-      lo = B < bs ? e + 1 : lo;
-      hi = B < be ? e + 1 : hi;
-    }
-    const float cl = (lo > 0 || hi == 0) ? 1.f : 0.f;
+  if (R.nf) {
+    // the floor contacts' stiffness sum over the bodies dof i moves: prefix sums P of K over the lanes, then
+    // P[fhi - 1] - P[flo - 1] (floor_run)
+    wscan_nw<21>(K, R.nf);
     float k[21];
 #pragma unroll
-    for (int e = 0; e < 21; e++) k[e] = fmaf(-lane_of(K[e], (lo - 1) & (WL - 1)), cl, lane_of(K[e], (hi - 1) & (WL - 1)));
+    for (int e = 0; e < 21; e++) k[e] = run_sum(K[e], R);
     // n = Kaa w + Kal v, f = Kal' w + Kll v
     n[0] = k[0] * w[0] + k[3] * w[1] + k[4] * w[2] + k[6] * v[0] + k[7] * v[1] + k[8] * v[2];
     n[1] = k[3] * w[0] + k[1] * w[1] + k[5] * w[2] + k[9] * v[0] + k[10] * v[1] + k[11] * v[2];
@@ -942,6 +966,7 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
     R.dim = (w >> 16) & 15u;
     R.mu = ((w >> 20) & 1u) ? s.fric : cPairMu[pair];
   }
+  floor_run(s, R, lane);
   wsync();
   // limit rows (dof order), then the contacts' rows (contact order) up to the row capacity
   R.lsg = 0.f; R.lD = 0.f; R.laref = 0.f; R.ljar = 0.f;
