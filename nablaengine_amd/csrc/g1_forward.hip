@@ -530,10 +530,10 @@ __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
     tau = w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
   }
   // contacts between two robot bodies: per distinct body (body 2 +, body 1 -)
-  for (unsigned m = wor(act && R.b1 != 0 ? (1u << R.b1) | (1u << R.b2) : 0u); m; m &= m - 1u) {
+  const bool selfc = act && R.b1 != 0;
+  for (unsigned m = ballot(selfc) ? wor(selfc ? (1u << R.b1) | (1u << R.b2) : 0u) : 0u; m; m &= m - 1u) {
     const int B = __builtin_ctz(m);
-    const bool self = act && R.b1 != 0;
-    const float sd = (self && R.b2 == B) ? 1.f : ((self && R.b1 == B) ? -1.f : 0.f);
+    const float sd = (selfc && R.b2 == B) ? 1.f : ((selfc && R.b1 == B) ? -1.f : 0.f);
     float x[6] = {sd * T[0], sd * T[1], sd * T[2], sd * F[0], sd * F[1], sd * F[2]};
     wsum_nw<6>(x, s.ncon);  // contact lanes only
     if ((dm >> B) & 1u) tau += w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
@@ -614,7 +614,10 @@ __device__ __forceinline__ void contact_stiffness(const Rows& R, const float* dd
 //   Contacts between two robot bodies: J'CJ = sum over the active pyramid edges t of u_t u_t', u_t = sqrt(D) J' e_t,
 //   u_t[d] = sigma_d S_d . (r x e_t, e_t) with sigma_d = (dof d moves body 2) - (dof d moves body 1); added as
 //   U U' on the matrix cores (fp32 MFMA), SELF_BATCH contacts (4 edges each) a batch.
-__device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con) {
+//   clear: zero s.L first. Not needed when s.L holds a factor with the tree's sparsity (of M or of an earlier H
+//   without contacts between robot bodies): such a factor is exactly 0 off the pattern, and the rows below overwrite
+//   every entry on it.
+__device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con, bool clear) {
   float d[4];
 #pragma unroll
   for (int t = 0; t < 4; t++) d[t] = (con && t < R.nr && R.jar[t] < 0.f) ? R.D : 0.f;
@@ -645,7 +648,8 @@ __device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con
   }
   PROF(PH_HCOMP);
   // rows of H: zero, then M[i][j] + S_j . (n, f) on the ancestor dofs j of i (M's nonzeros are on these chains)
-  for (int e = lane; e < NTRI + 2; e += WL) s.L[e] = 0.f;
+  if (clear)
+    for (int e = lane; e < NTRI + 2; e += WL) s.L[e] = 0.f;
   if (lane < NV) {
     const int bi = lane < 6 ? 1 : lane - 4;
     // the chain of dof i's body: its ancestor dofs (and the root's j <= i). Every load first (S rows, M entries:
@@ -788,7 +792,7 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
     cost = cost0;
   }
   newton_grad(s, R, lane, con);
-  int it = 0;
+  int it = 0, lpat = 0;  // lpat: the pattern of the factor in s.L (the smooth dynamics leave M's, the tree's)
   bool conv = false, zsame = false;
   while (it < iterations) {
     // a compiler barrier: LDS values are loaded where they are used inside the iteration, not hoisted out of the loop
@@ -799,9 +803,10 @@ __device__ __forceinline__ NewtonOut newton(Sim& s, Rows& R, int lane, bool con,
     if (zsame) {  // no row changed its zone in the last step: H, and so its factor in s.L, are unchanged
       p = ltl_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     } else {
-      const int pattern = hessian(s, R, lane, con);
+      const int pattern = hessian(s, R, lane, con, lpat != 0);
       PROF(PH_HESS);
       factor_L(s, lane, pattern);
+      lpat = pattern;
       PROF(PH_FACTOR);
       p = ltl_solve(s.L, lane < NV ? -s.grad[lane] : 0.f, lane);
     }
@@ -1030,7 +1035,7 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   if (lane == 0) s.niter = no.it;
   if (rec) {  // the final zones, and H's factor at them (assembled again when the last step changed a zone)
     if (!no.fresh) {
-      const int pattern = hessian(s, R, lane, con);
+      const int pattern = hessian(s, R, lane, con, true);
       factor_L(s, lane, pattern);
     }
     tape_put(rec + REC_LH, s.L, NTRI, REC_LQ - REC_LH, lane);
