@@ -63,6 +63,30 @@ __device__ __forceinline__ void put(Cand& o, int which, int slot, float dist, co
   for (int k = 0; k < 9; k++) o.fr[which][k] = fr[k];
 }
 
+// broadphase over the 502 pairs (step.py:1789-1826): the narrowphase's first test with a relative slack of 1e-5 (the
+// plane's normal distance against the bounding radius, else the bounding spheres), candidates compacted into cand in
+// pair order; returns their count. Branch-free and unrolled (a clamped pair index, the spare slot cand[NPAIR + 1]
+// for the dropped ones), so every iteration's table loads are issued together.
+__device__ __forceinline__ int broadphase(const float (*gx)[4], const float* fn, unsigned short* cand, int lane) {
+  int ncand = 0;
+#pragma unroll
+  for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {
+    const int pr = lane + WL * k;
+    const unsigned w = cPairW[pr < NPAIR ? pr : NPAIR - 1];
+    const int g1 = w & 255u, g2 = (w >> 8) & 255u;
+    const float dif[3] = {gx[g2][0] - gx[g1][0], gx[g2][1] - gx[g1][1], gx[g2][2] - gx[g1][2]};
+    const unsigned cls = (w >> 21) & 7u;
+    const float r1 = cGrb[g1], r2 = cGrb[g2], rb = r1 + r2;
+    const bool plane = cls == 0u || cls == 4u;
+    const bool keep = pr < NPAIR && (plane ? dot3(dif, fn) <= r2 * (1.f + 1e-5f) + 1e-6f
+                                           : dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f);
+    const unsigned long long bal = ballot(keep);
+    cand[keep ? ncand + prefix_count(bal, lane) : NPAIR + 1] = (unsigned short)pr;
+    ncand += __popcll(bal);
+  }
+  return ncand;
+}
+
 // narrowphase of pair pr (step.py:1042-1143 collide_pair), zero margin
 __device__ void collide_pair(const float (*gx)[4], const float (*gq)[4], int pr, Cand& o) {
   o.has[0] = o.has[1] = false;

@@ -309,28 +309,12 @@ __device__ void collision(Sim& s, int lane) {
     qmul(qb, gq, s.u.col.gq[lane]);
   }
   wsync();
-  // broadphase: the narrowphase's first test with a relative slack of 1e-5, candidates compacted in pair order
-  float fn[3];
+  float fn[3];  // the floor's normal, then the broadphase
   {
     const float q0[4] = {s.u.col.gq[0][0], s.u.col.gq[0][1], s.u.col.gq[0][2], s.u.col.gq[0][3]};
     zaxis(q0, fn);
   }
-  int ncand = 0;
-  for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {  // branch-free: both tests, clamped pair index, sink store
-    const int pr = lane + WL * k;
-    const unsigned w = cPairW[pr < NPAIR ? pr : NPAIR - 1];
-    const int g1 = w & 255u, g2 = (w >> 8) & 255u;
-    const float dif[3] = {s.u.col.gx[g2][0] - s.u.col.gx[g1][0], s.u.col.gx[g2][1] - s.u.col.gx[g1][1],
-                          s.u.col.gx[g2][2] - s.u.col.gx[g1][2]};
-    const unsigned cls = (w >> 21) & 7u;
-    const float r1 = cGrb[g1], r2 = cGrb[g2], rb = r1 + r2;
-    const bool plane = cls == 0u || cls == 4u;
-    const bool keep = pr < NPAIR && (plane ? dot3(dif, fn) <= r2 * (1.f + 1e-5f) + 1e-6f
-                                           : dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f);
-    const unsigned long long bal = ballot(keep);
-    s.u.col.cand[keep ? ncand + prefix_count(bal, lane) : NPAIR + 1] = (unsigned short)pr;  // else the spare slot
-    ncand += __popcll(bal);
-  }
+  const int ncand = broadphase(s.u.col.gx, fn, s.u.col.cand, lane);
   wsync();
   // narrowphase: one candidate per lane; contacts placed by a prefix sum of the per-lane counts (pair order)
   int total = 0;

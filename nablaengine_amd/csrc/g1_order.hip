@@ -28,11 +28,21 @@ constexpr int COST_SELF = 12;
 __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict__ qpos, int* __restrict__ cost) {
   __shared__ float q[40];
   __shared__ float bq[NB][4], bx[NB][4];
+  __shared__ float hl[NB][8];  // each hinge body's local rotation (quat (x) hinge rotation) and offset in its parent
   __shared__ float gx[NGEOM][4], gq[NGEOM][4];
   __shared__ unsigned short cand[NPAIR + 2];
   const int lane = threadIdx.x, w = blockIdx.x;
   if (w >= nw) return;
   if (lane < NQ) q[lane] = qpos[(size_t)w * NQ + lane];
+  wsync();
+  if (lane >= 2 && lane < NB) {  // one hinge rotation per body, then the chain walks use products only
+    float sn, cs;
+    sincosf(0.5f * q[cQadr[lane]], &sn, &cs);
+    const float qb[4] = {cQuat[4 * lane], cQuat[4 * lane + 1], cQuat[4 * lane + 2], cQuat[4 * lane + 3]};
+    const float ha[4] = {cs, sn * cAxis[3 * lane], sn * cAxis[3 * lane + 1], sn * cAxis[3 * lane + 2]};
+    qmul(qb, ha, hl[lane]);
+    for (int c = 0; c < 3; c++) hl[lane][4 + c] = cPos[3 * lane + c];
+  }
   wsync();
   if (lane < NB) {
     float Q[4], X[3];
@@ -42,17 +52,20 @@ __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict
       for (int k = 0; k < 3; k++) X[k] = q[k];
     }
     const int depth = cDepth[lane];
-    for (int l = 1; l < depth; l++) {
-      const int k = cTree.path[lane][l];
-      const float qb[4] = {cQuat[4 * k], cQuat[4 * k + 1], cQuat[4 * k + 2], cQuat[4 * k + 3]};
-      const float pb[3] = {cPos[3 * k], cPos[3 * k + 1], cPos[3 * k + 2]};
-      float t[3], q0[4], sn, cs;
-      qrot(Q, pb, t);
-      for (int c = 0; c < 3; c++) X[c] += t[c];
-      qmul(Q, qb, q0);
-      sincosf(0.5f * q[cQadr[k]], &sn, &cs);
-      const float ha[4] = {cs, sn * cAxis[3 * k], sn * cAxis[3 * k + 1], sn * cAxis[3 * k + 2]};
-      qmul(q0, ha, Q);
+    int pth[MAXDEPTH];  // the path's bodies, all loaded before the walk
+#pragma unroll
+    for (int l = 1; l < MAXDEPTH; l++) pth[l] = cTree.path[lane][l];
+#pragma unroll
+    for (int l = 1; l < MAXDEPTH; l++) {
+      if (l < depth) {
+        const float* h = hl[pth[l]];
+        const float ql[4] = {h[0], h[1], h[2], h[3]}, pb[3] = {h[4], h[5], h[6]};
+        float t[3], q1[4];
+        qrot(Q, pb, t);
+        for (int c = 0; c < 3; c++) X[c] += t[c];
+        qmul(Q, ql, q1);
+        for (int c = 0; c < 4; c++) Q[c] = q1[c];
+      }
     }
     for (int k = 0; k < 4; k++) bq[lane][k] = lane == 0 ? (k == 0 ? 1.f : 0.f) : Q[k];
     for (int k = 0; k < 3; k++) bx[lane][k] = lane == 0 ? 0.f : X[k];
@@ -74,25 +87,7 @@ __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict
     const float q0[4] = {gq[0][0], gq[0][1], gq[0][2], gq[0][3]};
     zaxis(q0, fn);
   }
-  int ncand = 0;
-  for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {
-    const int pr = lane + WL * k;
-    bool keep = false;
-    if (pr < NPAIR) {
-      const unsigned pw = cPairW[pr];
-      const int g1 = pw & 255u, g2 = (pw >> 8) & 255u;
-      const float dif[3] = {gx[g2][0] - gx[g1][0], gx[g2][1] - gx[g1][1], gx[g2][2] - gx[g1][2]};
-      const unsigned cls = (pw >> 21) & 7u;
-      if (cls == 0u || cls == 4u) keep = dot3(dif, fn) <= cGrb[g2] * (1.f + 1e-5f) + 1e-6f;
-      else {
-        const float rb = cGrb[g1] + cGrb[g2];
-        keep = dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f;
-      }
-    }
-    const unsigned long long bal = ballot(keep);
-    if (keep) cand[ncand + prefix_count(bal, lane)] = (unsigned short)pr;
-    ncand += __popcll(bal);
-  }
+  const int ncand = broadphase(gx, fn, cand, lane);
   wsync();
   int c = 0;
   for (int c0 = 0; c0 < ncand; c0 += WL) {
