@@ -592,9 +592,9 @@ __device__ __forceinline__ void contact_stiffness(const Rows& R, const float* dd
 // H = M + J' D J on the rows with x < 0, packed into s.L (lane i writes row i); returns the factorization pattern its
 // contacts between robot bodies need (factor_L: 0 the tree's sparsity, 1 the common self-contact fill, 2 dense).
 //   Floor contacts: J'CJ of a contact on body B is S_i' K S_j on every pair of dofs moving B, with K = Phi' C Phi its
-//   6x6 stiffness about O. The contacts are summed per body by wave reductions (one pass per distinct body, usually
-//   the two feet); dof i accumulates (n, f) = (sum of K over the bodies it moves) S_i, and H[i][j] = S_j . (n, f) on
-//   i's ancestor dofs j (the composite stiffness of i's subtree, as CRBA composites inertia).
+//   6x6 stiffness about O. Dof i takes the sum of K over the floor contacts on the bodies it moves, one lane run
+//   (floor_run) read from the prefix sums of K over the lanes, accumulates (n, f) = (that sum) S_i, and
+//   H[i][j] = S_j . (n, f) on i's ancestor dofs j (the composite stiffness of i's subtree, as CRBA composites inertia).
 //   Contacts between two robot bodies: J'CJ = sum over the active pyramid edges t of u_t u_t', u_t = sqrt(D) J' e_t,
 //   u_t[d] = sigma_d S_d . (r x e_t, e_t) with sigma_d = (dof d moves body 2) - (dof d moves body 1); added as
 //   U U' on the matrix cores (fp32 MFMA), SELF_BATCH contacts (4 edges each) a batch.
