@@ -207,7 +207,12 @@ __device__ __forceinline__ int wscan_excl(int v, int lane) {
   }
   return x - v;
 }
-__device__ __forceinline__ void wsync() { __syncthreads(); }
+// The LDS barrier of a workgroup of one wave (every kernel that calls it has 64 threads): a wave's LDS instructions
+// execute in issue order, so a lane's LDS write is seen by every later LDS read of the wave with no hardware barrier
+// and no wait for the outstanding LDS operations (__syncthreads' workgroup fence drains them). Only the compiler
+// must not move memory accesses across this point. LDS written by the memory unit (global_load_lds) is not ordered
+// this way: its readers wait for it explicitly (s_waitcnt vmcnt).
+__device__ __forceinline__ void wsync() { asm volatile("" ::: "memory"); }
 
 // x with lane L's value replaced by 0 (v_writelane_b32 with the lane an inline constant: one instruction, no compare)
 template <int L>
@@ -382,7 +387,7 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
       float* rowbase = Lp + lane;
 #pragma unroll
       for (int m = NROOT; m < NV; m++) rowbase[tri(m, 0)] = c[m];
-      __syncthreads();
+      wsync();
       const int r = lane & 15, q = lane >> 4;
       mfma4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
