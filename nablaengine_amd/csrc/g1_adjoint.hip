@@ -61,9 +61,6 @@ __device__ __forceinline__ Sv ld_sv(const float* p) {
   for (int k = 0; k < 3; k++) { r.w[k] = p[k]; r.v[k] = p[4 + k]; }
   return r;
 }
-__device__ __forceinline__ void st_sv(float* p, const Sv& x) {
-  for (int k = 0; k < 3; k++) { p[k] = x.w[k]; p[4 + k] = x.v[k]; }
-}
 
 enum { TW_V = 0, TW_L, TW_Y, TW_AW, TW_A2, TW_A1, NTW };  // per-body twists
 enum { FB_F1 = 0, FB_P, FB_X1, FB_F2, FB_P2, FB_EG, FB_OL, FB_OA, FB_OV, NFB };  // per-body force vectors

@@ -56,7 +56,6 @@ constexpr float kScale = (float)(1.0 / (MEANINERTIA * NV));  // Newton's cost / 
 constexpr float kTol = (float)TOLERANCE;
 
 // ------------------------------------------------------------------------------------------------ lane helpers
-__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 // The lane index as a value the compiler cannot see through: lane-dependent addresses and masks computed from it stay
 // where they are used. Without this, loop-invariant code motion hoists them out of the solver's loops (dozens of
 // per-lane addresses and lane masks), and the register allocator spills them to scratch, putting a scratch reload on
