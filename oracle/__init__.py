@@ -24,6 +24,10 @@ Parity status of each function (how it is pinned; the tests that pin it are name
 - ``fd_vjp``, ``step_mt``: against ``fd_jacobian`` / ``step`` (the same arithmetic, batched / threaded).
 - ``substep_hessian``: H^-1 against central differences of a* in an applied generalized force; ``ltl`` against numpy's
   Cholesky of the order-reversed matrix.
+- ``step_f32`` (``g1_oracle_f32.cpp``: the same restatement with float32 storage and mostly float32 arithmetic, a
+  yardstick of the error float32 rounding alone gives a step): the float64 ``step`` and its pins carry over, the text
+  being the same; it equals ``step`` within float32 accuracy where Newton converges, and differs from it by the
+  Hessian's conditioning after one or a few iterations (``tests/test_oracle.py``).
 """
 
 import ctypes
@@ -34,9 +38,11 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle_g1.so")
+LIB_F32 = os.path.join(HERE, "liboracle_g1_f32.so")
 NQ, NV, NU, NB = 36, 35, 29, 31
 
 _lib = None
+_lib32 = None
 
 
 def build():
@@ -107,6 +113,32 @@ def step(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=
                       info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), _p(fl), None if qf is None else _p(qf),
                       None if freeze is None else _p(freeze), int(freeze_mode))
     return (oq, ov, ow, info, fl) if flops else (oq, ov, ow, info)
+
+
+def step_f32(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4):
+    """``step`` evaluated in float32 (the restatement compiled with float storage, g1_oracle_f32.cpp): (qpos' (B, 36),
+    qvel' (B, 35), warm' (B, 35), info (B, 4) int32), the outputs float32. A yardstick of float32 rounding, not the
+    checker of any output by itself."""
+    global _lib32
+    if _lib32 is None:
+        if not os.path.exists(LIB_F32):
+            build()
+        L = ctypes.CDLL(LIB_F32)
+        fp, ip = ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int)
+        L.g1o_step.argtypes = [ctypes.c_int, fp, fp, fp, fp, fp, fp, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                               ctypes.c_float, ctypes.c_int, fp, fp, fp, ip, fp]
+        _lib32 = L
+    f = lambda a, shape: np.ascontiguousarray(np.asarray(a, np.float32).reshape(shape))
+    qpos = f(qpos, (-1, NQ))
+    B = qpos.shape[0]
+    qvel, warm, ctrl, friction, com = f(qvel, (B, NV)), f(warm, (B, NV)), f(ctrl, (B, NU)), f(friction, (B,)), f(com, (B, 3))
+    oq, ov, ow = np.empty((B, NQ), np.float32), np.empty((B, NV), np.float32), np.empty((B, NV), np.float32)
+    info, fl = np.empty((B, 4), np.int32), np.empty(B, np.float32)
+    P = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    _lib32.g1o_step(B, P(qpos), P(qvel), P(warm), P(ctrl), P(friction), P(com), int(iterations), float(tol),
+                    int(ls_max), float(ls_tol), int(nsub), P(oq), P(ov), P(ow),
+                    info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), P(fl))
+    return oq, ov, ow, info
 
 
 def step_mt(threads, qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7,

@@ -362,6 +362,30 @@ def test_ten_iteration_tail_is_the_iteration_cap():
     assert e20.max() < 1e-13
 
 
+def test_float32_yardstick():
+    """oracle.step_f32 (the restatement with float storage) on 256 config-1 states: its outputs are float32 and not
+    the float64 ones; where Newton converges (10 iterations) it equals the float64 step to float32 accuracy (qvel
+    median <= 2e-6, p99 <= 2e-5); after one iteration its qvel is off by more than 10x that, because the first
+    Newton direction solves H p = -g with cond(H) ~ 1e5-1e6 (the contacts' stiffness against M) and only further
+    iterations wash the solve's rounding out. That is the float32 error floor a GPU step at a low iteration cap is
+    held to."""
+    st = synthetic.states(256, config=1, seed=31)
+    d = {k: st[k].astype(np.float64) for k in st}
+    rel = lambda a, b: np.linalg.norm(a - b, axis=1) / np.maximum(np.linalg.norm(b, axis=1), 1e-12)
+    errs = {}
+    for it in (1, 10):
+        q32, v32, w32, i32 = oracle.step_f32(**st, iterations=it)
+        q64, v64, w64, i64 = oracle.step(**d, **dict(oracle.ENGINE, iterations=it))
+        assert v32.dtype == np.float32 and not np.array_equal(v32.astype(np.float64), v64)
+        errs[it] = rel(v32, v64)
+    ev = errs[10]
+    assert np.median(ev) <= 2e-6 and np.percentile(ev, 99) <= 2e-5
+    assert np.median(errs[1]) > 10 * np.median(ev)
+    M, H = oracle.substep_hessian(*(d[k][0] for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")),
+                                  iterations=0)
+    assert np.linalg.cond(H) > 1e4
+
+
 def test_ltl_is_the_reversed_cholesky():
     """oracle.ltl (the leaf-first factor A = L' L) against a textbook routine: with J the order reversal, J A J = C C'
     (numpy's Cholesky), so L = J C' J; on random SPD matrices and on M + h kv of a state."""
