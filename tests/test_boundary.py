@@ -143,3 +143,41 @@ def test_diagnostics_names_and_overflow_warning():
         assert len(w) == 1 and issubclass(w[0].category, RuntimeWarning)
     assert torch_ffi.set_overflow_warnings(True) in (False, True)
     assert torch_ffi.set_overflow_warnings(False) is True
+
+
+def test_c_abi_rejects_bad_arguments_before_any_launch():
+    """The C entries check their arguments on the host and return a hipError_t (hipErrorInvalidValue = 1) or the
+    static entry's capacity error (-2) without touching a device, the reference's convention (jax_ffi.py:198-258: an
+    int return, 0 on success); an empty batch is a successful no-op. Called here without a GPU: none of these paths
+    reaches the HIP runtime."""
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built (python -m nablaengine_amd.build)")
+    lib = ctypes.CDLL(LIB)
+    P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    fwd = [P, I] + [P] * 6 + [I, I] + [P] * 7
+    lib.dk_fwd_forward.argtypes = fwd
+    lib.dk_fwd_forward_ordered.argtypes = fwd
+    lib.dk_fwd_forward_static.argtypes = fwd[:-1]
+    lib.dk_fwd_order.argtypes = [P, I, P, P]
+    adj = [P, I, I] + [P] * 10 + [F, I, I, P]
+    lib.dk_adjoint_work.argtypes = adj
+    lib.dk_adjoint.argtypes = adj[:-1]
+    lib.dk_kv2_n3_adjoint.argtypes = adj[:-3]
+    lib.dk_fwd_kinematics.argtypes = [P, I] + [P] * 8
+    lib.dk_torch_diag_fwd.argtypes = [P, P, I, I, I, P, P]
+    n6 = [None] * 6
+    f = lambda nw, it=10, nsub=4, work=None: lib.dk_fwd_forward(None, nw, *n6, it, nsub, *[None] * 6, work)
+    assert f(0) == 0
+    assert f(-1) == 1 and f(3, nsub=0) == 1 and f(3, nsub=33) == 1 and f(3, it=-1) == 1
+    assert lib.dk_fwd_forward_ordered(None, 3, *n6, 10, 4, *[None] * 7) == 1  # an order needs its work buffer
+    assert lib.dk_fwd_order(None, 3, None, None) == 1 and lib.dk_fwd_order(None, 0, None, None) == 0
+    assert lib.dk_fwd_forward_static(None, 131072 + 1, *n6, 10, 4, *[None] * 6) == -2
+    a = lambda nw, kv=1, n=0, nsub=4, tape=None, ctrl=None: lib.dk_adjoint_work(
+        None, nw, nsub, tape, *[None] * 8, ctrl, 0.2, kv, n, None)
+    assert a(0) == 0
+    assert a(-1) == 1 and a(3, nsub=0) == 1 and a(3, kv=3) == 1 and a(3, n=4) == 1 and a(3, kv=-1) == 1
+    assert a(3, kv=2) == 1  # the soft clamp recomputes the actuator force: ctrl is required
+    assert a(3, tape=0x1004) == 1  # the factors are copied 16 bytes at a time: the tape must be 16-byte aligned
+    assert lib.dk_kv2_n3_adjoint(None, 3, 4, *[None] * 10, 0.2) == 1
+    assert lib.dk_fwd_kinematics(None, -1, *[None] * 8) == 1 and lib.dk_fwd_kinematics(None, 0, *[None] * 8) == 0
+    assert lib.dk_torch_diag_fwd(None, None, 3, 4, 10, None, None) == 1
