@@ -115,19 +115,25 @@ def step(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=
     return (oq, ov, ow, info, fl) if flops else (oq, ov, ow, info)
 
 
-def step_f32(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4):
-    """``step`` evaluated in float32 (the restatement compiled with float storage, g1_oracle_f32.cpp): (qpos' (B, 36),
-    qvel' (B, 35), warm' (B, 35), info (B, 4) int32), the outputs float32. A yardstick of float32 rounding, not the
-    checker of any output by itself."""
+def _f32():
+    """The float32 build of the restatement (liboracle_g1_f32.so), its entries' argument types set."""
     global _lib32
     if _lib32 is None:
         if not os.path.exists(LIB_F32):
             build()
         L = ctypes.CDLL(LIB_F32)
-        fp, ip = ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int)
-        L.g1o_step.argtypes = [ctypes.c_int, fp, fp, fp, fp, fp, fp, ctypes.c_int, ctypes.c_float, ctypes.c_int,
-                               ctypes.c_float, ctypes.c_int, fp, fp, fp, ip, fp]
+        fp, ip, i, f = ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_float
+        L.g1o_step.argtypes = [i, fp, fp, fp, fp, fp, fp, i, f, i, f, i, fp, fp, fp, ip, fp]
+        L.g1o_vjp_ex.argtypes = [i, fp, fp, fp, fp, fp, fp, i, f, i, f, i, fp, fp, i, i, f, f, f, fp, fp, fp]
         _lib32 = L
+    return _lib32
+
+
+def step_f32(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4):
+    """``step`` evaluated in float32 (the restatement compiled with float storage, g1_oracle_f32.cpp): (qpos' (B, 36),
+    qvel' (B, 35), warm' (B, 35), info (B, 4) int32), the outputs float32. A yardstick of float32 rounding, not the
+    checker of any output by itself."""
+    _f32()
     f = lambda a, shape: np.ascontiguousarray(np.asarray(a, np.float32).reshape(shape))
     qpos = f(qpos, (-1, NQ))
     B = qpos.shape[0]
@@ -139,6 +145,24 @@ def step_f32(qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_
                     int(ls_max), float(ls_tol), int(nsub), P(oq), P(ov), P(ow),
                     info.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), P(fl))
     return oq, ov, ow, info
+
+
+def vjp_f32(qpos, qvel, warm, ctrl, friction, com, g_qpos, g_qvel, clamp_kv=1, normal=0, clamp_soft=0.2,
+            iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4, normal_eps=1e-3, parallel_eps=1.2e-3):
+    """``vjp`` evaluated in float32 (g1_oracle_f32.cpp, as ``step_f32``): the float32 rounding yardstick of a
+    gradient, not the checker of any gradient by itself."""
+    _f32()
+    f = lambda a, shape: np.ascontiguousarray(np.asarray(a, np.float32).reshape(shape))
+    qpos = f(qpos, (-1, NQ))
+    B = qpos.shape[0]
+    args = [qpos, f(qvel, (B, NV)), f(warm, (B, NV)), f(ctrl, (B, NU)), f(friction, (B,)), f(com, (B, 3))]
+    gq, gv = f(g_qpos, (B, NQ)), f(g_qvel, (B, NV))
+    oq, ov, ou = np.empty((B, NQ), np.float32), np.empty((B, NV), np.float32), np.empty((B, NU), np.float32)
+    P = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    _lib32.g1o_vjp_ex(B, *map(P, args), int(iterations), float(tol), int(ls_max), float(ls_tol), int(nsub), P(gq),
+                      P(gv), int(clamp_kv), int(normal), float(clamp_soft), float(normal_eps), float(parallel_eps),
+                      P(oq), P(ov), P(ou))
+    return oq, ov, ou
 
 
 def step_mt(threads, qpos, qvel, warm, ctrl, friction, com, iterations=10, tol=1e-8, ls_max=40, ls_tol=1e-7,
