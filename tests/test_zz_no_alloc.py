@@ -63,6 +63,34 @@ def test_static_forward_equals_the_work_buffer_forward(lib):
         assert torch.isfinite(a[1]).all()
 
 
+def test_static_forward_at_capacity(lib):
+    """At DK_STATIC_MAX_WORLDS worlds the static scratch (a permutation and a cost per world) is exactly full: outputs
+    and info bitwise the work-buffer forward's (no tape, no contact output at this size)."""
+    import torch
+    hdr = open(os.path.join(ROOT, "include", "nablaengine_g1.h")).read()
+    B = int(re.search(r"#define DK_STATIC_MAX_WORLDS (\d+)", hdr).group(1))
+    print(f"static forward at capacity: {B} config-1 worlds", flush=True)
+    st = synthetic.states(B, config=1, seed=5)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = [torch.from_numpy(st[k]).cuda() for k in KEYS]
+    res = []
+    for static in (True, False):
+        out = [torch.empty((B, 36), device="cuda"), torch.empty((B, 35), device="cuda"),
+               torch.empty((B, 35), device="cuda"), torch.full((B, 4), -1, dtype=torch.int32, device="cuda")]
+        if static:
+            rc = lib.dk_fwd_forward_static(stream, B, *map(p, args), 10, 4, *map(p, out), None, None)
+        else:
+            work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+            rc = lib.dk_fwd_forward(stream, B, *map(p, args), 10, 4, *map(p, out), None, None, p(work))
+        torch.cuda.synchronize()
+        assert rc == 0
+        res.append(out)
+    for x, y in zip(*res):
+        assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+    assert torch.isfinite(res[0][1]).all() and (res[0][3][:, 0] >= 1).all()
+
+
 def test_static_forward_capacity_error(lib):
     import torch
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
