@@ -47,3 +47,39 @@ def test_slices_are_bitwise_the_whole_batch(ffi, config):
         for name, w, p in zip(names, whole, part):
             assert np.array_equal(w[a:b].view(np.uint32) if w.dtype == np.float32 else w[a:b],
                                   p.view(np.uint32) if p.dtype == np.float32 else p), (config, a, b, name)
+
+
+def test_nonfinite_worlds_leave_the_others_alone(ffi):
+    """Worlds with non-finite inputs (NaN in qvel, inf in ctrl, NaN in the root quaternion, NaN friction) run their
+    bounded loops to the end like any other (the Newton iteration cap, the line search's 40 evaluations, contact
+    counts from comparisons): every other world's outputs, tape and gradients are bitwise those of the clean batch.
+    The NaN state's worlds come out non-finite and the backward flags their gradients in its info (bits << 16); an
+    infinite ctrl is a saturated actuator (its force clamped to the limit, the clamp bit set in every record) and
+    the world stays finite."""
+    import torch
+    B = 257
+    st = synthetic.states(B, config=1, seed=79)
+    cq, cv = synthetic.cotangents(B, seed=80)
+    x, tcq, tcv = _cat(st, cq, cv)
+    clean = _run(ffi, x, tcq, tcv)
+    bad = {3: ("qvel", 0), 100: ("ctrl", 5), 200: ("qpos", 4), 256: ("friction", None)}
+    y = [t.clone() for t in x]
+    keys = ("qpos", "qvel", "warm", "ctrl", "friction", "com")
+    for w, (k, j) in bad.items():
+        t = y[keys.index(k)]
+        if j is None:
+            t[w] = np.nan
+        else:
+            t[w, j] = np.inf if k == "ctrl" else np.nan
+    dirty = _run(ffi, y, tcq, tcv)
+    keep = np.setdiff1d(np.arange(B), list(bad))
+    names = ("qpos'", "qvel'", "warm'", "info", "tape", "g_qpos", "g_qvel", "g_ctrl", "backward info")
+    for name, a, b in zip(names, clean, dirty):
+        view = (lambda z: z[keep].view(np.uint32)) if a.dtype == np.float32 else (lambda z: z[keep])
+        assert np.array_equal(view(a), view(b)), name
+    for w in (3, 200):
+        assert not np.isfinite(dirty[1][w]).all(), w
+        assert (dirty[8][w] >> 16) & 7, w  # the backward's non-finite gradient bits (qpos 1, qvel 2, ctrl 4)
+    assert np.isfinite(dirty[0][100]).all() and np.isfinite(dirty[1][100]).all()
+    clamp = dirty[4][100].reshape(4, -1)[:, 2].view(np.uint32)  # each record's clamp mask (bit: dof)
+    assert ((clamp >> (6 + 5)) & 1).all()
