@@ -42,11 +42,17 @@ __global__ __launch_bounds__(256) void k_diag_fwd(unsigned long long* d, int nw,
     orow += (f & 16) != 0;
     lim += info[4 * w] >= iterations;
     if (tape)
-      for (int k = 0; k < nsub; k++) {
-        const unsigned fl = __float_as_uint(tape[((size_t)w * nsub + k) * REC_WORDS + REC_FLAGS]);
-        refact += (fl & FLAG_REFACT) != 0;
-        nonconv += (fl & FLAG_NONCONV) != 0;
-        sing += (fl & FLAG_SINGULAR) != 0;
+      for (int k0 = 0; k0 < nsub; k0 += 4) {  // 4 records' flags in flight at a time
+        unsigned fl[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+          fl[u] = k0 + u < nsub ? __float_as_uint(tape[((size_t)w * nsub + k0 + u) * REC_WORDS + REC_FLAGS]) : 0u;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          refact += (fl[u] & FLAG_REFACT) != 0;
+          nonconv += (fl[u] & FLAG_NONCONV) != 0;
+          sing += (fl[u] & FLAG_SINGULAR) != 0;
+        }
       }
   }
   diag_add(d, D_FWD_UNSUPPORTED, unsup);

@@ -113,29 +113,57 @@ __global__ __launch_bounds__(256) void k_cost_adj(int nw, int nsub, const float*
   const int w = blockIdx.x * blockDim.x + threadIdx.x;
   if (w >= nw) return;
   int c = 0;
-  for (int k = 0; k < nsub; k++) {
-    const unsigned h = __float_as_uint(tape[((size_t)w * nsub + k) * REC_WORDS + REC_HDR]);
-    c += (int)((h >> 8) & 255u);
+  for (int k0 = 0; k0 < nsub; k0 += 4) {  // 4 headers' loads in flight at a time
+    unsigned h[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      h[u] = k0 + u < nsub ? __float_as_uint(tape[((size_t)w * nsub + k0 + u) * REC_WORDS + REC_HDR]) : 0u;
+#pragma unroll
+    for (int u = 0; u < 4; u++) c += (int)((h[u] >> 8) & 255u);
   }
   c >>= 3;
   cost[w] = c < NBKT ? c : NBKT - 1;
 }
 
-// one workgroup: histogram of the costs, descending prefix, scatter (perm[slot] = world, heaviest first)
-__global__ __launch_bounds__(1024) void k_order(int nw, const int* __restrict__ cost, int* __restrict__ perm) {
+// one workgroup of ORDER_THREADS: histogram of the costs, descending prefix, scatter (perm[slot] = world, heaviest
+// first). Each thread takes its worlds ORDER_LOADS at a time, every load issued before the first is used (one memory
+// round trip per batch, not per world).
+constexpr int ORDER_THREADS = 1024, ORDER_LOADS = 8;
+__global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __restrict__ cost, int* __restrict__ perm) {
   __shared__ int cnt[NBKT], cur[NBKT];
   const int t = threadIdx.x;
-  for (int b = t; b < NBKT; b += blockDim.x) cnt[b] = 0;
+  if (t < NBKT) cnt[t] = 0;
   __syncthreads();
-  for (int w = t; w < nw; w += blockDim.x) atomicAdd(&cnt[cost[w]], 1);
+  for (int w0 = t; w0 < nw; w0 += ORDER_LOADS * ORDER_THREADS) {
+    int c[ORDER_LOADS];
+#pragma unroll
+    for (int u = 0; u < ORDER_LOADS; u++) {
+      const int w = w0 + u * ORDER_THREADS;
+      c[u] = w < nw ? cost[w] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < ORDER_LOADS; u++)
+      if (c[u] >= 0) atomicAdd(&cnt[c[u]], 1);
+  }
   __syncthreads();
   if (t == 0) {
     int acc = 0;
     for (int b = NBKT - 1; b >= 0; b--) { cur[b] = acc; acc += cnt[b]; }
   }
   __syncthreads();
-  for (int w = t; w < nw; w += blockDim.x) perm[atomicAdd(&cur[cost[w]], 1)] = w;
+  for (int w0 = t; w0 < nw; w0 += ORDER_LOADS * ORDER_THREADS) {
+    int c[ORDER_LOADS];
+#pragma unroll
+    for (int u = 0; u < ORDER_LOADS; u++) {
+      const int w = w0 + u * ORDER_THREADS;
+      c[u] = w < nw ? cost[w] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < ORDER_LOADS; u++)
+      if (c[u] >= 0) perm[atomicAdd(&cur[c[u]], 1)] = w0 + u * ORDER_THREADS;
+  }
 }
+static_assert(NBKT <= ORDER_THREADS, "one thread clears each bucket");
 
 // work buffer: perm (nw int32), cost (nw int32)
 size_t order_work_bytes(int nw) { return nw > 0 ? ((8 * (size_t)nw + 255) & ~(size_t)255) : 0; }
@@ -144,7 +172,7 @@ int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work) {
   int* perm = (int*)work;
   int* cost = perm + nw;
   hipLaunchKernelGGL(k_cost_fwd, dim3(nw), dim3(64), 0, st, nw, qpos, cost);
-  hipLaunchKernelGGL(k_order, dim3(1), dim3(1024), 0, st, nw, cost, perm);
+  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, cost, perm);
   return (int)hipGetLastError();
 }
 
@@ -152,7 +180,7 @@ int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* 
   int* perm = (int*)work;
   int* cost = perm + nw;
   hipLaunchKernelGGL(k_cost_adj, dim3((nw + 255) / 256), dim3(256), 0, st, nw, nsub, tape, cost);
-  hipLaunchKernelGGL(k_order, dim3(1), dim3(1024), 0, st, nw, cost, perm);
+  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, cost, perm);
   return (int)hipGetLastError();
 }
 
