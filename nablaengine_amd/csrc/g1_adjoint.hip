@@ -104,7 +104,10 @@ static_assert(offsetof(Adj, lt) % 16 == 0 && 3 * 256 <= 768 && NTRI <= 3 * 256, 
 
 // L_Q and L_H of a record copied into LDS by the memory unit (global_load_lds_dwordx4: lane l's 16 bytes land 16 l
 // bytes past the instruction's LDS base), 3 x 1024 bytes each; lanes past the factor's end load its start again into
-// the slack. Issued before the record's other loads, they arrive with them; no registers hold them.
+// the slack. Issued with the record's other loads, they arrive with them; no registers hold them. (The compiler waits
+// for these copies at the next LDS access, as it cannot tell their LDS writes apart; and any later global load's
+// wait covers them too, vmcnt counting in issue order, so they cannot be left in flight across the poses, whose
+// per-body constants are global loads.)
 __device__ __forceinline__ void load_factors(Adj& s, const float* __restrict__ rec, int lane) {
 #pragma unroll
   for (int c = 0; c < 3; c++) {
@@ -386,27 +389,33 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
 // ---------------------------------------------------------------------------------------------- one substep
 __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int clamp_kv, int normal,
                             float clamp_soft) {
-  // the record (the factors first, into LDS directly)
+  // the record: every field's load issued at once, on every lane (a lane past a field reads a word inside it and
+  // drops it; a field loaded under its own lane test waited for each load in turn), with the factors' copies into LDS
+  // (load_factors): one memory round trip
+  const int lq = min(lane, NQ - 1), lv = min(lane, NV - 1);
+  const float rq = rec[REC_QPOS + lq], rv = rec[REC_QVEL + lv], ra = rec[REC_ASTAR + lv], rd = rec[REC_AADV + lv];
+  const unsigned rc = __float_as_uint(rec[REC_CLAMP + (lane & 1)]), rz = __float_as_uint(rec[REC_LIMZONE + (lane & 1)]);
+  const unsigned rr = __float_as_uint(rec[REC_LIMROW + (lane & 1)]), rcz = __float_as_uint(rec[REC_CZONE + (lane & 7)]);
+  const unsigned rcon = __float_as_uint(rec[REC_CON + (lane & (MAXCON / 2 - 1))]), hdr = __float_as_uint(rec[REC_HDR]);
   load_factors(s, rec, lane);
-  if (lane < NQ) s.qpos[lane] = rec[REC_QPOS + lane];
+  if (lane < NQ) s.qpos[lane] = rq;
   if (lane < NV) {
-    s.qvel[lane] = rec[REC_QVEL + lane];
-    s.astar[lane] = rec[REC_ASTAR + lane];
-    s.aadv[lane] = rec[REC_AADV + lane];
-    s.at[lane] = s.astar[lane] - s.aadv[lane];
+    s.qvel[lane] = rv;
+    s.astar[lane] = ra;
+    s.aadv[lane] = rd;
+    s.at[lane] = ra - rd;
   }
   if (lane < 2) {
-    s.clampm[lane] = __float_as_uint(rec[REC_CLAMP + lane]);
-    s.limzone[lane] = __float_as_uint(rec[REC_LIMZONE + lane]);
-    s.limrow[lane] = __float_as_uint(rec[REC_LIMROW + lane]);
+    s.clampm[lane] = rc;
+    s.limzone[lane] = rz;
+    s.limrow[lane] = rr;
   }
-  if (lane < 8) s.czone[lane] = __float_as_uint(rec[REC_CZONE + lane]);
+  if (lane < 8) s.czone[lane] = rcz;
   if (lane < MAXCON / 2) {
-    const unsigned e = __float_as_uint(rec[REC_CON + lane]);
-    s.con[2 * lane] = (unsigned short)(e & 0xFFFFu);
-    s.con[2 * lane + 1] = (unsigned short)(e >> 16);
+    s.con[2 * lane] = (unsigned short)(rcon & 0xFFFFu);
+    s.con[2 * lane + 1] = (unsigned short)(rcon >> 16);
   }
-  if (lane == 0) s.ncon = min((int)(__float_as_uint(rec[REC_HDR]) & 255u), MAXCON);
+  if (lane == 0) s.ncon = min((int)(hdr & 255u), MAXCON);
   wsync();
   APROF(AP_RECORD);
   // poses: each hinge body's local transform (lane = body), then each body lane walks its chain (the chain table)
