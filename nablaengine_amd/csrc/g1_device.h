@@ -48,6 +48,22 @@ __constant__ inline Arr<int, NGEOM> cGbody = to_int(GEOM_BODY);
 __constant__ inline Arr<unsigned, NPAIR> cPairW = PAIRW;
 __constant__ inline Arr<float, NPAIR> cPairMu = to_float(PAIR_MU);
 __constant__ inline Tree cTree = TREE;
+// each body's chain (the dofs moving it, ascending) packed one byte a dof into 4 words, 255 past its end (a 16-byte row
+// per body: one load each)
+struct __align__(16) ChainWords { unsigned w[NB][MAXCHAIN / 4]; };
+constexpr ChainWords make_chain_words() {
+  ChainWords c{};
+  for (int b = 0; b < NB; b++)
+    for (int k = 0; k < MAXCHAIN / 4; k++) {
+      unsigned wd = 0u;
+      for (int e = 0; e < 4; e++)
+        wd |= (4 * k + e < TREE.nchain[b] ? (unsigned)TREE.chain[b][4 * k + e] : 255u) << (8 * e);
+      c.w[b][k] = wd;
+    }
+  return c;
+}
+__constant__ inline ChainWords cChainW = make_chain_words();
+static_assert(MAXCHAIN == 16, "a chain row is one 16-byte load");
 
 constexpr float kH = (float)TIMESTEP;
 constexpr float kGrav[3] = {(float)GRAVITY[0], (float)GRAVITY[1], (float)GRAVITY[2]};
@@ -252,13 +268,12 @@ __device__ __forceinline__ int chain_dof(const unsigned* ch, int t, bool* on) {
   return d != 255u ? (int)d : 0;
 }
 __device__ __forceinline__ void chain_table(unsigned (*chain)[MAXCHAIN / 4], int lane) {
+  const uint4 v = reinterpret_cast<const uint4*>(cChainW.w)[lane < NB ? lane : 0];  // every lane's load in bounds
   if (lane < NB) {
-    const int n = cTree.nchain[lane];
-    for (int k = 0; k < MAXCHAIN / 4; k++) {
-      unsigned wd = 0u;
-      for (int e = 0; e < 4; e++) wd |= (4 * k + e < n ? (unsigned)cTree.chain[lane][4 * k + e] : 255u) << (8 * e);
-      chain[lane][k] = wd;
-    }
+    chain[lane][0] = v.x;
+    chain[lane][1] = v.y;
+    chain[lane][2] = v.z;
+    chain[lane][3] = v.w;
   }
 }
 

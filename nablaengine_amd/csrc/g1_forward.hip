@@ -1108,11 +1108,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int lane = threadIdx.x;
   if ((int)blockIdx.x >= nw) return;
   const int w = perm ? perm[blockIdx.x] : (int)blockIdx.x;  // heaviest worlds first (g1_order.hip)
-  if (lane < NQ) s.qpos[lane] = qpos[(size_t)w * NQ + lane];
-  if (lane < NV) { s.qvel[lane] = qvel[(size_t)w * NV + lane]; s.qacc[lane] = warm[(size_t)w * NV + lane]; }
-  if (lane < NU) s.ctrl[lane] = ctrl[(size_t)w * NU + lane];
-  if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
-  if (lane == 0) { s.fric = fric[w]; s.flags = 0; s.niter = 0; }
+  // the world's inputs: every load issued at once, on every lane (a lane past a row reads a word inside it and drops
+  // it), one memory round trip
+  const int lq = min(lane, NQ - 1), lv = min(lane, NV - 1), lu = min(lane, NU - 1), lc = min(lane, 2);
+  const float iq = qpos[(size_t)w * NQ + lq], iv = qvel[(size_t)w * NV + lv], iw = warm[(size_t)w * NV + lv];
+  const float iu = ctrl[(size_t)w * NU + lu], ic = com[(size_t)w * 3 + lc], ifr = fric[w];
+  if (lane < NQ) s.qpos[lane] = iq;
+  if (lane < NV) { s.qvel[lane] = iv; s.qacc[lane] = iw; }
+  if (lane < NU) s.ctrl[lane] = iu;
+  if (lane < 3) s.com[lane] = ic;
+  if (lane == 0) { s.fric = ifr; s.flags = 0; s.niter = 0; }
   s.dsub[lane] = lane < NV ? cTree.dofmask32[lane] : 0u;
   chain_table(s.chain, lane);
   if (lane < 8) s.S[NV][lane] = 0.f;  // body_vel's zero padding row and entries
