@@ -397,6 +397,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   const unsigned rc = __float_as_uint(rec[REC_CLAMP + (lane & 1)]), rz = __float_as_uint(rec[REC_LIMZONE + (lane & 1)]);
   const unsigned rr = __float_as_uint(rec[REC_LIMROW + (lane & 1)]), rcz = __float_as_uint(rec[REC_CZONE + (lane & 7)]);
   const unsigned rcon = __float_as_uint(rec[REC_CON + (lane & (MAXCON / 2 - 1))]), hdr = __float_as_uint(rec[REC_HDR]);
+  const unsigned rfl = __float_as_uint(rec[REC_FLAGS]);  // the records' flags, summed into the backward's info
   load_factors(s, rec, lane);
   if (lane < NQ) s.qpos[lane] = rq;
   if (lane < NV) {
@@ -415,7 +416,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     s.con[2 * lane] = (unsigned short)(rcon & 0xFFFFu);
     s.con[2 * lane + 1] = (unsigned short)(rcon >> 16);
   }
-  if (lane == 0) s.ncon = min((int)(hdr & 255u), MAXCON);
+  if (lane == 0) { s.ncon = min((int)(hdr & 255u), MAXCON); s.flags |= (int)rfl; }
   wsync();
   APROF(AP_RECORD);
   // poses: each hinge body's local transform (lane = body), then each body lane walks its chain (the chain table)
@@ -879,9 +880,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if ((int)blockIdx.x >= nw) return;
   const int w = perm ? perm[blockIdx.x] : (int)blockIdx.x;  // heaviest worlds first (g1_order.hip)
   const float* wt = tape + (size_t)w * nsub * REC_WORDS;
-  if (lane < 3) s.com[lane] = com[(size_t)w * 3 + lane];
-  if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = ctrl ? ctrl[(size_t)w * NU + lane] : 0.f; }
-  if (lane == 0) { s.fric = fric[w]; s.flags = 0; }
+  // the world's inputs: every load issued at once, on every lane (a lane past a row reads a word inside it and drops
+  // it), one memory round trip
+  const int lc = min(lane, 2), lu = min(lane, NU - 1), lv = min(lane, NV - 1);
+  const int lqo = min(lane < 3 ? lane : lane + 1, NQ - 1);  // qpos-form entry of tangent dof lane (< 3 or >= 6)
+  const float ic = com[(size_t)w * 3 + lc], iu = ctrl ? ctrl[(size_t)w * NU + lu] : 0.f, ifr = fric[w];
+  const float igv = gv_out[(size_t)w * NV + lv], igq = gq_out[(size_t)w * NQ + lqo];
+  if (lane < 3) s.com[lane] = ic;
+  if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = iu; }
+  if (lane == 0) { s.fric = ifr; s.flags = 0; }
 #ifdef G1_PROFILE
   if (lane < NPHASE) s.prof_acc[lane] = 0;
   if (lane == 0) {
@@ -894,8 +901,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
   // the output cotangents in the tangent space at the output state (its root quaternion: the last substep's
   // integration replayed from the record)
-  if (lane < NV) s.vb[lane] = gv_out[(size_t)w * NV + lane];
-  if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = gq_out[(size_t)w * NQ + (lane < 3 ? lane : lane + 1)];
+  if (lane < NV) s.vb[lane] = igv;
+  if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = igq;
   if (lane == 0) {
     const float* rec = wt + (size_t)(nsub - 1) * REC_WORDS;
     float wv[3], q[4];
@@ -920,10 +927,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
   }
   wsync();
-  for (int k = nsub - 1; k >= 0; k--) {
-    if (lane == 0) s.flags |= (int)__float_as_uint(wt[(size_t)k * REC_WORDS + REC_FLAGS]);  // the records' flags
-    adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
-  }
+  for (int k = nsub - 1; k >= 0; k--) adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
   // gradients: qpos form (the quaternion's 2 q (x) (0, t)), qvel, ctrl
   float* oq = gq_in + (size_t)w * NQ;
   if (lane < 3) oq[lane] = s.qb[lane];
