@@ -6,8 +6,9 @@
 //   records' flags), 8 bwd_calls, 9 bwd_rows, 10 nonfinite_rows (a non-finite gradient), 11-13 nonfinite_{qpos,qvel,
 //   ctrl}_rows, 14 nonfinite_cotangent_rows, 15 replay_mismatch_worlds, 16 fwd_contact_overflow_worlds,
 //   17 fwd_row_overflow_worlds.
-// The backward also writes the non-finite bits (1 qpos, 2 qvel, 4 ctrl, 8 cotangent) << 16 into its info. One thread per
-// world (grid-stride), a wave sum per count, one 64-bit atomic add per wave and count; integer counts only.
+// The backward also writes the non-finite bits (1 qpos, 2 qvel, 4 ctrl, 8 cotangent) << 16 into its info. The forward's
+// counters: one thread per world (grid-stride); the backward's: one wave per world; a wave sum per count, one 64-bit
+// atomic add per wave and count; integer counts only.
 #include "g1_device.h"
 #include "g1_tape.h"
 
@@ -69,23 +70,33 @@ __global__ __launch_bounds__(256) void k_diag_fwd(unsigned long long* d, int nw,
   }
 }
 
+// one wave per world (4 worlds per workgroup of 256): lane l reads entry l of each row (the rows' loads coalesced, all
+// issued at once), the wave's ballots give the row's non-finite bits
 __global__ __launch_bounds__(256) void k_diag_bwd(unsigned long long* d, int nw, const float* __restrict__ gq,
                                                   const float* __restrict__ gv, const float* __restrict__ gu,
                                                   const float* __restrict__ cq, const float* __restrict__ cv,
                                                   int* __restrict__ info) {
+  static_assert(NQ <= 64 && NV <= 64 && NU <= 64, "one row per wave");
+  const int lane = threadIdx.x & 63, w = blockIdx.x * 4 + (threadIdx.x >> 6);
   int rows = 0, rq = 0, rv = 0, ru = 0, rc = 0, rm = 0;
-  for (int w = blockIdx.x * blockDim.x + threadIdx.x; w < nw; w += gridDim.x * blockDim.x) {
-    const unsigned b = (all_finite(gq + (size_t)w * NQ, NQ) ? 0u : 1u) | (all_finite(gv + (size_t)w * NV, NV) ? 0u : 2u)
-                       | (all_finite(gu + (size_t)w * NU, NU) ? 0u : 4u)
-                       | (all_finite(cq + (size_t)w * NQ, NQ) && all_finite(cv + (size_t)w * NV, NV) ? 0u : 8u);
-    const int f = info[w];
-    info[w] = f | (int)(b << NONFINITE_SHIFT);
-    rows += (b & 7u) != 0;
-    rq += (b & 1u) != 0;
-    rv += (b & 2u) != 0;
-    ru += (b & 4u) != 0;
-    rc += (b & 8u) != 0;
-    rm += (f & ADJ_REPLAY_MISMATCH) != 0;
+  if (w < nw) {  // wave-uniform
+    const int lq = min(lane, NQ - 1), lv = min(lane, NV - 1), lu = min(lane, NU - 1);
+    const float xq = gq[(size_t)w * NQ + lq], xv = gv[(size_t)w * NV + lv], xu = gu[(size_t)w * NU + lu];
+    const float yq = cq[(size_t)w * NQ + lq], yv = cv[(size_t)w * NV + lv];
+    const bool bq = __ballot(!__builtin_isfinite(xq)) != 0ull, bv = __ballot(!__builtin_isfinite(xv)) != 0ull;
+    const bool bu = __ballot(!__builtin_isfinite(xu)) != 0ull;
+    const bool bc = __ballot(!(__builtin_isfinite(yq) && __builtin_isfinite(yv))) != 0ull;
+    const unsigned b = (bq ? 1u : 0u) | (bv ? 2u : 0u) | (bu ? 4u : 0u) | (bc ? 8u : 0u);
+    if (lane == 0) {
+      const int f = info[w];
+      info[w] = f | (int)(b << NONFINITE_SHIFT);
+      rows = (b & 7u) != 0;
+      rq = (b & 1u) != 0;
+      rv = (b & 2u) != 0;
+      ru = (b & 4u) != 0;
+      rc = (b & 8u) != 0;
+      rm = (f & ADJ_REPLAY_MISMATCH) != 0;
+    }
   }
   diag_add(d, D_NONFINITE, rows);
   diag_add(d, D_NONFINITE_QPOS, rq);
@@ -112,7 +123,7 @@ int launch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, int
 
 int launch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float* gq, const float* gv, const float* gu,
                     const float* cq, const float* cv, int* info) {
-  hipLaunchKernelGGL(k_diag_bwd, dim3(diag_grid(nw)), dim3(256), 0, st, d, nw, gq, gv, gu, cq, cv, info);
+  hipLaunchKernelGGL(k_diag_bwd, dim3(nw > 0 ? (nw + 3) / 4 : 1), dim3(256), 0, st, d, nw, gq, gv, gu, cq, cv, info);
   return (int)hipGetLastError();
 }
 
