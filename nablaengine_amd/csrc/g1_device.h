@@ -416,7 +416,9 @@ __device__ __forceinline__ void ltl_factor(float* Lp, int lane_) {
       const float d4 = __shfl(acc[0], lane + 16, 64), d5 = __shfl(acc[1], lane + 16, 64);
       c[0] -= acc[0]; c[1] -= acc[1]; c[2] -= acc[2]; c[3] -= acc[3]; c[4] -= d4; c[5] -= d5;
     }
-    const float d = fmaxf(rdl(c[k], k), 1e-30f);
+    // the pivot, floored at 1e-30 on the lanes before the broadcast: one v_max on a vector register (a max of the
+    // broadcast scalar would first canonicalize it, a second instruction on the pivot's dependency chain)
+    const float d = rdl(fmaxf(c[k], 1e-30f), k);
     // L[k][j] = A[k][j] / sqrt(d) on lane j; on lane k itself d / sqrt(d) = L[k][k] (the hardware 1/sqrt, 1 ulp)
     c[k] *= __builtin_amdgcn_rsqf(d);
     // every broadcast of the step first, then the updates: a v_readlane's SGPR is not read by the next instruction;
