@@ -67,6 +67,18 @@ int dk_torch_diag_fwd(hipStream_t st, unsigned long long* d, int nw, int nsub, i
                       const float* tape);
 int dk_torch_diag_bwd(hipStream_t st, unsigned long long* d, int nw, const float* gq, const float* gv, const float* gu,
                       const float* cq, const float* cv, int* info);
+/* No counterpart in the reference (its torch_ffi launches the diagnostics kernel after each call): dk_fwd_forward /
+ * dk_adjoint_work with dk_torch_diag_fwd / dk_torch_diag_bwd's counting done by the forward / adjoint kernel itself,
+ * each world adding its part at its end (one launch fewer per call). The same outputs, the same counters in d (d is
+ * required), and for the adjoint the same non-finite bits << 16 in info (the output cotangents gq_out, gv_out are the
+ * rows dk_torch_diag_bwd's cq, cv check). */
+int dk_fwd_forward_diag(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm,
+                        const float* ctrl, const float* fric, const float* com, int iterations, int nsub, float* oq,
+                        float* ov, float* ow, int* info, float* ocon, float* tape, void* work, unsigned long long* d);
+int dk_adjoint_work_diag(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                         const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                         const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work,
+                         unsigned long long* d);
 /* Replaces <unit>_upload (jax_ffi.py:214-225): the model constants are compiled into this library, so the call only
  * checks that the current device can run the kernels; consts may be NULL. */
 int dk_fwd_upload(const float* consts, hipStream_t st);

@@ -13,6 +13,7 @@
 // Determinism: every sum has a fixed order (lane = body sums over contacts in contact order; lane = dof sums over
 // bodies in body order); no atomics.
 #include "g1_collide.h"
+#include "g1_diag.h"
 #include "g1_tape.h"
 
 namespace g1k {
@@ -874,7 +875,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                                                 float* __restrict__ gq_in, float* __restrict__ gv_in,
                                                 float* __restrict__ gctrl, int* __restrict__ info,
                                                 const float* __restrict__ ctrl, float clamp_soft, int clamp_kv,
-                                                int normal, const int* __restrict__ perm) {
+                                                int normal, const int* __restrict__ perm,
+                                                unsigned long long* __restrict__ diag) {
   __shared__ Adj s;
   const int lane = threadIdx.x;
   if ((int)blockIdx.x >= nw) return;
@@ -888,7 +890,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const float igv = gv_out[(size_t)w * NV + lv], igq = gq_out[(size_t)w * NQ + lqo];
   if (lane < 3) s.com[lane] = ic;
   if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = iu; }
-  if (lane == 0) { s.fric = ifr; s.flags = 0; }
+  bool cbad = false;  // with the counters: a non-finite entry in the output cotangents (every entry of both rows)
+  if (diag) {
+    const float icq = gq_out[(size_t)w * NQ + min(lane, NQ - 1)];
+    cbad = ballot(!(__builtin_isfinite(icq) && __builtin_isfinite(igv))) != 0ull;
+  }
+  if (lane == 0) { s.fric = ifr; s.flags = cbad ? NONFINITE_COT << NONFINITE_SHIFT : 0; }
 #ifdef G1_PROFILE
   if (lane < NPHASE) s.prof_acc[lane] = 0;
   if (lane == 0) {
@@ -930,19 +937,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   for (int k = nsub - 1; k >= 0; k--) adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
   // gradients: qpos form (the quaternion's 2 q (x) (0, t)), qvel, ctrl
   float* oq = gq_in + (size_t)w * NQ;
-  if (lane < 3) oq[lane] = s.qb[lane];
-  if (lane >= 6 && lane < NV) oq[lane + 1] = s.qb[lane];
+  bool nq = false;  // a non-finite entry among those this lane writes
+  if (lane < 3 || (lane >= 6 && lane < NV)) {
+    oq[lane < 3 ? lane : lane + 1] = s.qb[lane];
+    nq = !__builtin_isfinite(s.qb[lane]);
+  }
   if (lane == 0) {
     const float* q0 = wt + REC_QPOS + 3;
     const float n = rsqrtf(q0[0] * q0[0] + q0[1] * q0[1] + q0[2] * q0[2] + q0[3] * q0[3]);
     const float qq[4] = {q0[0] * n, q0[1] * n, q0[2] * n, q0[3] * n}, t[4] = {0.f, s.qb[3], s.qb[4], s.qb[5]};
     float r[4];
     qmul(qq, t, r);
-    for (int k = 0; k < 4; k++) oq[3 + k] = 2.f * r[k];
+    for (int k = 0; k < 4; k++) {
+      const float o = 2.f * r[k];
+      oq[3 + k] = o;
+      nq |= !__builtin_isfinite(o);
+    }
   }
-  if (lane < NV) gv_in[(size_t)w * NV + lane] = s.vb[lane];
-  if (lane < NU) gctrl[(size_t)w * NU + lane] = s.ub[lane];
-  if (lane == 0) info[w] = s.flags;
+  const float xv = s.vb[min(lane, NV - 1)], xu = s.ub[min(lane, NU - 1)];
+  if (lane < NV) gv_in[(size_t)w * NV + lane] = xv;
+  if (lane < NU) gctrl[(size_t)w * NU + lane] = xu;
+  int nb = 0;  // with the counters: the non-finite bits of the gradients (k_diag_bwd's, from the values written)
+  if (diag)
+    nb = (ballot(nq) ? NONFINITE_QPOS : 0) | (ballot(!__builtin_isfinite(xv)) ? NONFINITE_QVEL : 0)
+         | (ballot(!__builtin_isfinite(xu)) ? NONFINITE_CTRL : 0);
+  if (lane == 0) {
+    const int f = s.flags | nb << NONFINITE_SHIFT;
+    info[w] = f;
+    if (diag) {  // this world's part of the counters
+      const int b = f >> NONFINITE_SHIFT;
+      if (b & 7) atomicAdd(&diag[D_NONFINITE], 1ull);
+      if (b & NONFINITE_QPOS) atomicAdd(&diag[D_NONFINITE_QPOS], 1ull);
+      if (b & NONFINITE_QVEL) atomicAdd(&diag[D_NONFINITE_QVEL], 1ull);
+      if (b & NONFINITE_CTRL) atomicAdd(&diag[D_NONFINITE_CTRL], 1ull);
+      if (b & NONFINITE_COT) atomicAdd(&diag[D_NONFINITE_COT], 1ull);
+      if (f & ADJ_REPLAY_MISMATCH) atomicAdd(&diag[D_REPLAY_MISMATCH], 1ull);
+      if (blockIdx.x == 0) {
+        atomicAdd(&diag[D_BWD_CALLS], 1ull);
+        atomicAdd(&diag[D_BWD_ROWS], (unsigned long long)nw);
+      }
+    }
+  }
 #ifdef G1_PROFILE
   wsync();
   if (lane == 0) s.prof_acc[AP_T1] = __builtin_amdgcn_s_memrealtime();
@@ -954,7 +989,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
-                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work) {
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work,
+                   unsigned long long* diag) {
   if (nw <= 0) return 0;
   if (reinterpret_cast<uintptr_t>(tape) & 15u) return (int)hipErrorInvalidValue;  // 16-byte copies of the factors
   const int* perm = nullptr;
@@ -964,7 +1000,7 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
     perm = (const int*)work;
   }
   hipLaunchKernelGGL(k_adjoint, dim3(nw), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in,
-                     gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm);
+                     gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm, diag);
   return (int)hipGetLastError();
 }
 size_t adjoint_lds_bytes() { return sizeof(Adj); }

@@ -8,7 +8,7 @@
 namespace g1k {
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info, float* ocon, float* tape, void* work, int order);
+                   int* info, float* ocon, float* tape, void* work, int order, unsigned long long* diag);
 int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work);
 size_t order_work_bytes(int nw);
 size_t forward_lds_bytes();
@@ -27,7 +27,8 @@ int launch_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float
                           const float* gsc, const float* gq_in, const float* gv_in, float* gq, float* gv);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
-                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work);
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work,
+                   unsigned long long* diag);
 }  // namespace g1k
 
 namespace {
@@ -76,7 +77,15 @@ int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel,
                    int* info, float* ocon, float* tape, void* work) {
   if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0) return (int)hipErrorInvalidValue;
   return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
-                             work, 1);
+                             work, 1, nullptr);
+}
+
+int dk_fwd_forward_diag(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm,
+                        const float* ctrl, const float* fric, const float* com, int iterations, int nsub, float* oq,
+                        float* ov, float* ow, int* info, float* ocon, float* tape, void* work, unsigned long long* d) {
+  if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0 || !d) return (int)hipErrorInvalidValue;
+  return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
+                             work, 1, d);
 }
 
 int dk_fwd_order(hipStream_t st, int nw, const float* qpos, void* work) {
@@ -89,7 +98,7 @@ int dk_fwd_forward_ordered(hipStream_t st, int nw, const float* qpos, const floa
                            float* ov, float* ow, int* info, float* ocon, float* tape, const void* work) {
   if (nw < 0 || nsub < 1 || nsub > 32 || iterations < 0 || (nw > 0 && !work)) return (int)hipErrorInvalidValue;
   return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
-                             const_cast<void*>(work), 2);
+                             const_cast<void*>(work), 2, nullptr);
 }
 
 int dk_fwd_kinematics(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* com, float* qn,
@@ -138,7 +147,7 @@ int dk_fwd_forward_static(hipStream_t st, int nw, const float* qpos, const float
   const int rc = scratch_ptr(&work);
   if (rc) return rc;
   return g1k::launch_forward(st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub, oq, ov, ow, info, ocon, tape,
-                             work, 1);
+                             work, 1, nullptr);
 }
 
 // the profiling build's per-world phase cycles of the last forward (test and measurement helper; -1 in production)
@@ -166,7 +175,18 @@ int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const f
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
   return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
-                             clamp_soft, clamp_kv, normal, work);
+                             clamp_soft, clamp_kv, normal, work, nullptr);
+}
+
+int dk_adjoint_work_diag(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                         const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                         const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work,
+                         unsigned long long* d) {
+  if (nw < 0 || nsub < 1 || nsub > 32 || clamp_kv < 0 || clamp_kv > 2 || normal < 0 || normal > 3 || !d)
+    return (int)hipErrorInvalidValue;
+  if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
+  return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
+                             clamp_soft, clamp_kv, normal, work, d);
 }
 
 long long dk_adjoint_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }

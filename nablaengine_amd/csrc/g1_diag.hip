@@ -1,36 +1,16 @@
 // Diagnostic counters of the forward and the backward (the reference's dk_torch_diag_fwd / dk_torch_diag_bwd,
-// torch_ffi.py:85-156): a caller-owned array of 18 uint64 counters per device, added to by one small kernel after each
-// forward / backward, in the reference's order (torch_ffi.py:56-59 DIAG):
-//   0 fwd_calls, 1 fwd_worlds, 2 fwd_unsupported_worlds (info[3] != 0), 3 fwd_iteration_limit_worlds (the last
-//   substep's iterations reached the cap), 4 tape_records, 5 refact_records, 6 nonconv_records, 7 singular_records (the
-//   records' flags), 8 bwd_calls, 9 bwd_rows, 10 nonfinite_rows (a non-finite gradient), 11-13 nonfinite_{qpos,qvel,
-//   ctrl}_rows, 14 nonfinite_cotangent_rows, 15 replay_mismatch_worlds, 16 fwd_contact_overflow_worlds,
-//   17 fwd_row_overflow_worlds.
-// The backward also writes the non-finite bits (1 qpos, 2 qvel, 4 ctrl, 8 cotangent) << 16 into its info. The forward's
-// counters: one thread per world (grid-stride); the backward's: one wave per world; a wave sum per count, one 64-bit
-// atomic add per wave and count; integer counts only.
+// torch_ffi.py:85-156) as kernels of their own, run after a forward / backward: the counters and their order are in
+// g1_diag.h. The forward's counters: one thread per world (grid-stride); the backward's: one wave per world; a wave
+// sum per count, one 64-bit atomic add per wave and count; integer counts only.
 #include "g1_device.h"
+#include "g1_diag.h"
 #include "g1_tape.h"
 
 namespace g1k {
 
-enum {
-  D_FWD_CALLS = 0, D_FWD_WORLDS, D_FWD_UNSUPPORTED, D_FWD_ITER_LIMIT, D_TAPE_RECORDS, D_REFACT, D_NONCONV, D_SINGULAR,
-  D_BWD_CALLS, D_BWD_ROWS, D_NONFINITE, D_NONFINITE_QPOS, D_NONFINITE_QVEL, D_NONFINITE_CTRL, D_NONFINITE_COT,
-  D_REPLAY_MISMATCH, D_CONTACT_OVERFLOW, D_ROW_OVERFLOW, NDIAG
-};
-constexpr int NONFINITE_SHIFT = 16;
-constexpr int ADJ_REPLAY_MISMATCH = 1 << 13;
-
 __device__ __forceinline__ void diag_add(unsigned long long* d, int k, int v) {
   const int t = wsumi(v);
   if ((threadIdx.x & 63) == 0 && t) atomicAdd(&d[k], (unsigned long long)t);
-}
-
-__device__ __forceinline__ bool all_finite(const float* x, int n) {
-  bool ok = true;
-  for (int i = 0; i < n; i++) ok &= __builtin_isfinite(x[i]);
-  return ok;
 }
 
 __global__ __launch_bounds__(256) void k_diag_fwd(unsigned long long* d, int nw, int nsub, int iterations,

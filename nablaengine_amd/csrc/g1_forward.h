@@ -19,6 +19,7 @@ struct __align__(16) Sim {
   float O[4];
   float fric;
   int ncon, ncon_raw, nlim, nefc, flags, niter;
+  int dcnt;  // the records' flags counted over the substeps: refactored | not converged << 8 | singular << 16
   unsigned clampm[2];  // dofs whose actuator force is at its limit (tape)
 #ifdef G1_PROFILE
   unsigned long long prof_t, prof_acc[NPHASE];

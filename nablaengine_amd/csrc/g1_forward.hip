@@ -18,6 +18,7 @@
 // plus the cross-chain terms of contacts between two robot bodies.
 #include "g1_forward.h"
 #include "g1_collide.h"
+#include "g1_diag.h"
 #include "g1_tape.h"
 
 #define PROF(k) PROF_MARK(s.prof_acc, s.prof_t, k)
@@ -1040,6 +1041,7 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
                                      | (unsigned)min(no.it, 255) << 24);
       rec[REC_FLAGS] = __uint_as_float((unsigned)(s.flags & 20) | (no.fresh ? 0u : (unsigned)FLAG_REFACT)
                                        | (no.conv ? 0u : (unsigned)FLAG_NONCONV) | (sing ? (unsigned)FLAG_SINGULAR : 0u));
+      s.dcnt += (no.fresh ? 0 : 1) | (no.conv ? 0 : 1 << 8) | (sing ? 1 << 16 : 0);
     }
     wsync();
   }
@@ -1103,7 +1105,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                                                 int iterations, int nsub, float* __restrict__ oqpos,
                                                 float* __restrict__ oqvel, float* __restrict__ owarm,
                                                 int* __restrict__ info, float* __restrict__ ocon,
-                                                float* __restrict__ tape, const int* __restrict__ perm) {
+                                                float* __restrict__ tape, const int* __restrict__ perm,
+                                                unsigned long long* __restrict__ diag) {
   __shared__ Sim s;
   const int lane = threadIdx.x;
   if ((int)blockIdx.x >= nw) return;
@@ -1117,7 +1120,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane < NV) { s.qvel[lane] = iv; s.qacc[lane] = iw; }
   if (lane < NU) s.ctrl[lane] = iu;
   if (lane < 3) s.com[lane] = ic;
-  if (lane == 0) { s.fric = ifr; s.flags = 0; s.niter = 0; }
+  if (lane == 0) { s.fric = ifr; s.flags = 0; s.niter = 0; s.dcnt = 0; }
   s.dsub[lane] = lane < NV ? cTree.dofmask32[lane] : 0u;
   chain_table(s.chain, lane);
   if (lane < 8) s.S[NV][lane] = 0.f;  // body_vel's zero padding row and entries
@@ -1151,6 +1154,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     info[4 * w + 1] = s.ncon_raw;
     info[4 * w + 2] = s.nefc;
     info[4 * w + 3] = s.flags;
+    if (diag) {  // this world's part of the diagnostic counters (what k_diag_fwd counts from info and the tape)
+      const int f = s.flags, dc = s.dcnt;
+      if (f) atomicAdd(&diag[D_FWD_UNSUPPORTED], 1ull);
+      if (f & 4) atomicAdd(&diag[D_CONTACT_OVERFLOW], 1ull);
+      if (f & 16) atomicAdd(&diag[D_ROW_OVERFLOW], 1ull);
+      if (s.niter >= iterations) atomicAdd(&diag[D_FWD_ITER_LIMIT], 1ull);
+      if (dc & 255) atomicAdd(&diag[D_REFACT], (unsigned long long)(dc & 255));
+      if ((dc >> 8) & 255) atomicAdd(&diag[D_NONCONV], (unsigned long long)((dc >> 8) & 255));
+      if (dc >> 16) atomicAdd(&diag[D_SINGULAR], (unsigned long long)(dc >> 16));
+      if (blockIdx.x == 0) {
+        atomicAdd(&diag[D_FWD_CALLS], 1ull);
+        atomicAdd(&diag[D_FWD_WORLDS], (unsigned long long)nw);
+        if (tape) atomicAdd(&diag[D_TAPE_RECORDS], (unsigned long long)nw * (unsigned long long)nsub);
+      }
+    }
   }
 }
 
@@ -1158,10 +1176,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 namespace g1k {
 int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work);
-// order: 0 index order (work unused), 1 compute the order into work first, 2 the order already in work
+// order: 0 index order (work unused), 1 compute the order into work first, 2 the order already in work; diag: the
+// diagnostic counters added to by each world at its end, or NULL
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
-                   int* info, float* ocon, float* tape, void* work, int order) {
+                   int* info, float* ocon, float* tape, void* work, int order, unsigned long long* diag) {
   if (nw <= 0) return 0;
   const int* perm = nullptr;
   if (work && order) {  // the dispatch order, heaviest worlds first
@@ -1172,7 +1191,7 @@ int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel,
     perm = (const int*)work;
   }
   hipLaunchKernelGGL(k_forward, dim3(nw), dim3(64), 0, st, nw, qpos, qvel, warm, ctrl, fric, com, iterations, nsub,
-                     oq, ov, ow, info, ocon, tape, perm);
+                     oq, ov, ow, info, ocon, tape, perm, diag);
   return (int)hipGetLastError();
 }
 size_t forward_lds_bytes() { return sizeof(Sim); }

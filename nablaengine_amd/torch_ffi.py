@@ -28,8 +28,9 @@ calls are the torch.library custom ops nablaengine::forward, ::backward, ::kinem
 fake implementations (opaque nodes, no graph break with fullgraph=True; reference torch_ffi.py:583-655); in eager mode
 the same functions are called directly.
 
-Diagnostics (reference torch_ffi.py:56-62, 664-742): per device 18 int64 counters (DIAG) added to on the device by one
-small kernel after each forward and backward (set_diagnostics(False) skips it), read with diagnostics() (the tensor)
+Diagnostics (reference torch_ffi.py:56-62, 664-742): per device 18 int64 counters (DIAG) added to on the device by the
+forward and adjoint kernels, each world at its end (set_diagnostics(False) skips it; the reference runs a small kernel
+after each call, which the library also exports: dk_torch_diag_fwd / _bwd), read with diagnostics() (the tensor)
 or read_diagnostics() (a dict; resets). The backward's info then also carries the non-finite bits (NONFINITE_* <<
 NONFINITE_SHIFT) besides the union of the records' flags and ADJ_REPLAY_MISMATCH. set_overflow_warnings(True) warns
 when worlds exceeded the contact or row capacity.
@@ -103,6 +104,8 @@ def load_library(path=None):
         vp, i32, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
         lib.dk_fwd_forward.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 7
         lib.dk_fwd_forward.restype = i32
+        lib.dk_fwd_forward_diag.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 8
+        lib.dk_fwd_forward_diag.restype = i32
         lib.dk_fwd_forward_ordered.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 7
         lib.dk_fwd_forward_ordered.restype = i32
         lib.dk_fwd_order.argtypes, lib.dk_fwd_order.restype = [vp, i32, vp, vp], i32
@@ -113,6 +116,8 @@ def load_library(path=None):
         lib.dk_adjoint.restype = i32
         lib.dk_adjoint_work.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp]
         lib.dk_adjoint_work.restype = i32
+        lib.dk_adjoint_work_diag.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
+        lib.dk_adjoint_work_diag.restype = i32
         lib.dk_adjoint_work_bytes.argtypes, lib.dk_adjoint_work_bytes.restype = [i32], ctypes.c_longlong
         lib.dk_fwd_kinematics.argtypes, lib.dk_fwd_kinematics.restype = [vp, i32] + [vp] * 8, i32
         lib.dk_torch_diag_fwd.argtypes, lib.dk_torch_diag_fwd.restype = [vp, vp, i32, i32, i32, vp, vp], i32
@@ -255,15 +260,15 @@ def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, t
     work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device=qpos.device)
     with _OnDevice(dev):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        _rc(lib.dk_fwd_forward(st, B, *map(_ptr, (qpos, qvel, warm, ctrl, friction, com)), int(iterations),
-                               int(substeps), _ptr(q1), _ptr(v1), _ptr(w1), _ptr(info), None,
-                               _ptr(tp) if tape else None, _ptr(work) if work.numel() else None),
-            "the forward launch")
+        args = (st, B, *map(_ptr, (qpos, qvel, warm, ctrl, friction, com)), int(iterations), int(substeps),
+                _ptr(q1), _ptr(v1), _ptr(w1), _ptr(info), None, _ptr(tp) if tape else None,
+                _ptr(work) if work.numel() else None)
+        if _DIAG_ON[0]:  # the counters added to by the forward kernel itself (dk_torch_diag_fwd's counts)
+            _rc(lib.dk_fwd_forward_diag(*args, _ptr(_DIAG[dev])), "the forward launch")
+        else:
+            _rc(lib.dk_fwd_forward(*args), "the forward launch")
         if kinematics:  # the output state's kinematics (reference torch_ffi.py:488-489)
             _rc(lib.dk_fwd_kinematics(st, B, _ptr(q1), _ptr(v1), _ptr(com), *map(_ptr, kin)), "the kinematics launch")
-        if _DIAG_ON[0]:
-            _rc(lib.dk_torch_diag_fwd(st, _ptr(_DIAG[dev]), B, int(substeps), int(iterations), _ptr(info),
-                                      _ptr(tp) if tape else None), "the forward diagnostics launch")
     return [q1, v1, w1, info, tp] + kin
 
 
@@ -308,14 +313,13 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
             _rc(lib.dk_fwd_kinematics_vjp(st, B, _ptr(q1), _ptr(v1), _ptr(com), *map(_ptr, kin_cot), _ptr(g_qpos),
                                           _ptr(g_qvel), _ptr(cq), _ptr(cv)), "the kinematics VJP launch")
             g_qpos, g_qvel = cq, cv
-        _rc(lib.dk_adjoint_work(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos),
-                                _ptr(g_qvel), _ptr(gq), _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl),
-                                ctypes.c_float(0.0 if clamp_soft is None else clamp_soft), v[0], v[1],
-                                _ptr(work) if work.numel() else None),
-            "the adjoint launch")
-        if _DIAG_ON[0]:  # counters, and the non-finite bits into info (reference torch_ffi.py:538-540)
-            _rc(lib.dk_torch_diag_bwd(st, _ptr(_DIAG[dev]), B, _ptr(gq), _ptr(gv), _ptr(gu), _ptr(g_qpos), _ptr(g_qvel),
-                                      _ptr(info)), "the backward diagnostics launch")
+        args = (st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos), _ptr(g_qvel), _ptr(gq),
+                _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl), ctypes.c_float(0.0 if clamp_soft is None else clamp_soft),
+                v[0], v[1], _ptr(work) if work.numel() else None)
+        if _DIAG_ON[0]:  # counters, and the non-finite bits into info (reference torch_ffi.py:538-540), by the
+            _rc(lib.dk_adjoint_work_diag(*args, _ptr(_DIAG[dev])), "the adjoint launch")  # adjoint kernel itself
+        else:
+            _rc(lib.dk_adjoint_work(*args), "the adjoint launch")
     return [gq, gv, gu, info]
 
 
@@ -560,8 +564,8 @@ def backward(tape, friction, com, g_qpos, g_qvel, *, substeps=SUBSTEPS, clamp_kv
 
 def set_diagnostics(enabled):
     """Switch the device counters and the backward's non-finite bits on (the default) or off; returns the previous
-    setting (reference torch_ffi.py:678-686). One small kernel per forward and per backward; outputs and gradients are
-    the same either way."""
+    setting (reference torch_ffi.py:678-686). When on, the forward and adjoint kernels add each world's counts at its
+    end (dk_fwd_forward_diag / dk_adjoint_work_diag); outputs and gradients are the same either way."""
     prev = _DIAG_ON[0]
     _DIAG_ON[0] = bool(enabled)
     return prev

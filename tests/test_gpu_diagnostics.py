@@ -124,3 +124,62 @@ def test_capacity_overflow(ffi):
     finally:
         ffi.set_overflow_warnings(prev)
     assert any(issubclass(w.category, RuntimeWarning) and "capacity" in str(w.message) for w in w1_)
+
+
+def test_fused_counters_equal_the_separate_kernels(ffi):
+    """The C ABI's dk_fwd_forward_diag / dk_adjoint_work_diag (each world adds its counts at the end of the forward
+    and adjoint kernels; torch_ffi's path) against dk_fwd_forward + dk_torch_diag_fwd and dk_adjoint_work +
+    dk_torch_diag_bwd (the reference's separate kernels) on the same contact-heavy batch with non-finite worlds and
+    cotangents: bitwise the same outputs and gradients, the same backward info (its non-finite bits included), and
+    the same 18 counters."""
+    import ctypes
+    import torch
+    lib = ffi._STATE["lib"]
+    for name in ("dk_torch_diag_fwd", "dk_torch_diag_bwd", "dk_fwd_forward_diag", "dk_adjoint_work_diag"):
+        assert hasattr(lib, name)
+    B, nsub, it = 1000, 4, 10
+    st = synthetic.states(B, config=4, seed=83)
+    st["qvel"][3, 7] = np.nan  # a world whose state, outputs and gradients are non-finite
+    cq, cv = synthetic.cotangents(B, seed=84)
+    cq[7, 3] = np.inf  # the root quaternion's first entry (read by the quaternion's cotangent only)
+    cv[9, 0] = np.nan
+    args = [_t(st[k]) for k in KEYS]
+    tcq, tcv = _t(cq), _t(cv)
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    S = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    kw = dict(dtype=torch.float32, device="cuda")
+    work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+    rw = ffi.rec_words()
+    runs = []
+    for fused in (False, True):
+        d = torch.zeros(18, dtype=torch.int64, device="cuda")
+        q1, v1, w1 = (torch.empty((B, n), **kw) for n in (36, 35, 35))
+        info = torch.empty((B, 4), dtype=torch.int32, device="cuda")
+        tape = torch.empty((B, nsub * rw), **kw)
+        fa = [S, B] + [P(a) for a in args] + [it, nsub, P(q1), P(v1), P(w1), P(info), None, P(tape), P(work)]
+        if fused:
+            assert lib.dk_fwd_forward_diag(*fa, P(d)) == 0
+        else:
+            assert lib.dk_fwd_forward(*fa) == 0
+            assert lib.dk_torch_diag_fwd(S, P(d), B, nsub, it, P(info), P(tape)) == 0
+        gq, gv, gu = (torch.empty((B, n), **kw) for n in (36, 35, 29))
+        binfo = torch.empty((B,), dtype=torch.int32, device="cuda")
+        ba = [S, B, nsub, P(tape), P(args[4]), P(args[5]), P(tcq), P(tcv), P(gq), P(gv), P(gu), P(binfo), None,
+              ctypes.c_float(0.0), 0, 3, P(work)]
+        if fused:
+            assert lib.dk_adjoint_work_diag(*ba, P(d)) == 0
+        else:
+            assert lib.dk_adjoint_work(*ba) == 0
+            assert lib.dk_torch_diag_bwd(S, P(d), B, P(gq), P(gv), P(gu), P(tcq), P(tcv), P(binfo)) == 0
+        torch.cuda.synchronize()
+        runs.append([x.cpu().numpy() for x in (q1, v1, w1, info, tape, gq, gv, gu, binfo, d)])
+    names = ("qpos'", "qvel'", "warm'", "info", "tape", "g_qpos", "g_qvel", "g_ctrl", "backward info", "counters")
+    for name, a, b in zip(names, *runs):
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b), name
+    d = dict(zip(ffi.DIAG, runs[1][-1].tolist()))
+    nf = (runs[1][8] >> ffi.NONFINITE_SHIFT) & 15
+    print({k: v for k, v in d.items() if v})
+    assert nf[7] & ffi.NONFINITE_COT and nf[9] & ffi.NONFINITE_COT and nf[3] & 7  # (bad cotangents spread)
+    assert d["nonfinite_cotangent_rows"] == 2 and d["nonfinite_rows"] == int(((nf & 7) != 0).sum()) >= 1
+    assert d["fwd_calls"] == 1 and d["bwd_calls"] == 1 and d["fwd_worlds"] == B and d["tape_records"] == nsub * B
