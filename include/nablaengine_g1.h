@@ -120,6 +120,16 @@ int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const f
                     const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                     const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work);
 long long dk_adjoint_work_bytes(int nw);
+/* No counterpart in the reference's ABI: the adjoint's dispatch order on its own, written into work
+ * (dk_adjoint_work_bytes(nw) bytes) from the tape; and the adjoint launched with that order already in work, for
+ * callers that run several VJPs on one tape (the step Jacobian's 71 one-hot cotangents). d: the diagnostic counters,
+ * counted as dk_adjoint_work_diag does, or NULL (no counting, no non-finite bits in info). Results are the same in any
+ * order. */
+int dk_adjoint_order(hipStream_t st, int nw, int nsub, const float* tape, void* work);
+int dk_adjoint_work_ordered(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                            const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl,
+                            int* info, const float* ctrl, float clamp_soft, int clamp_kv, int normal, const void* work,
+                            unsigned long long* d);
 
 /* The reference's per-variant unit names (jax_ffi.py:180,845-846: dk_kv{0,1,2}_n{0..3}), each the entry above with
  * its (clamp_kv, normal) fixed; _upload, _launch and _sizes as dk_fwd_upload / dk_fwd_launch / dk_fwd_sizes (o[6],

@@ -989,14 +989,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
-                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work,
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, int order,
                    unsigned long long* diag) {
   if (nw <= 0) return 0;
   if (reinterpret_cast<uintptr_t>(tape) & 15u) return (int)hipErrorInvalidValue;  // 16-byte copies of the factors
   const int* perm = nullptr;
-  if (work) {  // the dispatch order, heaviest worlds first
-    const int rc = launch_order_adj(st, nw, nsub, tape, work);
-    if (rc) return rc;
+  if (work && order) {  // the dispatch order, heaviest worlds first (order 1: computed here; 2: already in work)
+    if (order == 1) {
+      const int rc = launch_order_adj(st, nw, nsub, tape, work);
+      if (rc) return rc;
+    }
     perm = (const int*)work;
   }
   hipLaunchKernelGGL(k_adjoint, dim3(nw), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in,

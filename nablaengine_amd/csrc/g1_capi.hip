@@ -27,8 +27,9 @@ int launch_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float
                           const float* gsc, const float* gq_in, const float* gv_in, float* gq, float* gv);
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
-                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work,
+                   const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, int order,
                    unsigned long long* diag);
+int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
 }  // namespace g1k
 
 namespace {
@@ -175,7 +176,7 @@ int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const f
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
   return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
-                             clamp_soft, clamp_kv, normal, work, nullptr);
+                             clamp_soft, clamp_kv, normal, work, 1, nullptr);
 }
 
 int dk_adjoint_work_diag(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
@@ -186,7 +187,24 @@ int dk_adjoint_work_diag(hipStream_t st, int nw, int nsub, const float* tape, co
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
   return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
-                             clamp_soft, clamp_kv, normal, work, d);
+                             clamp_soft, clamp_kv, normal, work, 1, d);
+}
+
+int dk_adjoint_order(hipStream_t st, int nw, int nsub, const float* tape, void* work) {
+  if (nw < 0 || nsub < 1 || nsub > 32 || (nw > 0 && !work)) return (int)hipErrorInvalidValue;
+  return nw > 0 ? g1k::launch_order_adj(st, nw, nsub, tape, work) : 0;
+}
+
+int dk_adjoint_work_ordered(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
+                            const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl,
+                            int* info, const float* ctrl, float clamp_soft, int clamp_kv, int normal, const void* work,
+                            unsigned long long* d) {
+  if (nw < 0 || nsub < 1 || nsub > 32 || clamp_kv < 0 || clamp_kv > 2 || normal < 0 || normal > 3 ||
+      (nw > 0 && !work))
+    return (int)hipErrorInvalidValue;
+  if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
+  return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
+                             clamp_soft, clamp_kv, normal, const_cast<void*>(work), 2, d);
 }
 
 long long dk_adjoint_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }

@@ -4,7 +4,7 @@ torch_ffi.py module docstring for rollouts with torch.utils.checkpoint):
   jacobian(qpos, qvel, warm, ctrl, friction, com, *, iterations, substeps, clamp_kv, normal, clamp_soft)
       -> (J (B, 71, 99), info (B, 4)): the full step Jacobian per world, rows the outputs (qpos' in qpos form 36,
          qvel' 35), columns the inputs (qpos tangent 35, qvel 35, ctrl 29), from one taped forward and 71 one-hot
-         VJPs on that tape (the reference's method);
+         VJPs on that tape (the reference's method), the adjoint's dispatch order computed once for the 71;
   rollout(qpos, qvel, warm, ctrls, friction, com, *, checkpoint_every=8, **step_kw) -> [(qpos_t, qvel_t)]: T steps
       under autograd, each segment of checkpoint_every steps recomputed in the backward (torch.utils.checkpoint):
       only the segment being differentiated holds its tapes.
@@ -18,15 +18,16 @@ NOUT, NIN = torch_ffi.NQ + torch_ffi.NV, 2 * torch_ffi.NV + torch_ffi.NU  # 71 x
 
 
 def qpos_tangent(qpos, g):
-    """(B, 36) qpos-form cotangents -> (B, 35) tangent-form (integrate_pos's transpose at 0) at states qpos."""
+    """(..., B, 36) qpos-form cotangents -> (..., B, 35) tangent-form (integrate_pos's transpose at 0) at states qpos
+    (B, 36)."""
     import torch
     q = qpos[:, 3:7] / qpos[:, 3:7].norm(dim=1, keepdim=True)
-    gq = g[:, 3:7]
+    gq = g[..., 3:7]
     # vec(conj(q) (x) gq): w = q0, v = -q[1:]; (w, v) (x) (s, u) = (w s - v.u, w u + s v + v x u)
     w, v = q[:, :1], -q[:, 1:]
-    s, u = gq[:, :1], gq[:, 1:]
-    rot = 0.5 * (w * u + s * v + torch.cross(v, u, dim=1))
-    return torch.cat([g[:, :3], rot, g[:, 7:]], dim=1)
+    s, u = gq[..., :1], gq[..., 1:]
+    rot = 0.5 * (w * u + s * v + torch.cross(v.expand_as(u), u, dim=-1))
+    return torch.cat([g[..., :3], rot, g[..., 7:]], dim=-1)
 
 
 def jacobian(qpos, qvel, warm, ctrl, friction, com, *, iterations=torch_ffi.ITERATIONS, substeps=torch_ffi.SUBSTEPS,
@@ -36,21 +37,14 @@ def jacobian(qpos, qvel, warm, ctrl, friction, com, *, iterations=torch_ffi.ITER
     q1, v1, w1, info, tape = torch_ffi.forward(qpos, qvel, warm, ctrl, friction, com, iterations=iterations,
                                                substeps=substeps, tape=True)
     B = qpos.shape[0]
-    kw = dict(dtype=torch.float32, device=qpos.device)
-    J = torch.empty((B, NOUT, NIN), **kw)
-    gq_out, gv_out = torch.zeros((B, torch_ffi.NQ), **kw), torch.zeros((B, torch_ffi.NV), **kw)
+    eye = torch.eye(NOUT, dtype=torch.float32, device=qpos.device)  # output r's one-hot cotangent, every world
+    cq = eye[:, :torch_ffi.NQ].unsqueeze(1).expand(NOUT, B, torch_ffi.NQ).contiguous()
+    cv = eye[:, torch_ffi.NQ:].unsqueeze(1).expand(NOUT, B, torch_ffi.NV).contiguous()
     soft_ctrl = ctrl if int(clamp_kv) == 2 else None
-    for r in range(NOUT):
-        g = gq_out if r < torch_ffi.NQ else gv_out
-        c = r if r < torch_ffi.NQ else r - torch_ffi.NQ
-        g[:, c] = 1.0
-        gq, gv, gu, _ = torch_ffi.backward(tape, friction, com, gq_out, gv_out, substeps=substeps, clamp_kv=clamp_kv,
-                                           normal=normal, ctrl=soft_ctrl, clamp_soft=clamp_soft)
-        g[:, c] = 0.0
-        J[:, r, :torch_ffi.NV] = qpos_tangent(qpos, gq)
-        J[:, r, torch_ffi.NV:2 * torch_ffi.NV] = gv
-        J[:, r, 2 * torch_ffi.NV:] = gu
-    return J, info
+    gq, gv, gu, _ = torch_ffi._vjps(tape, friction, com, cq, cv, soft_ctrl, substeps=substeps, clamp_kv=clamp_kv,
+                                    normal=normal, clamp_soft=clamp_soft)
+    J = torch.cat([qpos_tangent(qpos, gq), gv, gu], dim=2)  # (71, B, 99)
+    return J.transpose(0, 1).contiguous(), info
 
 
 def rollout(qpos, qvel, warm, ctrls, friction, com, *, checkpoint_every=8, **step_kw):

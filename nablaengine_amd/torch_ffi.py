@@ -118,6 +118,9 @@ def load_library(path=None):
         lib.dk_adjoint_work.restype = i32
         lib.dk_adjoint_work_diag.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
         lib.dk_adjoint_work_diag.restype = i32
+        lib.dk_adjoint_order.argtypes, lib.dk_adjoint_order.restype = [vp, i32, i32, vp, vp], i32
+        lib.dk_adjoint_work_ordered.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
+        lib.dk_adjoint_work_ordered.restype = i32
         lib.dk_adjoint_work_bytes.argtypes, lib.dk_adjoint_work_bytes.restype = [i32], ctypes.c_longlong
         lib.dk_fwd_kinematics.argtypes, lib.dk_fwd_kinematics.restype = [vp, i32] + [vp] * 8, i32
         lib.dk_torch_diag_fwd.argtypes, lib.dk_torch_diag_fwd.restype = [vp, vp, i32, i32, i32, vp, vp], i32
@@ -272,8 +275,8 @@ def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, t
     return [q1, v1, w1, info, tp] + kin
 
 
-def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal, clamp_soft, kin_state=(),
-                   kin_cot=()):
+def _backward_checks(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal):
+    """The backward's argument checks (TypeError / ValueError, reference torch_ffi.py:419-428); returns (device, B)."""
     import torch
     if not isinstance(tape, torch.Tensor) or tape.device.type != "cuda":
         raise _err("tape must be a GPU torch.Tensor")
@@ -292,6 +295,14 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
         _check("ctrl", ctrl, (B, NU), dev)
     if dev not in _READY:
         init(dev)
+    return dev, B
+
+
+def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal, clamp_soft, kin_state=(),
+                   kin_cot=()):
+    import torch
+    dev, B = _backward_checks(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal)
+    v = (int(clamp_kv), int(normal))
     kw = dict(dtype=torch.float32, device=tape.device)
     gq, gv, gu = torch.empty((B, NQ), **kw), torch.empty((B, NV), **kw), torch.empty((B, NU), **kw)
     info = torch.empty((B,), dtype=torch.int32, device=tape.device)
@@ -322,6 +333,55 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
             _rc(lib.dk_adjoint_work(*args), "the adjoint launch")
     return [gq, gv, gu, info]
 
+
+
+def _vjps(tape, friction, com, g_qpos, g_qvel, ctrl=None, *, substeps=SUBSTEPS, clamp_kv=CLAMP_KV, normal=NORMAL,
+          clamp_soft=None):
+    """K VJPs of one taped step: g_qpos (K, B, 36) and g_qvel (K, B, 35) output cotangents -> g_qpos_in (K, B, 36),
+    g_qvel_in (K, B, 35), g_ctrl (K, B, 29) and the last VJP's info (B,). Each k is backward(tape, ..., g_qpos[k],
+    g_qvel[k]) bitwise (the diagnostics count K backward calls), with the adjoint's dispatch order computed once for
+    all K (dk_adjoint_order, dk_adjoint_work_ordered): the step Jacobian's driver."""
+    import torch
+    K = g_qpos.shape[0] if isinstance(g_qpos, torch.Tensor) and g_qpos.dim() == 3 else 0
+    if K < 1 or not isinstance(g_qvel, torch.Tensor) or g_qvel.dim() != 3 or g_qvel.shape[0] != K:
+        raise _err("g_qpos (K, B, 36) and g_qvel (K, B, 35), K >= 1")
+    dev, B = _backward_checks(tape, friction, com, g_qpos[0], g_qvel[0], ctrl, substeps, clamp_kv, normal)
+    kw = dict(dtype=torch.float32, device=tape.device)
+    gq, gv, gu = (torch.empty((K, B, n), **kw) for n in (NQ, NV, NU))
+    info = torch.empty((B,), dtype=torch.int32, device=tape.device)
+    if B == 0:
+        return gq, gv, gu, info
+    lib = _STATE["lib"]
+    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
+    soft = ctypes.c_float(0.0 if clamp_soft is None else clamp_soft)
+    with _OnDevice(dev):
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        _rc(lib.dk_adjoint_order(st, B, int(substeps), _ptr(tape), _ptr(work)), "the adjoint order launch")
+        d = _ptr(_DIAG[dev]) if _DIAG_ON[0] else None
+        for k in range(K):
+            _check("g_qpos[k]", g_qpos[k], (B, NQ), dev)
+            _check("g_qvel[k]", g_qvel[k], (B, NV), dev)
+            _rc(lib.dk_adjoint_work_ordered(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com),
+                                            _ptr(g_qpos[k]), _ptr(g_qvel[k]), _ptr(gq[k]), _ptr(gv[k]), _ptr(gu[k]),
+                                            _ptr(info), _ptr(ctrl), soft, int(clamp_kv), int(normal), _ptr(work), d),
+                "the adjoint launch")
+    return gq, gv, gu, info
+    dev = tape.device.index
+    lib = _STATE["lib"]
+    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
+    soft = ctypes.c_float(0.0 if clamp_soft is None else clamp_soft)
+    with _OnDevice(dev):
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        _rc(lib.dk_adjoint_order(st, B, int(substeps), _ptr(tape), _ptr(work)), "the adjoint order launch")
+        d = _ptr(_DIAG[dev]) if _DIAG_ON[0] else None
+        for k in range(1, K):
+            _check("g_qpos[k]", g_qpos[k], (B, NQ), dev)
+            _check("g_qvel[k]", g_qvel[k], (B, NV), dev)
+            _rc(lib.dk_adjoint_work_ordered(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com),
+                                            _ptr(g_qpos[k]), _ptr(g_qvel[k]), _ptr(gq[k]), _ptr(gv[k]), _ptr(gu[k]),
+                                            _ptr(info), _ptr(ctrl), soft, int(clamp_kv), int(normal), _ptr(work), d),
+                "the adjoint launch")
+    return gq, gv, gu, info
 
 def _kinematics_impl(qpos, qvel, com):
     import torch

@@ -67,6 +67,31 @@ def test_jacobian_is_the_vjp(ffi):
     assert np.median(e) <= 2e-5 and e.max() <= 5e-4
 
 
+
+def test_jacobian_rows_are_the_backward_vjps(ffi):
+    """The Jacobian driver's 71 VJPs share one adjoint dispatch order (dk_adjoint_order, dk_adjoint_work_ordered): each
+    row is bitwise the VJP torch_ffi.backward computes for that output's one-hot cotangent, on contact-heavy states at
+    a batch size that is not a multiple of anything (the order never changes a result); the diagnostics count 71
+    backward calls."""
+    import torch
+    from nablaengine_amd import rollout
+    B = 301
+    st = synthetic.states(B, config=4, seed=85)
+    args = [_t(st[k]) for k in KEYS]
+    ffi.read_diagnostics(reset=True)
+    J, info = rollout.jacobian(*args)
+    d = ffi.read_diagnostics()
+    assert d["bwd_calls"] == 71 and d["bwd_rows"] == 71 * B and d["fwd_calls"] == 1
+    q1, v1, w1, info2, tape = ffi.forward(*args, tape=True)
+    assert torch.equal(info, info2)
+    for r in (0, 3, 6, 35, 36, 40, 70):
+        cq = torch.zeros((B, 36), device="cuda")
+        cv = torch.zeros((B, 35), device="cuda")
+        (cq if r < 36 else cv)[:, r if r < 36 else r - 36] = 1.0
+        gq, gv, gu, _ = ffi.backward(tape, args[4], args[5], cq, cv)
+        row = torch.cat([rollout.qpos_tangent(args[0], gq), gv, gu], 1)
+        assert torch.equal(J[:, r, :].view(torch.int32), row.view(torch.int32)), r
+
 def test_checkpointed_rollout_is_bitwise_the_plain_one(ffi):
     """A 4-step BPTT rollout on contact-heavy config-4 states: the gradients of a loss on every state with segments
     of 2 steps recomputed in the backward are bitwise those with every tape kept."""
