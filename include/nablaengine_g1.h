@@ -114,7 +114,7 @@ int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float*
                const float* ctrl, float clamp_soft, int clamp_kv, int normal);
 
 /* No counterpart in the reference's ABI (its adjoint entries take no work buffer): dk_adjoint with a work buffer of
- * dk_adjoint_work_bytes(nw) bytes, in which the worlds are ordered heaviest first (the tape's row counts) before the
+ * dk_adjoint_work_bytes(nw) bytes, in which the worlds are ordered heaviest first (the tape's contacts) before the
  * launch. Same results as dk_adjoint, which is this entry with work = NULL. */
 int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                     const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
