@@ -181,3 +181,18 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     assert lib.dk_kv2_n3_adjoint(None, 3, 4, *[None] * 10, 0.2) == 1
     assert lib.dk_fwd_kinematics(None, -1, *[None] * 8) == 1 and lib.dk_fwd_kinematics(None, 0, *[None] * 8) == 0
     assert lib.dk_torch_diag_fwd(None, None, 3, 4, 10, None, None) == 1
+    # the entries with the counters or a precomputed adjoint order
+    lib.dk_fwd_forward_diag.argtypes = fwd + [P]
+    lib.dk_adjoint_work_diag.argtypes = adj + [P]
+    lib.dk_adjoint_work_ordered.argtypes = adj + [P]
+    lib.dk_adjoint_order.argtypes = [P, I, I, P, P]
+    d = 0x1000  # never dereferenced: every call below returns before a launch
+    fd = lambda nw, d=d: lib.dk_fwd_forward_diag(None, nw, *n6, 10, 4, *[None] * 7, d)
+    assert fd(0) == 0 and fd(-1) == 1 and fd(3, d=None) == 1  # the counters are required
+    ad = lambda nw, d=d: lib.dk_adjoint_work_diag(None, nw, 4, None, *[None] * 9, 0.2, 1, 0, None, d)
+    assert ad(0) == 0 and ad(-1) == 1 and ad(3, d=None) == 1
+    assert lib.dk_adjoint_order(None, 3, 4, None, None) == 1 and lib.dk_adjoint_order(None, 0, 4, None, None) == 0
+    ao = lambda nw, work=None, tape=None, kv=1: lib.dk_adjoint_work_ordered(None, nw, 4, tape, *[None] * 9, 0.2, kv,
+                                                                            0, work, None)
+    assert ao(0) == 0 and ao(3) == 1  # the order is read from work
+    assert ao(3, work=d, kv=2) == 1 and ao(3, work=d, tape=0x1004) == 1
