@@ -130,6 +130,13 @@ int dk_adjoint_work_ordered(hipStream_t st, int nw, int nsub, const float* tape,
                             const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl,
                             int* info, const float* ctrl, float clamp_soft, int clamp_kv, int normal, const void* work,
                             unsigned long long* d);
+/* No counterpart in the reference's ABI: ncot VJPs of one tape in one launch (the step Jacobian's 71 one-hot
+ * cotangents), each set bitwise what dk_adjoint_work_diag gives for it. gq_out (ncot, nw, 36), gv_out (ncot, nw, 35)
+ * -> gq_in (ncot, nw, 36), gv_in (ncot, nw, 35), gctrl (ncot, nw, 29), info (ncot, nw); work as dk_adjoint_work's (one
+ * dispatch order for every set); d: the counters (ncot backward calls), or NULL. nw * ncot < 2^31. */
+int dk_adjoint_many(hipStream_t st, int nw, int ncot, int nsub, const float* tape, const float* fric, const float* com,
+                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, unsigned long long* d);
 
 /* The reference's per-variant unit names (jax_ffi.py:180,845-846: dk_kv{0,1,2}_n{0..3}), each the entry above with
  * its (clamp_kv, normal) fixed; _upload, _launch and _sizes as dk_fwd_upload / dk_fwd_launch / dk_fwd_sizes (o[6],

@@ -876,23 +876,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                                                 float* __restrict__ gctrl, int* __restrict__ info,
                                                 const float* __restrict__ ctrl, float clamp_soft, int clamp_kv,
                                                 int normal, const int* __restrict__ perm,
-                                                unsigned long long* __restrict__ diag) {
+                                                unsigned long long* __restrict__ diag, int ncot) {
   __shared__ Adj s;
   const int lane = threadIdx.x;
-  if ((int)blockIdx.x >= nw) return;
-  const int w = perm ? perm[blockIdx.x] : (int)blockIdx.x;  // heaviest worlds first (g1_order.hip)
+  if ((int)blockIdx.x >= nw * ncot) return;
+  // ncot sets of output cotangents on one tape, set-major: workgroup b takes set b / nw; within a set the worlds run
+  // heaviest first (g1_order.hip). wr: the world's row in its set's cotangents, gradients and info
+  const int kc = (int)blockIdx.x / nw, wi = (int)blockIdx.x - kc * nw;
+  const int w = perm ? perm[wi] : wi, wr = kc * nw + w;
   const float* wt = tape + (size_t)w * nsub * REC_WORDS;
   // the world's inputs: every load issued at once, on every lane (a lane past a row reads a word inside it and drops
   // it), one memory round trip
   const int lc = min(lane, 2), lu = min(lane, NU - 1), lv = min(lane, NV - 1);
   const int lqo = min(lane < 3 ? lane : lane + 1, NQ - 1);  // qpos-form entry of tangent dof lane (< 3 or >= 6)
   const float ic = com[(size_t)w * 3 + lc], iu = ctrl ? ctrl[(size_t)w * NU + lu] : 0.f, ifr = fric[w];
-  const float igv = gv_out[(size_t)w * NV + lv], igq = gq_out[(size_t)w * NQ + lqo];
+  const float igv = gv_out[(size_t)wr * NV + lv], igq = gq_out[(size_t)wr * NQ + lqo];
   if (lane < 3) s.com[lane] = ic;
   if (lane < NU) { s.ub[lane] = 0.f; s.ctrl[lane] = iu; }
   bool cbad = false;  // with the counters: a non-finite entry in the output cotangents (every entry of both rows)
   if (diag) {
-    const float icq = gq_out[(size_t)w * NQ + min(lane, NQ - 1)];
+    const float icq = gq_out[(size_t)wr * NQ + min(lane, NQ - 1)];
     cbad = ballot(!(__builtin_isfinite(icq) && __builtin_isfinite(igv))) != 0ull;
   }
   if (lane == 0) { s.fric = ifr; s.flags = cbad ? NONFINITE_COT << NONFINITE_SHIFT : 0; }
@@ -925,7 +928,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       const float on = rsqrtf(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
       for (int k = 0; k < 4; k++) q[k] = o[k] * on;
     }
-    const float* g = gq_out + (size_t)w * NQ + 3;
+    const float* g = gq_out + (size_t)wr * NQ + 3;
     for (int k = 0; k < 3; k++) {
       float e[4] = {0.f, 0.f, 0.f, 0.f}, t[4];
       e[1 + k] = 1.f;
@@ -936,7 +939,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   wsync();
   for (int k = nsub - 1; k >= 0; k--) adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
   // gradients: qpos form (the quaternion's 2 q (x) (0, t)), qvel, ctrl
-  float* oq = gq_in + (size_t)w * NQ;
+  float* oq = gq_in + (size_t)wr * NQ;
   bool nq = false;  // a non-finite entry among those this lane writes
   if (lane < 3 || (lane >= 6 && lane < NV)) {
     oq[lane < 3 ? lane : lane + 1] = s.qb[lane];
@@ -955,15 +958,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
   }
   const float xv = s.vb[min(lane, NV - 1)], xu = s.ub[min(lane, NU - 1)];
-  if (lane < NV) gv_in[(size_t)w * NV + lane] = xv;
-  if (lane < NU) gctrl[(size_t)w * NU + lane] = xu;
+  if (lane < NV) gv_in[(size_t)wr * NV + lane] = xv;
+  if (lane < NU) gctrl[(size_t)wr * NU + lane] = xu;
   int nb = 0;  // with the counters: the non-finite bits of the gradients (k_diag_bwd's, from the values written)
   if (diag)
     nb = (ballot(nq) ? NONFINITE_QPOS : 0) | (ballot(!__builtin_isfinite(xv)) ? NONFINITE_QVEL : 0)
          | (ballot(!__builtin_isfinite(xu)) ? NONFINITE_CTRL : 0);
   if (lane == 0) {
     const int f = s.flags | nb << NONFINITE_SHIFT;
-    info[w] = f;
+    info[wr] = f;
     if (diag) {  // this world's part of the counters
       const int b = f >> NONFINITE_SHIFT;
       if (b & 7) atomicAdd(&diag[D_NONFINITE], 1ull);
@@ -972,7 +975,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       if (b & NONFINITE_CTRL) atomicAdd(&diag[D_NONFINITE_CTRL], 1ull);
       if (b & NONFINITE_COT) atomicAdd(&diag[D_NONFINITE_COT], 1ull);
       if (f & ADJ_REPLAY_MISMATCH) atomicAdd(&diag[D_REPLAY_MISMATCH], 1ull);
-      if (blockIdx.x == 0) {
+      if (wi == 0) {  // once per set of cotangents (a backward call each)
         atomicAdd(&diag[D_BWD_CALLS], 1ull);
         atomicAdd(&diag[D_BWD_ROWS], (unsigned long long)nw);
       }
@@ -990,7 +993,7 @@ int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* 
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, int order,
-                   unsigned long long* diag) {
+                   unsigned long long* diag, int ncot) {
   if (nw <= 0) return 0;
   if (reinterpret_cast<uintptr_t>(tape) & 15u) return (int)hipErrorInvalidValue;  // 16-byte copies of the factors
   const int* perm = nullptr;
@@ -1001,8 +1004,8 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
     }
     perm = (const int*)work;
   }
-  hipLaunchKernelGGL(k_adjoint, dim3(nw), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in,
-                     gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm, diag);
+  hipLaunchKernelGGL(k_adjoint, dim3(nw * ncot), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in,
+                     gv_in, gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm, diag, ncot);
   return (int)hipGetLastError();
 }
 size_t adjoint_lds_bytes() { return sizeof(Adj); }

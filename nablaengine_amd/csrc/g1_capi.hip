@@ -28,7 +28,7 @@ int launch_kinematics_vjp(hipStream_t st, int nw, const float* qpos, const float
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, int order,
-                   unsigned long long* diag);
+                   unsigned long long* diag, int ncot);
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
 }  // namespace g1k
 
@@ -176,7 +176,7 @@ int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const f
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
   return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
-                             clamp_soft, clamp_kv, normal, work, 1, nullptr);
+                             clamp_soft, clamp_kv, normal, work, 1, nullptr, 1);
 }
 
 int dk_adjoint_work_diag(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
@@ -187,7 +187,7 @@ int dk_adjoint_work_diag(hipStream_t st, int nw, int nsub, const float* tape, co
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
   return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
-                             clamp_soft, clamp_kv, normal, work, 1, d);
+                             clamp_soft, clamp_kv, normal, work, 1, d, 1);
 }
 
 int dk_adjoint_order(hipStream_t st, int nw, int nsub, const float* tape, void* work) {
@@ -204,7 +204,18 @@ int dk_adjoint_work_ordered(hipStream_t st, int nw, int nsub, const float* tape,
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
   return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
-                             clamp_soft, clamp_kv, normal, const_cast<void*>(work), 2, d);
+                             clamp_soft, clamp_kv, normal, const_cast<void*>(work), 2, d, 1);
+}
+
+int dk_adjoint_many(hipStream_t st, int nw, int ncot, int nsub, const float* tape, const float* fric, const float* com,
+                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
+                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, unsigned long long* d) {
+  if (nw < 0 || ncot < 1 || (long long)nw * ncot > 0x7fffffffLL || nsub < 1 || nsub > 32 || clamp_kv < 0 ||
+      clamp_kv > 2 || normal < 0 || normal > 3)
+    return (int)hipErrorInvalidValue;
+  if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
+  return g1k::launch_adjoint(st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in, gctrl, info, ctrl,
+                             clamp_soft, clamp_kv, normal, work, 1, d, ncot);
 }
 
 long long dk_adjoint_work_bytes(int nw) { return nw > 0 ? (long long)g1k::order_work_bytes(nw) : 0; }

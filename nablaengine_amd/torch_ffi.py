@@ -121,6 +121,8 @@ def load_library(path=None):
         lib.dk_adjoint_order.argtypes, lib.dk_adjoint_order.restype = [vp, i32, i32, vp, vp], i32
         lib.dk_adjoint_work_ordered.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
         lib.dk_adjoint_work_ordered.restype = i32
+        lib.dk_adjoint_many.argtypes = [vp, i32, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
+        lib.dk_adjoint_many.restype = i32
         lib.dk_adjoint_work_bytes.argtypes, lib.dk_adjoint_work_bytes.restype = [i32], ctypes.c_longlong
         lib.dk_fwd_kinematics.argtypes, lib.dk_fwd_kinematics.restype = [vp, i32] + [vp] * 8, i32
         lib.dk_torch_diag_fwd.argtypes, lib.dk_torch_diag_fwd.restype = [vp, vp, i32, i32, i32, vp, vp], i32
@@ -337,20 +339,31 @@ def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv
 
 def _vjps(tape, friction, com, g_qpos, g_qvel, ctrl=None, *, substeps=SUBSTEPS, clamp_kv=CLAMP_KV, normal=NORMAL,
           clamp_soft=None):
-    """K VJPs of one taped step: g_qpos (K, B, 36) and g_qvel (K, B, 35) output cotangents -> g_qpos_in (K, B, 36),
-    g_qvel_in (K, B, 35), g_ctrl (K, B, 29) and the last VJP's info (B,). Each k is backward(tape, ..., g_qpos[k],
-    g_qvel[k]) bitwise (the diagnostics count K backward calls), with the adjoint's dispatch order computed once for
-    all K (dk_adjoint_order, dk_adjoint_work_ordered): the step Jacobian's driver."""
+    """K VJPs of one taped step in one adjoint launch (dk_adjoint_many): g_qpos (K, B, 36) and g_qvel (K, B, 35)
+    output cotangents -> g_qpos_in (K, B, 36), g_qvel_in (K, B, 35), g_ctrl (K, B, 29) and info (K, B). Each k is
+    backward(tape, ..., g_qpos[k], g_qvel[k]) bitwise (the diagnostics count K backward calls), the worlds of every set
+    in one dispatch order: the step Jacobian's driver."""
     import torch
     K = g_qpos.shape[0] if isinstance(g_qpos, torch.Tensor) and g_qpos.dim() == 3 else 0
     if K < 1 or not isinstance(g_qvel, torch.Tensor) or g_qvel.dim() != 3 or g_qvel.shape[0] != K:
         raise _err("g_qpos (K, B, 36) and g_qvel (K, B, 35), K >= 1")
     dev, B = _backward_checks(tape, friction, com, g_qpos[0], g_qvel[0], ctrl, substeps, clamp_kv, normal)
+    _check("g_qpos", g_qpos, (K, B, NQ), dev)
+    _check("g_qvel", g_qvel, (K, B, NV), dev)
     kw = dict(dtype=torch.float32, device=tape.device)
     gq, gv, gu = (torch.empty((K, B, n), **kw) for n in (NQ, NV, NU))
-    info = torch.empty((B,), dtype=torch.int32, device=tape.device)
+    info = torch.empty((K, B), dtype=torch.int32, device=tape.device)
     if B == 0:
         return gq, gv, gu, info
+    lib = _STATE["lib"]
+    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
+    with _OnDevice(dev):
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        _rc(lib.dk_adjoint_many(st, B, K, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos),
+                                _ptr(g_qvel), _ptr(gq), _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl),
+                                ctypes.c_float(0.0 if clamp_soft is None else clamp_soft), int(clamp_kv), int(normal),
+                                _ptr(work), _ptr(_DIAG[dev]) if _DIAG_ON[0] else None), "the adjoint launch")
+    return gq, gv, gu, info
     lib = _STATE["lib"]
     work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
     soft = ctypes.c_float(0.0 if clamp_soft is None else clamp_soft)

@@ -196,3 +196,7 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
                                                                             0, work, None)
     assert ao(0) == 0 and ao(3) == 1  # the order is read from work
     assert ao(3, work=d, kv=2) == 1 and ao(3, work=d, tape=0x1004) == 1
+    lib.dk_adjoint_many.argtypes = [P, I, I, I] + [P] * 10 + [F, I, I, P, P]
+    am = lambda nw, k, kv=1, tape=None: lib.dk_adjoint_many(None, nw, k, 4, tape, *[None] * 9, 0.2, kv, 0, d, None)
+    assert am(0, 71) == 0 and am(-1, 71) == 1 and am(3, 0) == 1 and am(1 << 20, 1 << 12) == 1  # nw * ncot < 2^31
+    assert am(3, 71, kv=2) == 1 and am(3, 71, tape=0x1004) == 1
