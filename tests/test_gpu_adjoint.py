@@ -125,9 +125,9 @@ def test_adjoint_vs_oracle_config2(ffi):
         assert np.median(ef) <= TOL
 
 
-@pytest.mark.parametrize("substeps,iterations", [(1, 10), (2, 10), (7, 10), (2, 50)])
+@pytest.mark.parametrize("substeps,iterations", [(1, 10), (2, 10), (7, 10), (32, 10), (2, 50)])
 def test_adjoint_options_vs_oracle(ffi, substeps, iterations):
-    """The VJP of steps of 1, 2 and 7 substeps (the tape holds one record per substep; the adjoint runs them in
+    """The VJP of steps of 1, 2, 7 and 32 substeps (the tape holds one record per substep; the adjoint runs them in
     reverse), at the engine's 10 and at 50 Newton iterations, against the float64 oracle's analytic VJP at the same
     settings (exact mode, 256 config-1 worlds, cotangents N(0, 1)): per block (qpos tangent / qvel / ctrl) median
     relative error <= 1e-4 (the BASELINE gate), p99 <= 5x the p99 of the oracle's restatement evaluated in float32
