@@ -1,7 +1,8 @@
 """A world's results do not depend on the batch it is in (one world per wavefront; no arithmetic across worlds; the
 dispatch order only moves work in time): the forward's outputs, info and tape, and the adjoint's gradients, of any
 slice of a batch are bitwise those of the same worlds in the whole batch, at sizes that are not multiples of anything
-(1, 3, 63, 65, 1000, 2049), on config-1 and config-4 (contact-heavy) states. GPU."""
+(1, 3, 63, 65, 1000, 2049), on config-1 and config-4 (contact-heavy) states, and at config 4's full 16384 worlds.
+GPU."""
 import numpy as np
 import pytest
 
@@ -83,3 +84,24 @@ def test_nonfinite_worlds_leave_the_others_alone(ffi):
     assert np.isfinite(dirty[0][100]).all() and np.isfinite(dirty[1][100]).all()
     clamp = dirty[4][100].reshape(4, -1)[:, 2].view(np.uint32)  # each record's clamp mask (bit: dof)
     assert ((clamp >> (6 + 5)) & 1).all()
+
+
+def test_full_size_batch_is_bitwise_its_slices(ffi):
+    """At BASELINE config 4's size (16384 contact-heavy worlds, the largest batch the configs name): the forward's
+    outputs, info and tape and the adjoint's gradients of two 256-world slices taken from the whole batch (its start
+    and its end) are bitwise those of the same worlds run alone, and every world either stays finite or carries an
+    overflow flag."""
+    B = 16384
+    st = synthetic.states(B, config=4, seed=81)
+    cq, cv = synthetic.cotangents(B, seed=82)
+    x, tcq, tcv = _cat(st, cq, cv)
+    whole = _run(ffi, x, tcq, tcv)
+    names = ("qpos'", "qvel'", "warm'", "info", "tape", "g_qpos", "g_qvel", "g_ctrl", "backward info")
+    flagged = (whole[3][:, 3] & (4 | 16)) != 0
+    finite = np.isfinite(whole[1]).all(1) & np.isfinite(whole[0]).all(1) & np.isfinite(whole[5]).all(1)
+    assert (finite | flagged).all(), np.flatnonzero(~(finite | flagged))[:8]
+    for a, b in ((0, 256), (B - 256, B)):
+        part = _run(ffi, [t[a:b].contiguous() for t in x], tcq[a:b].contiguous(), tcv[a:b].contiguous())
+        for name, w, p in zip(names, whole, part):
+            assert np.array_equal(w[a:b].view(np.uint32) if w.dtype == np.float32 else w[a:b],
+                                  p.view(np.uint32) if p.dtype == np.float32 else p), (a, b, name)
