@@ -152,15 +152,19 @@ __global__ __launch_bounds__(256) void k_cost_adj(int nw, int nsub, const float*
   if (lane == 0) cost[w] = c < NBKT ? c : NBKT - 1;
 }
 
-// one workgroup of ORDER_THREADS: histogram of the costs, descending prefix, scatter (perm[slot] = world, heaviest
-// first). Each thread takes its worlds ORDER_LOADS at a time, every load issued before the first is used (one memory
-// round trip per batch, not per world).
+// one workgroup of ORDER_THREADS: histogram of the costs, descending prefix (a suffix scan on one wave), scatter
+// (perm[slot] = world, heaviest first). Each thread takes its worlds ORDER_LOADS at a time, every load issued before
+// the first is used (one memory round trip per batch, not per world).
 constexpr int ORDER_THREADS = 1024, ORDER_LOADS = 8;
 __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __restrict__ cost, int* __restrict__ perm) {
+  static_assert(NBKT == 128, "the bucket prefix: two buckets per lane of one wave");
   __shared__ int cnt[NBKT], cur[NBKT];
   const int t = threadIdx.x;
   if (t < NBKT) cnt[t] = 0;
   __syncthreads();
+  // the costs of this thread's worlds (the first ORDER_LOADS kept in registers for the scatter: all of them up to
+  // ORDER_LOADS x ORDER_THREADS worlds)
+  int c0[ORDER_LOADS];
   for (int w0 = t; w0 < nw; w0 += ORDER_LOADS * ORDER_THREADS) {
     int c[ORDER_LOADS];
 #pragma unroll
@@ -169,13 +173,25 @@ __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __re
       c[u] = w < nw ? cost[w] : -1;
     }
 #pragma unroll
-    for (int u = 0; u < ORDER_LOADS; u++)
+    for (int u = 0; u < ORDER_LOADS; u++) {
       if (c[u] >= 0) atomicAdd(&cnt[c[u]], 1);
+      if (w0 == t) c0[u] = c[u];
+    }
   }
   __syncthreads();
-  if (t == 0) {
-    int acc = 0;
-    for (int b = NBKT - 1; b >= 0; b--) { cur[b] = acc; acc += cnt[b]; }
+  // descending exclusive prefix: cur[b] = the worlds in buckets above b. Lane l of the first wave takes buckets 2l
+  // and 2l + 1; a suffix scan of their sums over the lanes (6 shuffle steps)
+  if (t < 64) {
+    const int lo = cnt[2 * t], hi = cnt[2 * t + 1], sum = lo + hi;
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_down(incl, o, 64);
+      if (t + o < 64) incl += v;
+    }
+    const int above = incl - sum;
+    cur[2 * t + 1] = above;
+    cur[2 * t] = above + hi;
   }
   __syncthreads();
   for (int w0 = t; w0 < nw; w0 += ORDER_LOADS * ORDER_THREADS) {
@@ -183,7 +199,7 @@ __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __re
 #pragma unroll
     for (int u = 0; u < ORDER_LOADS; u++) {
       const int w = w0 + u * ORDER_THREADS;
-      c[u] = w < nw ? cost[w] : -1;
+      c[u] = w0 == t ? c0[u] : (w < nw ? cost[w] : -1);
     }
 #pragma unroll
     for (int u = 0; u < ORDER_LOADS; u++)
