@@ -525,9 +525,8 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     float phi[3], t[3] = {s.qb[3], s.qb[4], s.qb[5]};
     for (int k = 0; k < 3; k++) phi[k] = kH * (s.qvel[3 + k] + kH * s.aadv[3 + k]);
     const float th = sqrtf(dot3(phi, phi));
-    float dq[4] = {1.f, 0.f, 0.f, 0.f};
+    float dq[4] = {1.f, 0.f, 0.f, 0.f}, sn = 0.f, cs = 1.f;
     if (th > 0.f) {
-      float sn, cs;
       sincosf(0.5f * th, &sn, &cs);
       const float st = sn / th;
       dq[0] = cs; dq[1] = st * phi[0]; dq[2] = st * phi[1]; dq[3] = st * phi[2];
@@ -535,13 +534,14 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     float rt[3];
     qrot(dq, t, rt);  // t = R(dq) t'
     for (int k = 0; k < 3; k++) s.qn[3 + k] = rt[k];
-    // J_r(phi)' t' = t' + c1 phi x t' + c2 phi x (phi x t')
+    // J_r(phi)' t' = t' + c1 phi x t' + c2 phi x (phi x t'), c1 = (1 - cos th) / th^2, c2 = (th - sin th) / th^3, with
+    // cos th and sin th from the half angle's sine and cosine above (1 - cos th = 2 sin^2(th / 2): no cancellation)
     float c1, c2;
     if (th < 1e-2f) { c1 = 0.5f - th * th / 24.f; c2 = 1.f / 6.f - th * th / 120.f; }
     else {
       const float i2 = 1.f / (th * th);
-      c1 = (1.f - cosf(th)) * i2;
-      c2 = (th - sinf(th)) * i2 / th;
+      c1 = 2.f * sn * sn * i2;
+      c2 = (th - 2.f * sn * cs) * i2 / th;
     }
     float pt[3], ppt[3];
     cross(phi, t, pt);
