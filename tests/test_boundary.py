@@ -200,3 +200,30 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     am = lambda nw, k, kv=1, tape=None: lib.dk_adjoint_many(None, nw, k, 4, tape, *[None] * 9, 0.2, kv, 0, d, None)
     assert am(0, 71) == 0 and am(-1, 71) == 1 and am(3, 0) == 1 and am(1 << 20, 1 << 12) == 1  # nw * ncot < 2^31
     assert am(3, 71, kv=2) == 1 and am(3, 71, tape=0x1004) == 1
+
+
+def test_device_counter_layout_matches_the_python_names():
+    """The counters' device layout (csrc/g1_diag.h: the enum the kernels index, the non-finite bits and shift, the
+    replay-mismatch bit) is the order and the values torch_ffi reads them with (the reference's, torch_ffi.py:56-61):
+    a counter added to the wrong slot would otherwise only show as a wrong name in read_diagnostics()."""
+    from nablaengine_amd import torch_ffi
+    h = open(os.path.join(ROOT, "nablaengine_amd", "csrc", "g1_diag.h")).read()
+    body = re.search(r"enum \{([^}]*)\}", h).group(1)
+    names = [n.strip().split("=")[0].strip() for n in body.split(",") if n.strip()]
+    assert names[-1] == "NDIAG" and len(names) - 1 == len(torch_ffi.DIAG)
+    conv = {"D_FWD_CALLS": "fwd_calls", "D_FWD_WORLDS": "fwd_worlds", "D_FWD_UNSUPPORTED": "fwd_unsupported_worlds",
+            "D_FWD_ITER_LIMIT": "fwd_iteration_limit_worlds", "D_TAPE_RECORDS": "tape_records",
+            "D_REFACT": "refact_records", "D_NONCONV": "nonconv_records", "D_SINGULAR": "singular_records",
+            "D_BWD_CALLS": "bwd_calls", "D_BWD_ROWS": "bwd_rows", "D_NONFINITE": "nonfinite_rows",
+            "D_NONFINITE_QPOS": "nonfinite_qpos_rows", "D_NONFINITE_QVEL": "nonfinite_qvel_rows",
+            "D_NONFINITE_CTRL": "nonfinite_ctrl_rows", "D_NONFINITE_COT": "nonfinite_cotangent_rows",
+            "D_REPLAY_MISMATCH": "replay_mismatch_worlds", "D_CONTACT_OVERFLOW": "fwd_contact_overflow_worlds",
+            "D_ROW_OVERFLOW": "fwd_row_overflow_worlds"}
+    assert [conv[n] for n in names[:-1]] == list(torch_ffi.DIAG)
+    def val(n):  # an integer literal or "a << b"
+        a, _, b = re.search(rf"\b{n} = ([^,;]+)[,;]", h).group(1).partition("<<")
+        return int(a) << int(b) if b else int(a)
+    assert (val("NONFINITE_QPOS"), val("NONFINITE_QVEL"), val("NONFINITE_CTRL"), val("NONFINITE_COT")) == \
+        (torch_ffi.NONFINITE_QPOS, torch_ffi.NONFINITE_QVEL, torch_ffi.NONFINITE_CTRL, torch_ffi.NONFINITE_COT)
+    assert val("NONFINITE_SHIFT") == torch_ffi.NONFINITE_SHIFT
+    assert val("ADJ_REPLAY_MISMATCH") == torch_ffi.ADJ_REPLAY_MISMATCH
