@@ -32,17 +32,20 @@ def qpos_tangent(qpos, g):
 
 def jacobian(qpos, qvel, warm, ctrl, friction, com, *, iterations=torch_ffi.ITERATIONS, substeps=torch_ffi.SUBSTEPS,
              clamp_kv=torch_ffi.CLAMP_KV, normal=torch_ffi.NORMAL, clamp_soft=None):
-    """The step Jacobian of every world (B, 71, 99) float32 and the forward's info."""
+    """The step Jacobian of every world (B, 71, 99) float32 and the forward's info. The options are backward()'s
+    (clamp_soft None: CLAMP_SOFT for the soft clamp), checked before anything is launched; each row is bitwise the VJP
+    backward() gives for its output's one-hot cotangent."""
     import torch
+    kv, nrm = torch_ffi._variant(clamp_kv, normal)
+    torch_ffi._soft_delta(kv, clamp_soft)
     q1, v1, w1, info, tape = torch_ffi.forward(qpos, qvel, warm, ctrl, friction, com, iterations=iterations,
                                                substeps=substeps, tape=True)
     B = qpos.shape[0]
     eye = torch.eye(NOUT, dtype=torch.float32, device=qpos.device)  # output r's one-hot cotangent, every world
     cq = eye[:, :torch_ffi.NQ].unsqueeze(1).expand(NOUT, B, torch_ffi.NQ).contiguous()
     cv = eye[:, torch_ffi.NQ:].unsqueeze(1).expand(NOUT, B, torch_ffi.NV).contiguous()
-    soft_ctrl = ctrl if int(clamp_kv) == 2 else None
-    gq, gv, gu, _ = torch_ffi._vjps(tape, friction, com, cq, cv, soft_ctrl, substeps=substeps, clamp_kv=clamp_kv,
-                                    normal=normal, clamp_soft=clamp_soft)
+    gq, gv, gu, _ = torch_ffi._vjp_sets(tape, friction, com, cq, cv, ctrl if kv == 2 else None, substeps=substeps,
+                                        clamp_kv=kv, normal=nrm, clamp_soft=clamp_soft)
     J = torch.cat([qpos_tangent(qpos, gq), gv, gu], dim=2)  # (71, B, 99)
     return J.transpose(0, 1).contiguous(), info
 

@@ -1,5 +1,5 @@
-"""PyTorch interface of the MI355X G1 engine, on torch's current HIP stream (a drop-in for the reference's
-``nablaengine.torch_ffi``, ``src/nablaengine/torch_ffi.py``).
+"""PyTorch surface of the MI355X G1 engine: a drop-in for the reference's ``nablaengine.torch_ffi``
+(``src/nablaengine/torch_ffi.py``; the entry points, their arguments, defaults and error classes are that module's).
 
   step(qpos, qvel, warm, ctrl, friction, com, *, iterations=10, substeps=4, clamp_kv=0, normal=3, clamp_soft=None,
        grad_decay=1.0, kinematics=False) -> (qpos', qvel', warm'[, qpos_n, xpos, xquat, cvel, subtree_com])
@@ -8,735 +8,684 @@
        -> (qpos', qvel', warm', info[, tape][, the kinematics outputs])
   backward(tape, friction, com, g_qpos, g_qvel, *, substeps=4, clamp_kv=0, normal=3, ctrl=None, clamp_soft=None,
            kinematics=None) -> (g_qpos, g_qvel, g_ctrl, info)
+  scale_grad(tree, gamma)
 
-The kinematics outputs (reference g1_engine/kinematics.py:1-45, MJX kinematics + com_pos + com_vel) of a state:
-qpos_n (B, 36) qpos with the root quaternion normalized, xpos (B, 31, 3), xquat (B, 31, 4) the body frames, cvel
-(B, 31, 6) [angular; linear] twists at subtree_com[:, 1], subtree_com (B, 31, 3). step(..., kinematics=True) gives
-those of its output state, bitwise kinematics(qpos', qvel', com); their cotangents join the step's in its backward.
+Per-world arrays are float32, contiguous, on one ROCm device, with the worlds B as the leading dimension: qpos (B, 36),
+qvel (B, 35), warm (B, 35), ctrl (B, 29), friction (B,), com (B, 3). Anything else is a TypeError: no array is cast,
+copied or moved to another device. Bad options are a ValueError, a failed library call a RuntimeError. B = 0 gives
+empty outputs and launches nothing.
 
-Arguments: float32 tensors on one ROCm device, contiguous, leading dimension B (the worlds): qpos (B, 36), qvel (B, 35),
-warm (B, 35), ctrl (B, 29), friction (B,), com (B, 3). Other dtypes, devices or shapes raise TypeError; nothing is
-cast or copied implicitly (reference torch_ffi.py:419-428 _check). Bad options raise ValueError (torch_ffi.py:824-829),
-a failed library call RuntimeError (torch_ffi.py:431-433 _rc). B = 0 returns empty outputs without a launch.
+The kinematics outputs of a state (the reference's g1_engine/kinematics.py:1-45): qpos_n (B, 36), the root
+quaternion normalized; xpos (B, 31, 3) and xquat (B, 31, 4), the body frames; cvel (B, 31, 6), [angular; linear]
+twists at subtree_com[:, 1]; subtree_com (B, 31, 3). step(..., kinematics=True) returns those of its output state,
+bitwise kinematics(qpos', qvel', com), and its backward pulls their cotangents back onto (qpos', qvel') first.
 
-The library is libnablaengine_g1.so next to this file (built in-tree by ``python -m nablaengine_amd.build``), loaded
-with ctypes; every call goes to its C entries (include/nablaengine_g1.h) with torch's current stream and the tensors'
-device pointers, the inputs' device made current. There is no fallback: without the library, or without a GPU, the
-calls raise. After init() the calls only launch kernels and allocate through torch's caching allocator (no host
-synchronization), so they can be captured in a HIP graph with fixed shapes. While torch.compile traces, the library
-calls are the torch.library custom ops nablaengine::forward, ::backward, ::kinematics and ::kinematics_backward with
-fake implementations (opaque nodes, no graph break with fullgraph=True; reference torch_ffi.py:583-655); in eager mode
-the same functions are called directly.
+How a call reaches the GPU. The library, libnablaengine_g1.so next to this file (``python -m nablaengine_amd.build``),
+is loaded once per process with ctypes; its C entries (include/nablaengine_g1.h) get the tensors' device pointers and
+torch's current stream of the inputs' device, made current for the call. Each library call is an operator of the
+``nablaengine`` namespace (forward, backward, kinematics, kinematics_backward), defined by schema with the dispatcher
+and given a fake (shape-only) implementation, so that torch.compile records it as one opaque node; eager calls go
+through the same operators. There is no fallback: without the library or without a GPU every call raises. After
+init() a call only launches kernels and takes memory from torch's caching allocator, so it may be captured in a HIP
+graph.
 
-Diagnostics (reference torch_ffi.py:56-62, 664-742): per device 18 int64 counters (DIAG) added to on the device by the
-forward and adjoint kernels, each world at its end (set_diagnostics(False) skips it; the reference runs a small kernel
-after each call, which the library also exports: dk_torch_diag_fwd / _bwd), read with diagnostics() (the tensor)
-or read_diagnostics() (a dict; resets). The backward's info then also carries the non-finite bits (NONFINITE_* <<
-NONFINITE_SHIFT) besides the union of the records' flags and ADJ_REPLAY_MISMATCH. set_overflow_warnings(True) warns
-when worlds exceeded the contact or row capacity.
+Autograd: step is differentiable in qpos, qvel and ctrl when one of the six inputs requires grad; the forward then
+also writes the tape (B, substeps x 1472 float32) and keeps it for the backward, the analytic adjoint. warm' is not
+differentiable; warm, friction and com get no gradient. grad_decay scales the state's cotangent through the step (a
+float32 product), not ctrl's.
+
+Diagnostics: per device an int64 tensor of the 18 counters of DIAG, added to by the forward and adjoint kernels
+themselves as each world ends (set_diagnostics(False) stops it); diagnostics() returns the tensor, read_diagnostics()
+a dict (synchronizing; by default it zeroes them). With counting on, the backward's info also carries the non-finite
+bits (NONFINITE_* << NONFINITE_SHIFT).
 """
 import atexit
 import ctypes
 import math
 import os
 import threading
+import warnings
+from typing import NamedTuple, Optional
 
-ITERATIONS, SUBSTEPS, CLAMP_KV, NORMAL = 10, 4, 0, 3  # reference torch_ffi.py:54
-CLAMP_SOFT, GRAD_DECAY = 0.2, 1.0  # reference torch_ffi.py:55
+import torch
+from torch import Tensor
+
+# ---- the interface's constants (names and values the reference's, torch_ffi.py:54-61) -------------------------------
+ITERATIONS, SUBSTEPS, CLAMP_KV, NORMAL = 10, 4, 0, 3
+CLAMP_SOFT, GRAD_DECAY = 0.2, 1.0
 NQ, NV, NU, NBODY = 36, 35, 29, 31
-MAXCON = 64
-OVERFLOW_CONTACTS, OVERFLOW_ROWS = 4, 16  # forward info[:, 3] bits (reference torch_ffi.py:60)
-# the diagnostic counters, in the reference's order (torch_ffi.py:56-59); backward info's non-finite bits (61)
+MAXCON, MAXROWS = 64, 192
+OVERFLOW_CONTACTS, OVERFLOW_ROWS = 4, 16  # forward info[:, 3]: contacts / rows beyond capacity were dropped
 DIAG = ("fwd_calls", "fwd_worlds", "fwd_unsupported_worlds", "fwd_iteration_limit_worlds", "tape_records",
         "refact_records", "nonconv_records", "singular_records", "bwd_calls", "bwd_rows", "nonfinite_rows",
         "nonfinite_qpos_rows", "nonfinite_qvel_rows", "nonfinite_ctrl_rows", "nonfinite_cotangent_rows",
         "replay_mismatch_worlds", "fwd_contact_overflow_worlds", "fwd_row_overflow_worlds")
 NONFINITE_QPOS, NONFINITE_QVEL, NONFINITE_CTRL, NONFINITE_COT, NONFINITE_SHIFT = 1, 2, 4, 8, 16
-ADJ_REPLAY_MISMATCH = 1 << 13  # backward info: a replayed contact was not found
-TAPE_REFACT, TAPE_NONCONV, TAPE_SINGULAR = 1 << 8, 1 << 9, 1 << 10  # the records' flags (also in backward info)
-VARIANTS = tuple((kv, n) for kv in (0, 1, 2) for n in (0, 1, 2, 3))  # adjoint variants (clamp_kv, normal)
+ADJ_REPLAY_MISMATCH = 1 << 13  # backward info: a replayed contact was not found among the recomputed ones
+TAPE_REFACT, TAPE_NONCONV, TAPE_SINGULAR = 1 << 8, 1 << 9, 1 << 10  # a tape record's flags (also in backward info)
+VARIANTS = tuple((kv, n) for kv in (0, 1, 2) for n in (0, 1, 2, 3))  # the adjoint's (clamp_kv, normal) options
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libnablaengine_g1.so")
-ARCH = "gfx950"  # the one architecture the library is built for
+ARCH = "gfx950"  # the library's one target
 
-_LOCK = threading.RLock()
-_STATE = {}
-_READY = set()
-_DIAG = {}  # device index -> int64 (len(DIAG),) counters on that device
-_DIAG_ON = [True]  # set_diagnostics
-_OVERFLOW_WARN = [os.environ.get("DK_OVERFLOW_WARN", "0") not in ("", "0")]  # set_overflow_warnings
+# the per-world part of each array's shape
+_KIN_OUT = (("qpos_n", (NQ,)), ("xpos", (NBODY, 3)), ("xquat", (NBODY, 4)), ("cvel", (NBODY, 6)),
+            ("subtree_com", (NBODY, 3)))
+_STATE_IN = (("qpos", (NQ,)), ("qvel", (NV,)), ("warm", (NV,)), ("ctrl", (NU,)), ("friction", ()), ("com", (3,)))
 
 
-def _err(msg, exc=TypeError):
-    return exc(f"nablaengine_amd.torch_ffi: {msg}")
+def _err(msg, kind=TypeError):
+    return kind(f"nablaengine_amd.torch_ffi: {msg}")
 
 
-def _library_path(artifact):
-    """The library an artifact names: a .so path, or a JSON file whose "library" key names it (relative to the JSON
-    file), as the reference's artifacts (torch_ffi.py:241-266); None: $DK_TORCH_ARTIFACT, $NABLA_G1_LIB, else the
-    in-tree build."""
-    a = artifact or os.environ.get("DK_TORCH_ARTIFACT") or os.environ.get("NABLA_G1_LIB") or LIB_PATH
-    a = os.fspath(a)
-    if a.endswith(".json"):
-        import json
-        with open(a) as f:
-            meta = json.load(f)
-        if "library" not in meta:
-            raise _err(f"artifact {a} names no library", RuntimeError)
-        return os.path.join(os.path.dirname(os.path.abspath(a)), meta["library"])
-    return a
+# ---- the native library ---------------------------------------------------------------------------------------------
+# C prototypes, "result:arguments", one letter a value: p pointer (device array, stream or NULL), i int, f float,
+# q long long, - void.
+_PROTOTYPES = {
+    "dk_fwd_forward": "i:pi" + "p" * 6 + "ii" + "p" * 7,
+    "dk_fwd_forward_diag": "i:pi" + "p" * 6 + "ii" + "p" * 8,
+    "dk_fwd_forward_ordered": "i:pi" + "p" * 6 + "ii" + "p" * 7,
+    "dk_fwd_forward_static": "i:pi" + "p" * 6 + "ii" + "p" * 6,
+    "dk_fwd_order": "i:pipp",
+    "dk_fwd_work_bytes": "q:i",
+    "dk_fwd_upload": "i:pp",
+    "dk_fwd_sizes": "-:p",
+    "dk_fwd_launch": "i:ip",
+    "dk_fwd_kinematics": "i:pi" + "p" * 8,
+    "dk_fwd_kinematics_vjp": "i:pi" + "p" * 12,
+    "dk_adjoint": "i:pii" + "p" * 10 + "fii",
+    "dk_adjoint_work": "i:pii" + "p" * 10 + "fiip",
+    "dk_adjoint_work_diag": "i:pii" + "p" * 10 + "fiipp",
+    "dk_adjoint_order": "i:piipp",
+    "dk_adjoint_work_ordered": "i:pii" + "p" * 10 + "fiipp",
+    "dk_adjoint_many": "i:piii" + "p" * 10 + "fiipp",
+    "dk_adjoint_work_bytes": "q:i",
+    "dk_torch_diag_fwd": "i:ppiiipp",
+    "dk_torch_diag_bwd": "i:ppi" + "p" * 6,
+    "dk_prof_read": "i:pi",
+    "dk_prof_read_adj": "i:pi",
+}
+_CTYPE = {"p": ctypes.c_void_p, "i": ctypes.c_int, "f": ctypes.c_float, "q": ctypes.c_longlong, "-": None}
+
+
+class _Native:
+    """The loaded library: its path, the ctypes handle with every entry's prototype set, and the sizes it reports
+    (dk_fwd_sizes: LDS bytes of the forward and the adjoint, tape words per world and substep, nq, nv, contacts)."""
+
+    def __init__(self, path):
+        self.path = path
+        self.dll = ctypes.CDLL(path)
+        for name, proto in _PROTOTYPES.items():
+            result, args = proto.split(":")
+            entry = getattr(self.dll, name)
+            entry.restype = _CTYPE[result]
+            entry.argtypes = [_CTYPE[c] for c in args]
+        sizes = (ctypes.c_longlong * 9)()
+        self.dll.dk_fwd_sizes(ctypes.cast(sizes, ctypes.c_void_p))
+        self.sizes = tuple(int(s) for s in sizes)
+        self.rec_words = self.sizes[2]
+
+    def run(self, what, entry, *args):
+        """Call a C entry; a nonzero return is a RuntimeError naming `what`."""
+        rc = getattr(self.dll, entry)(*args)
+        if rc:
+            raise _err(f"{what} failed (HIP error {rc})", RuntimeError)
+
+
+_lock = threading.RLock()
+_native: Optional[_Native] = None
+_counters = {}  # device index -> int64 (len(DIAG),) tensor; a device is ready once it has one
+_settings = {"count": True, "warn": os.environ.get("DK_OVERFLOW_WARN", "0") not in ("", "0")}
+
+
+def library_path(artifact=None):
+    """The library a call of init / load_library loads: artifact (a .so, or a .json file whose "library" names it
+    relative to the .json, as the reference's artifacts, torch_ffi.py:241-266), else $DK_TORCH_ARTIFACT, else
+    $NABLA_G1_LIB, else the in-tree build."""
+    path = os.fspath(artifact or os.environ.get("DK_TORCH_ARTIFACT") or os.environ.get("NABLA_G1_LIB") or LIB_PATH)
+    if not path.endswith(".json"):
+        return path
+    import json
+    with open(path) as f:
+        lib = json.load(f).get("library")
+    if lib is None:
+        raise _err(f"artifact {path} names no library", RuntimeError)
+    return os.path.join(os.path.dirname(os.path.abspath(path)), lib)
+
+
+def _load(artifact=None):
+    global _native
+    with _lock:
+        if _native is None:
+            path = library_path(artifact)
+            if not os.path.exists(path):
+                raise _err(f"{path} is missing: build it with `python -m nablaengine_amd.build`", RuntimeError)
+            _native = _Native(path)
+        elif artifact is not None and os.path.realpath(library_path(artifact)) != os.path.realpath(_native.path):
+            raise _err(f"{_native.path} is loaded already: one library per process", RuntimeError)
+        return _native
 
 
 def load_library(path=None):
-    """ctypes handle of the library with the C entries' argument types set (path: as init's artifact); raises
-    RuntimeError when it is missing (build it with `python -m nablaengine_amd.build`), or when another library is
-    loaded already (one library per process)."""
-    with _LOCK:
-        if "lib" in _STATE:
-            if path is not None and os.path.realpath(_library_path(path)) != os.path.realpath(_STATE["path"]):
-                raise _err(f"{_STATE['path']} is loaded: one library per process", RuntimeError)
-            return _STATE["lib"]
-        p = _library_path(path)
-        if not os.path.exists(p):
-            raise _err(f"{p} is missing: build it with `python -m nablaengine_amd.build`", RuntimeError)
-        lib = ctypes.CDLL(p)
-        vp, i32, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
-        lib.dk_fwd_forward.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 7
-        lib.dk_fwd_forward.restype = i32
-        lib.dk_fwd_forward_diag.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 8
-        lib.dk_fwd_forward_diag.restype = i32
-        lib.dk_fwd_forward_ordered.argtypes = [vp, i32] + [vp] * 6 + [i32, i32] + [vp] * 7
-        lib.dk_fwd_forward_ordered.restype = i32
-        lib.dk_fwd_order.argtypes, lib.dk_fwd_order.restype = [vp, i32, vp, vp], i32
-        lib.dk_fwd_work_bytes.argtypes, lib.dk_fwd_work_bytes.restype = [i32], ctypes.c_longlong
-        lib.dk_fwd_upload.argtypes, lib.dk_fwd_upload.restype = [vp, vp], i32
-        lib.dk_fwd_sizes.argtypes, lib.dk_fwd_sizes.restype = [vp], None
-        lib.dk_adjoint.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32]
-        lib.dk_adjoint.restype = i32
-        lib.dk_adjoint_work.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp]
-        lib.dk_adjoint_work.restype = i32
-        lib.dk_adjoint_work_diag.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
-        lib.dk_adjoint_work_diag.restype = i32
-        lib.dk_adjoint_order.argtypes, lib.dk_adjoint_order.restype = [vp, i32, i32, vp, vp], i32
-        lib.dk_adjoint_work_ordered.argtypes = [vp, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
-        lib.dk_adjoint_work_ordered.restype = i32
-        lib.dk_adjoint_many.argtypes = [vp, i32, i32, i32] + [vp] * 10 + [f32, i32, i32, vp, vp]
-        lib.dk_adjoint_many.restype = i32
-        lib.dk_adjoint_work_bytes.argtypes, lib.dk_adjoint_work_bytes.restype = [i32], ctypes.c_longlong
-        lib.dk_fwd_kinematics.argtypes, lib.dk_fwd_kinematics.restype = [vp, i32] + [vp] * 8, i32
-        lib.dk_torch_diag_fwd.argtypes, lib.dk_torch_diag_fwd.restype = [vp, vp, i32, i32, i32, vp, vp], i32
-        lib.dk_torch_diag_bwd.argtypes, lib.dk_torch_diag_bwd.restype = [vp, vp, i32] + [vp] * 6, i32
-        lib.dk_fwd_kinematics_vjp.argtypes, lib.dk_fwd_kinematics_vjp.restype = [vp, i32] + [vp] * 12, i32
-        sizes = (ctypes.c_longlong * 9)()
-        lib.dk_fwd_sizes(ctypes.cast(sizes, vp))
-        _STATE["sizes"] = [int(x) for x in sizes]
-        _STATE["path"] = p
-        _STATE["lib"] = lib
-        return lib
+    """The ctypes handle of the library, every C entry's prototype set (path: as init's artifact). RuntimeError when
+    the file is missing or another library is loaded already (one library per process)."""
+    return _load(path).dll
 
 
 def rec_words():
     """Tape words per world and substep."""
-    load_library()
-    return _STATE["sizes"][2]
-
-
-def init(device=None, artifact=None, model_dir=None, model=None, foot_pairs=None):
-    """Load the library and check that `device` (default: torch's current device) can run it; idempotent per device,
-    one library per process (reference torch_ffi.py:268-290). artifact: the library (a .so, or a JSON artifact naming
-    it); default $DK_TORCH_ARTIFACT, else the in-tree build. The G1 model is compiled into the library, so nothing is
-    uploaded and nothing synchronizes; another model (model_dir / model / foot_pairs) is a ValueError. Returns the
-    library's path, architecture and sizes."""
-    import torch
-    if model_dir is not None or model is not None or foot_pairs is not None:
-        raise _err("the G1 model is compiled into this library: model_dir / model / foot_pairs are not supported",
-                   ValueError)
-    with _LOCK:
-        lib = load_library(artifact)
-        if not torch.cuda.is_available():
-            raise _err("no ROCm GPU visible: the engine runs on the GPU only", RuntimeError)
-        dev = torch.cuda.current_device() if device is None else torch.device(device).index
-        dev = torch.cuda.current_device() if dev is None else dev
-        if dev not in _READY:
-            arch = getattr(torch.cuda.get_device_properties(dev), "gcnArchName", ARCH).split(":")[0]
-            if arch != ARCH:
-                raise _err(f"cuda:{dev} is {arch}, the library is built for {ARCH} (one architecture per process)",
-                           RuntimeError)
-            with torch.cuda.device(dev):
-                rc = lib.dk_fwd_upload(None, ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
-            if rc:
-                raise _err(f"device cuda:{dev} cannot run the kernels (code {rc})", RuntimeError)
-            _DIAG[dev] = torch.zeros(len(DIAG), dtype=torch.int64, device=f"cuda:{dev}")
-            _READY.add(dev)
-        _custom_ops()  # defined here, outside any torch.compile trace (a definition inside one is not traceable),
-        _fn("step", _make_step_fn)  # as the autograd functions
-        _fn("kin", _make_kin_fn)
-        return dict(path=_STATE["path"], arch=ARCH, sizes=list(_STATE["sizes"]))
+    return _load().rec_words
 
 
 def tape_bytes(nworld, substeps=SUBSTEPS, steps=1):
-    """Bytes of the tapes of `steps` differentiated control steps (reference torch_ffi.py:454-458)."""
+    """Bytes of the tapes that `steps` differentiated control steps of `nworld` worlds keep."""
     return 4 * rec_words() * substeps * nworld * steps
 
 
-def _ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
-
-
-def _check(name, x, shape, dev, dtype=None):
-    import torch
-    dtype = dtype or torch.float32
-    if not isinstance(x, torch.Tensor):
-        raise _err(f"{name} must be a torch.Tensor, got {type(x).__name__}")
-    if x.dtype != dtype or tuple(x.shape) != tuple(shape) or x.device.type != "cuda" or not x.is_contiguous():
-        raise _err(f"{name} must be a contiguous {dtype} GPU tensor {tuple(shape)}, got {x.dtype} {tuple(x.shape)} on "
-                   f"{x.device}{'' if x.is_contiguous() else ' (not contiguous)'}")
-    if dev is not None and x.device.index != dev:
-        raise _err(f"{name} is on {x.device}, the other tensors on cuda:{dev}")
-
-
-def _rc(rc, what):
-    if rc:
-        raise _err(f"{what} failed (HIP error {rc})", RuntimeError)
-
-
-def _soft(clamp_kv, clamp_soft):
-    """The soft clamp's delta for clamp_kv 2 (None: CLAMP_SOFT); None for 0 / 1 (reference torch_ffi.py:436-449)."""
-    if int(clamp_kv) != 2:
-        if clamp_soft is not None:
-            raise _err(f"clamp_soft is the soft clamp's (clamp_kv=2), not clamp_kv={clamp_kv}", ValueError)
-        return None
-    d = float(CLAMP_SOFT if clamp_soft is None else clamp_soft)
-    if not (math.isfinite(d) and d >= 0.0):
-        raise _err(f"clamp_soft must be finite and >= 0, got {clamp_soft}", ValueError)
-    return d
-
-
-class _OnDevice:
-    def __init__(self, dev):
-        self.dev = dev
-
-    def __enter__(self):
-        import torch
-        self.prev = torch.cuda.current_device()
-        if self.prev != self.dev:
-            torch.cuda.set_device(self.dev)
-
-    def __exit__(self, *a):
-        import torch
-        if self.prev != self.dev:
-            torch.cuda.set_device(self.prev)
-
-
-def _kin_shapes(B):
-    return (B, NQ), (B, NBODY, 3), (B, NBODY, 4), (B, NBODY, 6), (B, NBODY, 3)
-
-
-def _kin_empty(B, device):
-    import torch
-    return [torch.empty(s, dtype=torch.float32, device=device) for s in _kin_shapes(B)]
-
-
-def _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics=False):
-    import torch
-    if not isinstance(qpos, torch.Tensor):
-        raise _err(f"qpos must be a torch.Tensor, got {type(qpos).__name__}")
-    if qpos.device.type != "cuda":
-        raise _err(f"qpos must be a GPU tensor, got {qpos.device}")
-    dev = qpos.device.index
-    B = qpos.shape[0] if qpos.dim() == 2 else -1
-    for name, x, shape in (("qpos", qpos, (B, NQ)), ("qvel", qvel, (B, NV)), ("warm", warm, (B, NV)),
-                           ("ctrl", ctrl, (B, NU)), ("friction", friction, (B,)), ("com", com, (B, 3))):
-        _check(name, x, shape, dev)
-    if substeps < 1 or substeps > 32 or iterations < 0:
-        raise _err("substeps in 1..32 and iterations >= 0", ValueError)
-    if dev not in _READY:
-        init(dev)
-    lib = _STATE["lib"]
-    kw = dict(dtype=torch.float32, device=qpos.device)
-    q1, v1, w1 = torch.empty((B, NQ), **kw), torch.empty((B, NV), **kw), torch.empty((B, NV), **kw)
-    info = torch.empty((B, 4), dtype=torch.int32, device=qpos.device)
-    rw = _STATE["sizes"][2]
-    tp = torch.empty((B if tape else 0, substeps * rw), **kw)
-    kin = _kin_empty(B, qpos.device) if kinematics else []
-    if B == 0:
-        return [q1, v1, w1, info, tp] + kin
-    work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device=qpos.device)
-    with _OnDevice(dev):
-        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        args = (st, B, *map(_ptr, (qpos, qvel, warm, ctrl, friction, com)), int(iterations), int(substeps),
-                _ptr(q1), _ptr(v1), _ptr(w1), _ptr(info), None, _ptr(tp) if tape else None,
-                _ptr(work) if work.numel() else None)
-        if _DIAG_ON[0]:  # the counters added to by the forward kernel itself (dk_torch_diag_fwd's counts)
-            _rc(lib.dk_fwd_forward_diag(*args, _ptr(_DIAG[dev])), "the forward launch")
-        else:
-            _rc(lib.dk_fwd_forward(*args), "the forward launch")
-        if kinematics:  # the output state's kinematics (reference torch_ffi.py:488-489)
-            _rc(lib.dk_fwd_kinematics(st, B, _ptr(q1), _ptr(v1), _ptr(com), *map(_ptr, kin)), "the kinematics launch")
-    return [q1, v1, w1, info, tp] + kin
-
-
-def _backward_checks(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal):
-    """The backward's argument checks (TypeError / ValueError, reference torch_ffi.py:419-428); returns (device, B)."""
-    import torch
-    if not isinstance(tape, torch.Tensor) or tape.device.type != "cuda":
-        raise _err("tape must be a GPU torch.Tensor")
-    dev = tape.device.index
-    rw = rec_words()
-    B = tape.shape[0]
-    for name, x, shape in (("tape", tape, (B, substeps * rw)), ("friction", friction, (B,)), ("com", com, (B, 3)),
-                           ("g_qpos", g_qpos, (B, NQ)), ("g_qvel", g_qvel, (B, NV))):
-        _check(name, x, shape, dev)
-    v = (int(clamp_kv), int(normal))
-    if v not in VARIANTS:
-        raise _err(f"no adjoint variant clamp_kv={clamp_kv} normal={normal}", ValueError)
-    if (v[0] == 2) != (ctrl is not None):
-        raise _err("clamp_kv=2 (the soft clamp) needs the step's ctrl; 0 and 1 take none", ValueError)
-    if ctrl is not None:
-        _check("ctrl", ctrl, (B, NU), dev)
-    if dev not in _READY:
-        init(dev)
-    return dev, B
-
-
-def _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal, clamp_soft, kin_state=(),
-                   kin_cot=()):
-    import torch
-    dev, B = _backward_checks(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal)
-    v = (int(clamp_kv), int(normal))
-    kw = dict(dtype=torch.float32, device=tape.device)
-    gq, gv, gu = torch.empty((B, NQ), **kw), torch.empty((B, NV), **kw), torch.empty((B, NU), **kw)
-    info = torch.empty((B,), dtype=torch.int32, device=tape.device)
-    if B == 0:
-        return [gq, gv, gu, info]
-    lib = _STATE["lib"]
-    if kin_state:
-        q1, v1 = kin_state
-        _check("qpos'", q1, (B, NQ), dev)
-        _check("qvel'", v1, (B, NV), dev)
-        for name, x, shape in zip(("g_qpos_n", "g_xpos", "g_xquat", "g_cvel", "g_subtree_com"), kin_cot,
-                                  _kin_shapes(B)):
-            _check(name, x, shape, dev)
-    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
-    with _OnDevice(dev):
-        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        if kin_state:  # the kinematics outputs' cotangents pulled back onto (qpos', qvel'), theirs added last
-            cq, cv = torch.empty((B, NQ), **kw), torch.empty((B, NV), **kw)
-            _rc(lib.dk_fwd_kinematics_vjp(st, B, _ptr(q1), _ptr(v1), _ptr(com), *map(_ptr, kin_cot), _ptr(g_qpos),
-                                          _ptr(g_qvel), _ptr(cq), _ptr(cv)), "the kinematics VJP launch")
-            g_qpos, g_qvel = cq, cv
-        args = (st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos), _ptr(g_qvel), _ptr(gq),
-                _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl), ctypes.c_float(0.0 if clamp_soft is None else clamp_soft),
-                v[0], v[1], _ptr(work) if work.numel() else None)
-        if _DIAG_ON[0]:  # counters, and the non-finite bits into info (reference torch_ffi.py:538-540), by the
-            _rc(lib.dk_adjoint_work_diag(*args, _ptr(_DIAG[dev])), "the adjoint launch")  # adjoint kernel itself
-        else:
-            _rc(lib.dk_adjoint_work(*args), "the adjoint launch")
-    return [gq, gv, gu, info]
-
-
-
-def _vjps(tape, friction, com, g_qpos, g_qvel, ctrl=None, *, substeps=SUBSTEPS, clamp_kv=CLAMP_KV, normal=NORMAL,
-          clamp_soft=None):
-    """K VJPs of one taped step in one adjoint launch (dk_adjoint_many): g_qpos (K, B, 36) and g_qvel (K, B, 35)
-    output cotangents -> g_qpos_in (K, B, 36), g_qvel_in (K, B, 35), g_ctrl (K, B, 29) and info (K, B). Each k is
-    backward(tape, ..., g_qpos[k], g_qvel[k]) bitwise (the diagnostics count K backward calls), the worlds of every set
-    in one dispatch order: the step Jacobian's driver."""
-    import torch
-    K = g_qpos.shape[0] if isinstance(g_qpos, torch.Tensor) and g_qpos.dim() == 3 else 0
-    if K < 1 or not isinstance(g_qvel, torch.Tensor) or g_qvel.dim() != 3 or g_qvel.shape[0] != K:
-        raise _err("g_qpos (K, B, 36) and g_qvel (K, B, 35), K >= 1")
-    dev, B = _backward_checks(tape, friction, com, g_qpos[0], g_qvel[0], ctrl, substeps, clamp_kv, normal)
-    _check("g_qpos", g_qpos, (K, B, NQ), dev)
-    _check("g_qvel", g_qvel, (K, B, NV), dev)
-    kw = dict(dtype=torch.float32, device=tape.device)
-    gq, gv, gu = (torch.empty((K, B, n), **kw) for n in (NQ, NV, NU))
-    info = torch.empty((K, B), dtype=torch.int32, device=tape.device)
-    if B == 0:
-        return gq, gv, gu, info
-    lib = _STATE["lib"]
-    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
-    with _OnDevice(dev):
-        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        _rc(lib.dk_adjoint_many(st, B, K, int(substeps), _ptr(tape), _ptr(friction), _ptr(com), _ptr(g_qpos),
-                                _ptr(g_qvel), _ptr(gq), _ptr(gv), _ptr(gu), _ptr(info), _ptr(ctrl),
-                                ctypes.c_float(0.0 if clamp_soft is None else clamp_soft), int(clamp_kv), int(normal),
-                                _ptr(work), _ptr(_DIAG[dev]) if _DIAG_ON[0] else None), "the adjoint launch")
-    return gq, gv, gu, info
-    lib = _STATE["lib"]
-    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
-    soft = ctypes.c_float(0.0 if clamp_soft is None else clamp_soft)
-    with _OnDevice(dev):
-        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        _rc(lib.dk_adjoint_order(st, B, int(substeps), _ptr(tape), _ptr(work)), "the adjoint order launch")
-        d = _ptr(_DIAG[dev]) if _DIAG_ON[0] else None
-        for k in range(K):
-            _check("g_qpos[k]", g_qpos[k], (B, NQ), dev)
-            _check("g_qvel[k]", g_qvel[k], (B, NV), dev)
-            _rc(lib.dk_adjoint_work_ordered(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com),
-                                            _ptr(g_qpos[k]), _ptr(g_qvel[k]), _ptr(gq[k]), _ptr(gv[k]), _ptr(gu[k]),
-                                            _ptr(info), _ptr(ctrl), soft, int(clamp_kv), int(normal), _ptr(work), d),
-                "the adjoint launch")
-    return gq, gv, gu, info
-    dev = tape.device.index
-    lib = _STATE["lib"]
-    work = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device=tape.device)
-    soft = ctypes.c_float(0.0 if clamp_soft is None else clamp_soft)
-    with _OnDevice(dev):
-        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        _rc(lib.dk_adjoint_order(st, B, int(substeps), _ptr(tape), _ptr(work)), "the adjoint order launch")
-        d = _ptr(_DIAG[dev]) if _DIAG_ON[0] else None
-        for k in range(1, K):
-            _check("g_qpos[k]", g_qpos[k], (B, NQ), dev)
-            _check("g_qvel[k]", g_qvel[k], (B, NV), dev)
-            _rc(lib.dk_adjoint_work_ordered(st, B, int(substeps), _ptr(tape), _ptr(friction), _ptr(com),
-                                            _ptr(g_qpos[k]), _ptr(g_qvel[k]), _ptr(gq[k]), _ptr(gv[k]), _ptr(gu[k]),
-                                            _ptr(info), _ptr(ctrl), soft, int(clamp_kv), int(normal), _ptr(work), d),
-                "the adjoint launch")
-    return gq, gv, gu, info
-
-def _kinematics_impl(qpos, qvel, com):
-    import torch
-    if not isinstance(qpos, torch.Tensor) or qpos.device.type != "cuda":
-        raise _err("qpos must be a GPU torch.Tensor")
-    dev = qpos.device.index
-    B = qpos.shape[0] if qpos.dim() == 2 else -1
-    for name, x, shape in (("qpos", qpos, (B, NQ)), ("qvel", qvel, (B, NV)), ("com", com, (B, 3))):
-        _check(name, x, shape, dev)
-    if dev not in _READY:
-        init(dev)
-    out = _kin_empty(B, qpos.device)
-    if B:
-        with _OnDevice(dev):
-            st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-            _rc(_STATE["lib"].dk_fwd_kinematics(st, B, _ptr(qpos), _ptr(qvel), _ptr(com), *map(_ptr, out)),
-                "the kinematics launch")
-    return out
-
-
-def _kinematics_backward_impl(qpos, qvel, com, *cot):
-    import torch
-    dev = qpos.device.index
-    B = qpos.shape[0]
-    for name, x, shape in (("qpos", qpos, (B, NQ)), ("qvel", qvel, (B, NV)), ("com", com, (B, 3))):
-        _check(name, x, shape, dev)
-    for name, x, shape in zip(("g_qpos_n", "g_xpos", "g_xquat", "g_cvel", "g_subtree_com"), cot, _kin_shapes(B)):
-        _check(name, x, shape, dev)
-    kw = dict(dtype=torch.float32, device=qpos.device)
-    gq, gv = torch.empty((B, NQ), **kw), torch.empty((B, NV), **kw)
-    if B:
-        with _OnDevice(dev):
-            st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-            _rc(_STATE["lib"].dk_fwd_kinematics_vjp(st, B, _ptr(qpos), _ptr(qvel), _ptr(com), *map(_ptr, cot), None,
-                                                    None, _ptr(gq), _ptr(gv)), "the kinematics VJP launch")
-    return [gq, gv]
-
-
-def _backward_op_impl(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv, normal,
-                      clamp_soft):
-    """_backward_impl with the custom op's argument order (reference torch_ffi.py:617-622): clamp_soft 0.0 for none."""
-    return _backward_impl(tape, friction, com, g_qpos, g_qvel, ctrl, substeps, clamp_kv, normal,
-                          None if clamp_kv != 2 else clamp_soft, tuple(kin_state), tuple(kin_cot))
-
-
-_OPS = {}
-_IMPL = dict(forward=_forward_impl, backward=_backward_op_impl, kinematics=_kinematics_impl,
-             kinematics_backward=_kinematics_backward_impl)
-
-
-def _ops():
-    """The library calls: the custom ops while torch.compile traces, the same functions called directly in eager
-    mode (no custom-op dispatch on the host path); reference torch_ffi.py:583-592."""
-    import torch
-    if not torch.compiler.is_compiling():
-        return _IMPL
-    return _custom_ops()
-
-
-def _custom_ops():
-    """nablaengine::forward, ::backward, ::kinematics, ::kinematics_backward (torch.library custom ops, no mutated
-    arguments, fresh outputs) with fake implementations giving the outputs' shapes; defined once per process
-    (reference torch_ffi.py:595-649)."""
-    if _OPS:
-        return _OPS
-    import torch
-    from typing import List, Optional
-    from torch import Tensor
-
-    @torch.library.custom_op("nablaengine::forward", mutates_args=())
-    def forward_op(qpos: Tensor, qvel: Tensor, warm: Tensor, ctrl: Tensor, friction: Tensor, com: Tensor,
-                   iterations: int, substeps: int, tape: bool, kinematics: bool) -> List[Tensor]:
-        return _forward_impl(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics)
-
-    @forward_op.register_fake
-    def _(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics):
-        B = qpos.shape[0]
-        out = [qpos.new_empty((B, NQ)), qpos.new_empty((B, NV)), qpos.new_empty((B, NV)),
-               qpos.new_empty((B, 4), dtype=torch.int32), qpos.new_empty((B if tape else 0, substeps * rec_words()))]
-        return out + ([qpos.new_empty(sh) for sh in _kin_shapes(B)] if kinematics else [])
-
-    @torch.library.custom_op("nablaengine::backward", mutates_args=())
-    def backward_op(tape: Tensor, friction: Tensor, com: Tensor, g_qpos: Tensor, g_qvel: Tensor,
-                    ctrl: Optional[Tensor], kin_state: List[Tensor], kin_cot: List[Tensor], substeps: int,
-                    clamp_kv: int, normal: int, clamp_soft: float) -> List[Tensor]:
-        return _backward_op_impl(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv,
-                                 normal, clamp_soft)
-
-    @backward_op.register_fake
-    def _(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv, normal, clamp_soft):
-        B = tape.shape[0]
-        return [tape.new_empty((B, NQ)), tape.new_empty((B, NV)), tape.new_empty((B, NU)),
-                tape.new_empty((B,), dtype=torch.int32)]
-
-    @torch.library.custom_op("nablaengine::kinematics", mutates_args=())
-    def kinematics_op(qpos: Tensor, qvel: Tensor, com: Tensor) -> List[Tensor]:
-        return _kinematics_impl(qpos, qvel, com)
-
-    @kinematics_op.register_fake
-    def _(qpos, qvel, com):
-        return [qpos.new_empty(sh) for sh in _kin_shapes(qpos.shape[0])]
-
-    @torch.library.custom_op("nablaengine::kinematics_backward", mutates_args=())
-    def kinematics_backward_op(qpos: Tensor, qvel: Tensor, com: Tensor, g_qpos_n: Tensor, g_xpos: Tensor,
-                               g_xquat: Tensor, g_cvel: Tensor, g_subtree_com: Tensor) -> List[Tensor]:
-        return _kinematics_backward_impl(qpos, qvel, com, g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com)
-
-    @kinematics_backward_op.register_fake
-    def _(qpos, qvel, com, g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com):
-        B = qpos.shape[0]
-        return [qpos.new_empty((B, NQ)), qpos.new_empty((B, NV))]
-
-    _OPS.update(forward=forward_op, backward=backward_op, kinematics=kinematics_op,
-                kinematics_backward=kinematics_backward_op)
-    return _OPS
-
-
-def _make_step_fn():
-    import torch
-
-    class _Step(torch.autograd.Function):
-        """reference torch_ffi.py:747-779: the tape as the residual; gradients for qpos, qvel and ctrl only; with
-        kinematics the output state's kinematics outputs too, their cotangents pulled back onto (qpos', qvel') first."""
-
-        @staticmethod
-        def forward(ctx, qpos, qvel, warm, ctrl, friction, com, iterations, substeps, clamp_kv, normal, clamp_soft,
-                    grad_decay, kin):
-            r = _ops()["forward"](qpos, qvel, warm, ctrl, friction, com, iterations, substeps, True, kin)
-            q1, v1, w1, info, tp = r[:5]
-            ctx.save_for_backward(tp, friction, com, ctrl, q1, v1)
-            ctx.opts = (substeps, clamp_kv, normal, clamp_soft, grad_decay, kin)
-            ctx.mark_non_differentiable(w1)
-            return (q1, v1, w1) + tuple(r[5:])
-
-        @staticmethod
-        def backward(ctx, g_q1, g_v1, g_w1, *g_kin):
-            tp, friction, com, ctrl, q1, v1 = ctx.saved_tensors
-            substeps, clamp_kv, normal, clamp_soft, grad_decay, kin = ctx.opts
-            g_q1 = torch.zeros_like(q1) if g_q1 is None else g_q1.contiguous()
-            g_v1 = torch.zeros_like(v1) if g_v1 is None else g_v1.contiguous()
-            ks, kc = [], []
-            if kin and any(g is not None for g in g_kin):
-                ks = [q1, v1]
-                kc = [torch.zeros(sh, dtype=torch.float32, device=q1.device) if g is None else g.contiguous()
-                      for g, sh in zip(g_kin, _kin_shapes(q1.shape[0]))]
-            gq, gv, gu, _ = _ops()["backward"](tp, friction, com, g_q1, g_v1, ctrl if clamp_kv == 2 else None, ks, kc,
-                                               substeps, clamp_kv, normal, 0.0 if clamp_soft is None else clamp_soft)
-            if grad_decay != 1.0:  # the state cotangent through this step times it, ctrl's not (float32 product)
-                gq, gv = gq * grad_decay, gv * grad_decay
-            return gq, gv, None, gu, None, None, None, None, None, None, None, None, None
-
-    return _Step
-
-
-def _make_kin_fn():
-    import torch
-
-    class _Kin(torch.autograd.Function):
-        """reference torch_ffi.py:787-804: gradients for qpos and qvel, none for com."""
-
-        @staticmethod
-        def forward(ctx, qpos, qvel, com):
-            out = _ops()["kinematics"](qpos, qvel, com)
-            ctx.save_for_backward(qpos, qvel, com)
-            return tuple(out)
-
-        @staticmethod
-        def backward(ctx, *g):
-            qpos, qvel, com = ctx.saved_tensors
-            g = [torch.zeros(sh, dtype=torch.float32, device=qpos.device) if x is None else x.contiguous()
-                 for x, sh in zip(g, _kin_shapes(qpos.shape[0]))]
-            gq, gv = _ops()["kinematics_backward"](qpos, qvel, com, *g)
-            return gq, gv, None
-
-    return _Kin
-
-
-_FNS = {}
-
-
-def _fn(name, make):
-    if name not in _FNS:
-        _FNS[name] = make()
-    return _FNS[name]
-
-
-def step(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, clamp_kv=CLAMP_KV,
-         normal=NORMAL, clamp_soft=None, grad_decay=GRAD_DECAY, kinematics=False):
-    """One control step: (qpos', qvel', warm'); kinematics=True: (qpos', qvel', warm', qpos_n, xpos, xquat, cvel,
-    subtree_com), the output state's kinematics (reference torch_ffi.py:817-835). Differentiable in qpos, qvel and ctrl
-    when any input requires grad (the forward then also writes the tape); warm' is not differentiable."""
-    import torch
-    if int(clamp_kv) not in (0, 1, 2) or int(normal) not in (0, 1, 2, 3):
-        raise _err("clamp_kv in {0, 1, 2}, normal in 0..3", ValueError)
-    soft = _soft(clamp_kv, clamp_soft)
-    gd = float(grad_decay)
-    if not math.isfinite(gd):
-        raise _err(f"grad_decay must be finite, got {grad_decay}", ValueError)
-    args = (qpos, qvel, warm, ctrl, friction, com)
-    if torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in args):
-        return _fn("step", _make_step_fn).apply(*args, int(iterations), int(substeps), int(clamp_kv), int(normal),
-                                                soft, gd, bool(kinematics))
-    r = _ops()["forward"](*args, int(iterations), int(substeps), False, bool(kinematics))
-    return tuple(r[:3]) + tuple(r[5:])
-
-
-def kinematics(qpos, qvel, com):
-    """Differentiable kinematics outputs of states (qpos, qvel, com): (qpos_n, xpos, xquat, cvel, subtree_com)
-    (reference torch_ffi.py:838-842); gradients for qpos and qvel, none for com. kinematics(q', v', com) of a step's
-    output is bitwise step(..., kinematics=True)'s."""
-    import torch
-    if torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in (qpos, qvel, com)):
-        return _fn("kin", _make_kin_fn).apply(qpos, qvel, com)
-    return tuple(_ops()["kinematics"](qpos, qvel, com))
-
-
-def forward(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, tape=False,
-            kinematics=False):
-    """One control step without autograd: (qpos', qvel', warm', info (B, 4) int32[, tape][, the kinematics outputs])
-    (reference torch_ffi.py:845-851)."""
-    r = _ops()["forward"](qpos, qvel, warm, ctrl, friction, com, int(iterations), int(substeps), bool(tape),
-                          bool(kinematics))
-    return tuple(r[:4]) + ((r[4],) if tape else ()) + tuple(r[5:])
-
-
-def backward(tape, friction, com, g_qpos, g_qvel, *, substeps=SUBSTEPS, clamp_kv=CLAMP_KV, normal=NORMAL, ctrl=None,
-             clamp_soft=None, kinematics=None):
-    """The adjoint of one control step from its tape: (g_qpos (B, 36), g_qvel (B, 35), g_ctrl (B, 29), info (B,))
-    (reference torch_ffi.py:854-865); kinematics: None or (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel,
-    g_subtree_com), the cotangents of the output state's kinematics outputs, pulled back and added first."""
-    soft = _soft(clamp_kv, clamp_soft)
-    if soft is not None and ctrl is None:
-        raise _err("clamp_kv=2 (the soft clamp) needs the step's ctrl", ValueError)
-    ks, kc = ([], []) if kinematics is None else (list(kinematics[:2]), list(kinematics[2:]))
-    if kinematics is not None and len(kc) != 5:
-        raise _err("kinematics = (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com)", ValueError)
-    return tuple(_ops()["backward"](tape, friction, com, g_qpos, g_qvel, ctrl if soft is not None else None, ks, kc,
-                                    int(substeps), int(clamp_kv), int(normal), 0.0 if soft is None else soft))
-
-
-def set_diagnostics(enabled):
-    """Switch the device counters and the backward's non-finite bits on (the default) or off; returns the previous
-    setting (reference torch_ffi.py:678-686). When on, the forward and adjoint kernels add each world's counts at its
-    end (dk_fwd_forward_diag / dk_adjoint_work_diag); outputs and gradients are the same either way."""
-    prev = _DIAG_ON[0]
-    _DIAG_ON[0] = bool(enabled)
-    return prev
+def init(device=None, artifact=None, model_dir=None, model=None, foot_pairs=None):
+    """Load the library (artifact as library_path's) and make `device` (default: torch's current one) ready to run
+    it; repeated calls are no-ops (the reference's init, torch_ffi.py:268-290). The G1 model is compiled into the
+    library, so nothing is uploaded and nothing synchronizes: naming another model (model_dir, model, foot_pairs) is a
+    ValueError. Returns the library's path, architecture and sizes."""
+    if (model_dir, model, foot_pairs) != (None, None, None):
+        raise _err("this library is built for the G1 model: model_dir / model / foot_pairs cannot change it",
+                   ValueError)
+    nat = _load(artifact)
+    dev = _device_index(device)
+    with _lock:
+        if dev not in _counters:
+            if not torch.cuda.is_available():
+                raise _err("no ROCm GPU is visible, and the engine has no CPU path", RuntimeError)
+            arch = getattr(torch.cuda.get_device_properties(dev), "gcnArchName", ARCH).split(":")[0]
+            if arch != ARCH:
+                raise _err(f"cuda:{dev} is {arch}; the library holds {ARCH} code only", RuntimeError)
+            with torch.cuda.device(dev):
+                nat.run(f"making cuda:{dev} ready", "dk_fwd_upload", None, _stream(dev))
+            _counters[dev] = torch.zeros(len(DIAG), dtype=torch.int64, device=f"cuda:{dev}")
+        _register_ops()  # outside any torch.compile trace: defining operators inside one is not traceable
+    return dict(path=nat.path, arch=ARCH, sizes=list(nat.sizes))
 
 
 def _device_index(device):
-    import torch
     if device is None:
         return torch.cuda.current_device()
     d = torch.device(device)
     return torch.cuda.current_device() if d.index is None else d.index
 
 
-def diagnostics(device=None):
-    """The device's counters: an int64 (len(DIAG),) GPU tensor in DIAG order, added up by every call since init or the
-    last reset; not copied or synchronized (reference torch_ffi.py:689-695)."""
-    dev = _device_index(device)
-    if dev not in _READY:
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _ready(dev):
+    if dev not in _counters:
         init(dev)
-    return _DIAG[dev]
+    return _native
 
 
-def read_diagnostics(device=None, reset=True):
-    """The device's counters as {name: int} (synchronizes); reset=True zeroes them afterwards; with
-    set_overflow_warnings(True) it warns when worlds exceeded the contact or row capacity (reference
-    torch_ffi.py:698-708)."""
-    d = diagnostics(device)
-    out = dict(zip(DIAG, (int(x) for x in d.cpu())))
-    if reset:
-        d.zero_()
-    if _OVERFLOW_WARN[0]:
-        warn_overflow(out)
+# ---- argument checks ------------------------------------------------------------------------------------------------
+
+class _Worlds:
+    """The worlds of one call: the device and the count B come from its first per-world array (per_world: the rank of
+    its per-world part); every array must then be a contiguous tensor of the given dtype on that device, shaped
+    (*lead, B, *per_world)."""
+
+    def __init__(self, name, x, per_world):
+        if not isinstance(x, Tensor) or x.device.type != "cuda":
+            where = x.device if isinstance(x, Tensor) else type(x).__name__
+            raise _err(f"{name} must be a torch.Tensor on a ROCm device, got {where}")
+        self.device = x.device
+        self.dev = x.device.index
+        self.B = x.shape[0] if x.dim() == 1 + len(per_world) else -1
+
+    def ptr(self, name, x, per_world, dtype=torch.float32, lead=()):
+        """x's device pointer after the checks; None stays None only where the caller allows it."""
+        want = (*lead, self.B, *per_world)
+        if (isinstance(x, Tensor) and x.dtype == dtype and tuple(x.shape) == want and x.device == self.device
+                and x.is_contiguous()):
+            return ctypes.c_void_p(x.data_ptr())
+        got = (f"{x.dtype} {tuple(x.shape)} on {x.device}{'' if x.is_contiguous() else ', not contiguous'}"
+               if isinstance(x, Tensor) else type(x).__name__)
+        raise _err(f"{name}: expected a contiguous {dtype} tensor {want} on {self.device}, got {got}")
+
+    def empty(self, *per_world, dtype=torch.float32, lead=()):
+        return torch.empty((*lead, self.B, *per_world), dtype=dtype, device=self.device)
+
+
+def _soft_delta(clamp_kv, clamp_soft):
+    """The soft clamp's delta: for clamp_kv 2, clamp_soft or CLAMP_SOFT when it is None (finite, >= 0); for 0 and 1
+    None, and clamp_soft must be None too."""
+    if int(clamp_kv) == 2:
+        delta = CLAMP_SOFT if clamp_soft is None else float(clamp_soft)
+        if math.isfinite(delta) and delta >= 0.0:
+            return delta
+        raise _err(f"clamp_soft must be finite and >= 0, got {clamp_soft}", ValueError)
+    if clamp_soft is not None:
+        raise _err(f"clamp_soft belongs to the soft clamp (clamp_kv=2), not to clamp_kv={clamp_kv}", ValueError)
+    return None
+
+
+def _variant(clamp_kv, normal):
+    v = (int(clamp_kv), int(normal))
+    if v not in VARIANTS:
+        raise _err(f"clamp_kv must be 0, 1 or 2 and normal 0..3, got clamp_kv={clamp_kv} normal={normal}", ValueError)
+    return v
+
+
+# ---- the library calls ----------------------------------------------------------------------------------------------
+
+def _forward_call(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics):
+    """One control step: [qpos', qvel', warm', info, tape (B or 0 rows)] + the output state's kinematics outputs."""
+    w = _Worlds("qpos", qpos, (NQ,))
+    ins = [w.ptr(name, x, shape) for (name, shape), x in zip(_STATE_IN, (qpos, qvel, warm, ctrl, friction, com))]
+    if not 1 <= substeps <= 32 or iterations < 0:
+        raise _err(f"substeps must be in 1..32 and iterations >= 0, got {substeps} and {iterations}", ValueError)
+    nat = _ready(w.dev)
+    q1, v1, w1, info = w.empty(NQ), w.empty(NV), w.empty(NV), w.empty(4, dtype=torch.int32)
+    tp = torch.empty((w.B if tape else 0, substeps * nat.rec_words), dtype=torch.float32, device=w.device)
+    kin = [w.empty(*shape) for _, shape in _KIN_OUT] if kinematics else []
+    out = [q1, v1, w1, info, tp] + kin
+    if w.B == 0:
+        return out
+    work = torch.empty((int(nat.dll.dk_fwd_work_bytes(w.B)),), dtype=torch.uint8, device=w.device)
+    P = ctypes.c_void_p
+    with torch.cuda.device(w.dev):
+        st = _stream(w.dev)
+        args = [st, w.B, *ins, int(iterations), int(substeps), P(q1.data_ptr()), P(v1.data_ptr()), P(w1.data_ptr()),
+                P(info.data_ptr()), None, P(tp.data_ptr()) if tape else None, P(work.data_ptr()) if work.numel() else None]
+        if _settings["count"]:  # the kernel adds each world's counts at its end (dk_torch_diag_fwd's counts)
+            nat.run("the forward launch", "dk_fwd_forward_diag", *args, P(_counters[w.dev].data_ptr()))
+        else:
+            nat.run("the forward launch", "dk_fwd_forward", *args)
+        if kinematics:
+            nat.run("the kinematics launch", "dk_fwd_kinematics", st, w.B, P(q1.data_ptr()), P(v1.data_ptr()),
+                    ins[5], *(P(t.data_ptr()) for t in kin))
     return out
 
 
-def warn_overflow(d, where="nablaengine_amd"):
-    """A RuntimeWarning when the counters d count worlds whose contacts (64) or constraint rows (192) exceeded the
-    per-world capacity: the extra ones were dropped, so those worlds miss support and friction forces; returns the
-    count (reference torch_ffi.py:711-724)."""
-    import warnings
-    nc, nr = d.get("fwd_contact_overflow_worlds", 0), d.get("fwd_row_overflow_worlds", 0)
-    if nc or nr:
-        warnings.warn(f"{where}: {nc} world-steps exceeded the contact capacity ({MAXCON} per world) and {nr} the "
-                      f"constraint-row capacity (192); their extra contacts / rows were dropped, so those worlds miss "
-                      f"support and friction forces (e.g. deep interpenetration)", RuntimeWarning, stacklevel=3)
-    return nc + nr
+def _backward_call(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv, normal,
+                   clamp_soft):
+    """The adjoint from a tape: [g_qpos (B, 36), g_qvel (B, 35), g_ctrl (B, 29), info (B,)]. kin_state = [qpos',
+    qvel'] with kin_cot the five kinematics outputs' cotangents, or both empty. clamp_soft: the delta (read for
+    clamp_kv 2 only)."""
+    kv, nrm = _variant(clamp_kv, normal)
+    if (kv == 2) != (ctrl is not None):
+        raise _err("the step's ctrl goes with clamp_kv=2 (the soft clamp) and only with it", ValueError)
+    w = _Worlds("tape", tape, (None,))
+    nat = _ready(w.dev)
+    ptape = w.ptr("tape", tape, (substeps * nat.rec_words,))
+    pf, pc = w.ptr("friction", friction, ()), w.ptr("com", com, (3,))
+    pgq, pgv = w.ptr("g_qpos", g_qpos, (NQ,)), w.ptr("g_qvel", g_qvel, (NV,))
+    pu = w.ptr("ctrl", ctrl, (NU,)) if ctrl is not None else None
+    if kin_state:
+        pks = [w.ptr(n, x, s) for n, x, s in zip(("qpos'", "qvel'"), kin_state, ((NQ,), (NV,)))]
+        pkc = [w.ptr("g_" + n, x, s) for (n, s), x in zip(_KIN_OUT, kin_cot)]
+        if len(pkc) != 5:
+            raise _err("kin_cot: the cotangents of the five kinematics outputs", ValueError)
+    gq, gv, gu, info = w.empty(NQ), w.empty(NV), w.empty(NU), w.empty(dtype=torch.int32)
+    if w.B == 0:
+        return [gq, gv, gu, info]
+    work = torch.empty((int(nat.dll.dk_adjoint_work_bytes(w.B)),), dtype=torch.uint8, device=w.device)
+    P = ctypes.c_void_p
+    with torch.cuda.device(w.dev):
+        st = _stream(w.dev)
+        if kin_state:  # the kinematics cotangents pulled back onto (qpos', qvel'); the step's own added last
+            cq, cv = w.empty(NQ), w.empty(NV)
+            nat.run("the kinematics VJP launch", "dk_fwd_kinematics_vjp", st, w.B, *pks, pc, *pkc, pgq, pgv,
+                    P(cq.data_ptr()), P(cv.data_ptr()))
+            pgq, pgv = P(cq.data_ptr()), P(cv.data_ptr())
+        args = [st, w.B, int(substeps), ptape, pf, pc, pgq, pgv, P(gq.data_ptr()), P(gv.data_ptr()), P(gu.data_ptr()),
+                P(info.data_ptr()), pu, ctypes.c_float(clamp_soft), kv, nrm, P(work.data_ptr()) if work.numel() else None]
+        if _settings["count"]:  # counts and the non-finite bits of info, by the adjoint kernel itself
+            nat.run("the adjoint launch", "dk_adjoint_work_diag", *args, P(_counters[w.dev].data_ptr()))
+        else:
+            nat.run("the adjoint launch", "dk_adjoint_work", *args)
+    return [gq, gv, gu, info]
 
 
-def set_overflow_warnings(enabled):
-    """Switch the capacity-overflow warnings on or off (default off, or $DK_OVERFLOW_WARN=1); when on, the counts
-    nobody read are reported once more at exit. Returns the previous setting (reference torch_ffi.py:727-735)."""
-    prev = _OVERFLOW_WARN[0]
-    _OVERFLOW_WARN[0] = bool(enabled)
-    return prev
+def _kinematics_call(qpos, qvel, com):
+    w = _Worlds("qpos", qpos, (NQ,))
+    ins = [w.ptr("qpos", qpos, (NQ,)), w.ptr("qvel", qvel, (NV,)), w.ptr("com", com, (3,))]
+    nat = _ready(w.dev)
+    out = [w.empty(*shape) for _, shape in _KIN_OUT]
+    if w.B:
+        with torch.cuda.device(w.dev):
+            nat.run("the kinematics launch", "dk_fwd_kinematics", _stream(w.dev), w.B, *ins,
+                    *(ctypes.c_void_p(t.data_ptr()) for t in out))
+    return out
 
 
-def _exit_report():
-    """At exit: the overflow warning for each device's counts since the last read (no reset); never raises."""
-    try:
-        if not (_DIAG_ON[0] and _OVERFLOW_WARN[0]):
-            return
-        for dev in sorted(_DIAG):
-            warn_overflow(dict(zip(DIAG, (int(x) for x in _DIAG[dev].cpu()))), where=f"nablaengine_amd (cuda:{dev})")
-    except Exception:  # noqa: BLE001  (interpreter or the runtime shutting down)
-        pass
+def _kinematics_backward_call(qpos, qvel, com, *cot):
+    w = _Worlds("qpos", qpos, (NQ,))
+    ins = [w.ptr("qpos", qpos, (NQ,)), w.ptr("qvel", qvel, (NV,)), w.ptr("com", com, (3,))]
+    ins += [w.ptr("g_" + n, x, s) for (n, s), x in zip(_KIN_OUT, cot)]
+    nat = _ready(w.dev)
+    gq, gv = w.empty(NQ), w.empty(NV)
+    if w.B:
+        with torch.cuda.device(w.dev):
+            nat.run("the kinematics VJP launch", "dk_fwd_kinematics_vjp", _stream(w.dev), w.B, *ins, None, None,
+                    ctypes.c_void_p(gq.data_ptr()), ctypes.c_void_p(gv.data_ptr()))
+    return [gq, gv]
 
 
-atexit.register(_exit_report)
+def _vjp_sets(tape, friction, com, g_qpos, g_qvel, ctrl=None, *, substeps=SUBSTEPS, clamp_kv=CLAMP_KV,
+              normal=NORMAL, clamp_soft=None):
+    """K VJPs of one taped step in one adjoint launch (dk_adjoint_many): output cotangents g_qpos (K, B, 36), g_qvel
+    (K, B, 35) -> (g_qpos (K, B, 36), g_qvel (K, B, 35), g_ctrl (K, B, 29), info (K, B)). Set k is bitwise
+    backward(tape, friction, com, g_qpos[k], g_qvel[k], ...) with the same options (clamp_soft None meaning
+    CLAMP_SOFT for clamp_kv 2, as there), and the counters count K backward calls. The step Jacobian's driver."""
+    kv, nrm = _variant(clamp_kv, normal)
+    delta = _soft_delta(kv, clamp_soft)
+    if (kv == 2) != (ctrl is not None):
+        raise _err("the step's ctrl goes with clamp_kv=2 (the soft clamp) and only with it", ValueError)
+    if not (isinstance(g_qpos, Tensor) and g_qpos.dim() == 3 and g_qpos.shape[0] >= 1):
+        raise _err("g_qpos must be a (K, B, 36) tensor with K >= 1")
+    K = g_qpos.shape[0]
+    w = _Worlds("tape", tape, (None,))
+    nat = _ready(w.dev)
+    if K * w.B * 64 >= 2 ** 32:
+        raise _err(f"{K} cotangent sets of {w.B} worlds exceed one launch's 2^32 work-items", ValueError)
+    args = [w.ptr("tape", tape, (substeps * nat.rec_words,)), w.ptr("friction", friction, ()),
+            w.ptr("com", com, (3,)), w.ptr("g_qpos", g_qpos, (NQ,), lead=(K,)),
+            w.ptr("g_qvel", g_qvel, (NV,), lead=(K,))]
+    pu = w.ptr("ctrl", ctrl, (NU,)) if ctrl is not None else None
+    outs = [w.empty(n, lead=(K,)) for n in (NQ, NV, NU)] + [w.empty(dtype=torch.int32, lead=(K,))]
+    if w.B == 0:
+        return tuple(outs)
+    work = torch.empty((int(nat.dll.dk_adjoint_work_bytes(w.B)),), dtype=torch.uint8, device=w.device)
+    P = ctypes.c_void_p
+    with torch.cuda.device(w.dev):
+        nat.run("the adjoint launch", "dk_adjoint_many", _stream(w.dev), w.B, K, int(substeps), *args,
+                *(P(t.data_ptr()) for t in outs), pu, ctypes.c_float(0.0 if delta is None else delta), kv, nrm,
+                P(work.data_ptr()), P(_counters[w.dev].data_ptr()) if _settings["count"] else None)
+    return tuple(outs)
 
 
-def _make_scale_fn():
-    import torch
+# ---- the operators (torch.library) ----------------------------------------------------------------------------------
+# Schemas: the reference's custom ops (torch_ffi.py:603-649), so that graphs recorded against either name the same
+# operators with the same arguments.
+_SCHEMAS = {
+    "forward": "forward(Tensor qpos, Tensor qvel, Tensor warm, Tensor ctrl, Tensor friction, Tensor com, "
+               "int iterations, int substeps, bool tape, bool kinematics) -> Tensor[]",
+    "backward": "backward(Tensor tape, Tensor friction, Tensor com, Tensor g_qpos, Tensor g_qvel, Tensor? ctrl, "
+                "Tensor[] kin_state, Tensor[] kin_cot, int substeps, int clamp_kv, int normal, float clamp_soft) "
+                "-> Tensor[]",
+    "kinematics": "kinematics(Tensor qpos, Tensor qvel, Tensor com) -> Tensor[]",
+    "kinematics_backward": "kinematics_backward(Tensor qpos, Tensor qvel, Tensor com, Tensor g_qpos_n, "
+                           "Tensor g_xpos, Tensor g_xquat, Tensor g_cvel, Tensor g_subtree_com) -> Tensor[]",
+}
 
-    class _Scale(torch.autograd.Function):
-        @staticmethod
-        def forward(ctx, gamma, *xs):
-            ctx.gamma = gamma
-            return tuple(x.view_as(x) for x in xs)
 
-        @staticmethod
-        def backward(ctx, *g):
-            return (None,) + tuple(None if x is None else x * ctx.gamma for x in g)
+def _fake_forward(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics):
+    B = qpos.shape[0]
+    shapes = [(B, NQ), (B, NV), (B, NV), None, (B if tape else 0, substeps * rec_words())]
+    out = [qpos.new_empty(s) if s else qpos.new_empty((B, 4), dtype=torch.int32) for s in shapes]
+    return out + ([qpos.new_empty((B, *s)) for _, s in _KIN_OUT] if kinematics else [])
 
-    return _Scale
+
+def _fake_backward(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv, normal,
+                   clamp_soft):
+    B = tape.shape[0]
+    return [tape.new_empty((B, n)) for n in (NQ, NV, NU)] + [tape.new_empty((B,), dtype=torch.int32)]
+
+
+def _fake_kinematics(qpos, qvel, com):
+    return [qpos.new_empty((qpos.shape[0], *s)) for _, s in _KIN_OUT]
+
+
+def _fake_kinematics_backward(qpos, qvel, com, *cot):
+    return [qpos.new_empty((qpos.shape[0], NQ)), qpos.new_empty((qpos.shape[0], NV))]
+
+
+_KERNELS = {"forward": (_forward_call, _fake_forward), "backward": (_backward_call, _fake_backward),
+            "kinematics": (_kinematics_call, _fake_kinematics),
+            "kinematics_backward": (_kinematics_backward_call, _fake_kinematics_backward)}
+_library_defs = []  # the torch.library.Library holding the definitions (kept alive for the process)
+
+
+def _ops():
+    """torch.ops.nablaengine, defined first where it is not yet (no lock taken once it is, so torch.compile traces
+    through this)."""
+    if not _library_defs:
+        _register_ops()
+    return torch.ops.nablaengine
+
+
+def _register_ops():
+    """Define the nablaengine operators once per process: the schema, the library call for every backend (a CPU or
+    other non-ROCm tensor reaches the checks and raises TypeError) and the fake implementation torch.compile traces
+    with. Returns torch.ops.nablaengine."""
+    with _lock:
+        if not _library_defs:
+            lib = torch.library.Library("nablaengine", "DEF")
+            for name, schema in _SCHEMAS.items():
+                call, fake = _KERNELS[name]
+                lib.define(schema)
+                lib.impl(name, call, "CompositeExplicitAutograd")
+                torch.library.register_fake(f"nablaengine::{name}", fake, lib=lib)
+            _library_defs.append(lib)
+    return torch.ops.nablaengine
+
+
+# ---- autograd -------------------------------------------------------------------------------------------------------
+
+class _StepOptions(NamedTuple):
+    iterations: int
+    substeps: int
+    clamp_kv: int
+    normal: int
+    delta: float  # the soft clamp's delta (clamp_kv 2), else 0
+    grad_decay: float
+    kinematics: bool
+
+
+class _StepFunction(torch.autograd.Function):
+    """step's autograd node: the forward writes the tape and keeps it with the arrays the adjoint reads; the backward
+    runs the adjoint (after the kinematics VJP when cotangents reach the kinematics outputs). Inputs (options, qpos,
+    qvel, warm, ctrl, friction, com); gradients for qpos, qvel and ctrl only (the reference's _Step,
+    torch_ffi.py:747-779)."""
+
+    @staticmethod
+    def forward(ctx, opts, qpos, qvel, warm, ctrl, friction, com):
+        q1, v1, w1, _info, tape, *kin = _ops().forward(qpos, qvel, warm, ctrl, friction, com, opts.iterations,
+                                                    opts.substeps, True, opts.kinematics)
+        ctx.opts = opts
+        ctx.save_for_backward(tape, friction, com, ctrl, q1, v1)
+        ctx.mark_non_differentiable(w1)
+        ctx.set_materialize_grads(False)
+        return (q1, v1, w1, *kin)
+
+    @staticmethod
+    def backward(ctx, g_q1, g_v1, _g_w1, *g_kin):
+        tape, friction, com, ctrl, q1, v1 = ctx.saved_tensors
+        o = ctx.opts
+        zero_or = lambda g, ref: torch.zeros_like(ref) if g is None else g.contiguous()  # noqa: E731
+        kin_state, kin_cot = [], []
+        if o.kinematics and any(g is not None for g in g_kin):
+            kin_state = [q1, v1]
+            kin_cot = [torch.zeros((q1.shape[0], *s), dtype=torch.float32, device=q1.device) if g is None
+                       else g.contiguous() for g, (_, s) in zip(g_kin, _KIN_OUT)]
+        gq, gv, gu, _ = _ops().backward(tape, friction, com, zero_or(g_q1, q1), zero_or(g_v1, v1),
+                                                 ctrl if o.clamp_kv == 2 else None, kin_state, kin_cot, o.substeps,
+                                                 o.clamp_kv, o.normal, o.delta)
+        if o.grad_decay != 1.0:
+            gq, gv = gq * o.grad_decay, gv * o.grad_decay
+        return None, gq, gv, None, gu, None, None
+
+
+class _KinematicsFunction(torch.autograd.Function):
+    """kinematics' autograd node: gradients for qpos and qvel, none for com (the reference's _Kin,
+    torch_ffi.py:785-804)."""
+
+    @staticmethod
+    def forward(ctx, qpos, qvel, com):
+        ctx.save_for_backward(qpos, qvel, com)
+        ctx.set_materialize_grads(False)
+        return tuple(_ops().kinematics(qpos, qvel, com))
+
+    @staticmethod
+    def backward(ctx, *g):
+        qpos, qvel, com = ctx.saved_tensors
+        cot = [torch.zeros((qpos.shape[0], *s), dtype=torch.float32, device=qpos.device) if x is None
+               else x.contiguous() for x, (_, s) in zip(g, _KIN_OUT)]
+        gq, gv = _ops().kinematics_backward(qpos, qvel, com, *cot)
+        return gq, gv, None
+
+
+def _wants_grad(*xs):
+    return torch.is_grad_enabled() and any(isinstance(x, Tensor) and x.requires_grad for x in xs)
+
+
+# ---- the public calls -----------------------------------------------------------------------------------------------
+
+def step(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, clamp_kv=CLAMP_KV,
+         normal=NORMAL, clamp_soft=None, grad_decay=GRAD_DECAY, kinematics=False):
+    """One control step -> (qpos', qvel', warm'), with kinematics=True followed by the output state's (qpos_n, xpos,
+    xquat, cvel, subtree_com) (the reference's step, torch_ffi.py:817-835). clamp_kv, normal, clamp_soft and
+    grad_decay shape the gradient only."""
+    kv, nrm = _variant(clamp_kv, normal)
+    delta = _soft_delta(kv, clamp_soft)
+    decay = float(grad_decay)
+    if not math.isfinite(decay):
+        raise _err(f"grad_decay must be finite, got {grad_decay}", ValueError)
+    ins = (qpos, qvel, warm, ctrl, friction, com)
+    if _wants_grad(*ins):
+        opts = _StepOptions(int(iterations), int(substeps), kv, nrm, 0.0 if delta is None else delta, decay,
+                            bool(kinematics))
+        return _StepFunction.apply(opts, *ins)
+    q1, v1, w1, _info, _tape, *kin = _ops().forward(*ins, int(iterations), int(substeps), False,
+                                                             bool(kinematics))
+    return (q1, v1, w1, *kin)
+
+
+def kinematics(qpos, qvel, com):
+    """The kinematics outputs (qpos_n, xpos, xquat, cvel, subtree_com) of the states (qpos, qvel, com), differentiable
+    in qpos and qvel (the reference's kinematics, torch_ffi.py:838-842)."""
+    if _wants_grad(qpos, qvel, com):
+        return _KinematicsFunction.apply(qpos, qvel, com)
+    return tuple(_ops().kinematics(qpos, qvel, com))
+
+
+def forward(qpos, qvel, warm, ctrl, friction, com, *, iterations=ITERATIONS, substeps=SUBSTEPS, tape=False,
+            kinematics=False):
+    """One control step outside autograd -> (qpos', qvel', warm', info (B, 4) int32[, tape][, kinematics outputs])
+    (the reference's forward, torch_ffi.py:845-851). info per world: Newton iterations of the last substep, contacts,
+    constraint rows, overflow bits (OVERFLOW_CONTACTS, OVERFLOW_ROWS)."""
+    with torch.no_grad():
+        q1, v1, w1, info, tp, *kin = _ops().forward(qpos, qvel, warm, ctrl, friction, com, int(iterations),
+                                                             int(substeps), bool(tape), bool(kinematics))
+    return (q1, v1, w1, info, *((tp,) if tape else ()), *kin)
+
+
+def backward(tape, friction, com, g_qpos, g_qvel, *, substeps=SUBSTEPS, clamp_kv=CLAMP_KV, normal=NORMAL, ctrl=None,
+             clamp_soft=None, kinematics=None):
+    """The adjoint of one control step from its tape -> (g_qpos (B, 36) in qpos form, g_qvel (B, 35), g_ctrl (B, 29),
+    info (B,) int32) (the reference's backward, torch_ffi.py:854-865). ctrl: the step's controls, for clamp_kv=2 only.
+    kinematics: None, or (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com) whose kinematics
+    cotangents are pulled back and added to g_qpos, g_qvel first."""
+    kv, nrm = _variant(clamp_kv, normal)
+    delta = _soft_delta(kv, clamp_soft)
+    if kv == 2 and ctrl is None:
+        raise _err("clamp_kv=2 (the soft clamp) needs the step's ctrl", ValueError)
+    kin_state, kin_cot = [], []
+    if kinematics is not None:
+        kinematics = list(kinematics)
+        if len(kinematics) != 7:
+            raise _err("kinematics = (qpos', qvel', g_qpos_n, g_xpos, g_xquat, g_cvel, g_subtree_com)", ValueError)
+        kin_state, kin_cot = kinematics[:2], kinematics[2:]
+    with torch.no_grad():
+        r = _ops().backward(tape, friction, com, g_qpos, g_qvel, ctrl if kv == 2 else None, kin_state,
+                                     kin_cot, int(substeps), kv, nrm, 0.0 if delta is None else delta)
+    return tuple(r)
+
+
+# ---- gradient scaling -----------------------------------------------------------------------------------------------
+
+class _ScaledCotangent(torch.autograd.Function):
+    """The identity on one tensor whose cotangent comes back multiplied by gamma (a float32 product)."""
+
+    @staticmethod
+    def forward(ctx, x, gamma):
+        ctx.gamma = gamma
+        return x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g * ctx.gamma, None
 
 
 def scale_grad(tree, gamma):
-    """The identity on a pytree of tensors whose cotangent the backward multiplies by gamma (floating tensors only)
-    (reference torch_ffi.py:868-899)."""
-    import torch
+    """The identity on a pytree whose floating-point tensors get their cotangents multiplied by gamma in the backward;
+    other leaves pass through (the reference's scale_grad, torch_ffi.py:868-899). Put on a rollout's carried state at
+    the top of each step, it makes a gradient through n step boundaries carry gamma^n."""
     from torch.utils import _pytree
     g = float(gamma)
     if not math.isfinite(g):
         raise _err(f"scale_grad's gamma must be finite, got {gamma}", ValueError)
-    leaves, spec = _pytree.tree_flatten(tree)
-    idx = [i for i, x in enumerate(leaves) if isinstance(x, torch.Tensor) and x.is_floating_point()]
-    if idx:
-        out = _fn("scale", _make_scale_fn).apply(g, *(leaves[i] for i in idx))
-        for i, x in zip(idx, out):
-            leaves[i] = x
-    return _pytree.tree_unflatten(leaves, spec)
+    return _pytree.tree_map(
+        lambda x: _ScaledCotangent.apply(x, g) if isinstance(x, Tensor) and x.is_floating_point() else x, tree)
+
+
+# ---- diagnostics ----------------------------------------------------------------------------------------------------
+
+def set_diagnostics(enabled):
+    """Counting on (the default) or off; returns the previous setting (the reference's set_diagnostics,
+    torch_ffi.py:678-686). On, the forward and adjoint kernels add each world's counts to the device's counters as it
+    ends (dk_fwd_forward_diag, dk_adjoint_work_diag) and the backward's info gets the non-finite bits. Outputs and
+    gradients do not depend on it."""
+    prev, _settings["count"] = _settings["count"], bool(enabled)
+    return prev
+
+
+def diagnostics(device=None):
+    """The device's counters: an int64 (len(DIAG),) GPU tensor in DIAG order, summed over the calls since init or the
+    last reset; neither copied nor synchronized (the reference's diagnostics, torch_ffi.py:689-695)."""
+    dev = _device_index(device)
+    _ready(dev)
+    return _counters[dev]
+
+
+def read_diagnostics(device=None, reset=True):
+    """The device's counters as {name: count} (a synchronization); reset zeroes them after the read. With overflow
+    warnings on, worlds beyond the contact or row capacity are reported (the reference's read_diagnostics,
+    torch_ffi.py:698-708)."""
+    t = diagnostics(device)
+    counts = {name: int(v) for name, v in zip(DIAG, t.tolist())}
+    if reset:
+        t.zero_()
+    if _settings["warn"]:
+        warn_overflow(counts)
+    return counts
+
+
+def warn_overflow(d, where="nablaengine_amd"):
+    """Warn (RuntimeWarning) when the counts d hold world-steps that found more than 64 contacts or 192 constraint
+    rows: the extra ones were dropped, so those worlds lack some support and friction forces. Returns how many
+    world-steps that is (the reference's warn_overflow, torch_ffi.py:711-724)."""
+    contacts, rows = d.get("fwd_contact_overflow_worlds", 0), d.get("fwd_row_overflow_worlds", 0)
+    if contacts or rows:
+        warnings.warn(f"{where}: world-steps over capacity: {contacts} found more than {MAXCON} contacts, {rows} more "
+                      f"than {MAXROWS} constraint rows; what did not fit was dropped, so those worlds miss part of "
+                      f"their support and friction forces (deep interpenetration?)", RuntimeWarning, stacklevel=3)
+    return contacts + rows
+
+
+def set_overflow_warnings(enabled):
+    """Overflow warnings on or off (default off, or $DK_OVERFLOW_WARN=1); on, read_diagnostics warns, and counts no
+    read took are reported once more at exit. Returns the previous setting (the reference's set_overflow_warnings,
+    torch_ffi.py:727-735)."""
+    prev, _settings["warn"] = _settings["warn"], bool(enabled)
+    return prev
+
+
+@atexit.register
+def _report_unread_overflow():
+    """At exit, with counting and warnings on: warn about each device's counts since the last read. Never raises."""
+    if not (_settings["count"] and _settings["warn"]):
+        return
+    try:
+        for dev, t in sorted(_counters.items()):
+            warn_overflow(dict(zip(DIAG, t.tolist())), where=f"nablaengine_amd (cuda:{dev})")
+    except Exception:  # noqa: BLE001  (the interpreter or the HIP runtime is shutting down)
+        pass

@@ -88,7 +88,7 @@ def test_custom_ops_fake_shapes():
     from nablaengine_amd import torch_ffi
     if not os.path.exists(LIB):
         pytest.skip("library not built")
-    torch_ffi._custom_ops()
+    torch_ffi._register_ops()
     B, rw = 5, torch_ffi.rec_words()
     with FakeTensorMode():
         a = [torch.empty(s) for s in ((B, 36), (B, 35), (B, 35), (B, 29), (B,), (B, 3))]
@@ -114,8 +114,9 @@ def test_init_artifacts_one_library_per_process(tmp_path):
         pytest.skip("library not built")
     lib = torch_ffi.load_library()
     art = tmp_path / "g1.json"
-    art.write_text(json.dumps({"library": os.path.relpath(torch_ffi._STATE["path"], tmp_path)}))
-    assert os.path.realpath(torch_ffi._library_path(str(art))) == os.path.realpath(torch_ffi._STATE["path"])
+    path = torch_ffi._native.path
+    art.write_text(json.dumps({"library": os.path.relpath(path, tmp_path)}))
+    assert os.path.realpath(torch_ffi.library_path(str(art))) == os.path.realpath(path)
     assert torch_ffi.load_library(str(art)) is lib
     other = tmp_path / "other.so"
     other.write_bytes(b"")
@@ -198,7 +199,8 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     assert ao(3, work=d, kv=2) == 1 and ao(3, work=d, tape=0x1004) == 1
     lib.dk_adjoint_many.argtypes = [P, I, I, I] + [P] * 10 + [F, I, I, P, P]
     am = lambda nw, k, kv=1, tape=None: lib.dk_adjoint_many(None, nw, k, 4, tape, *[None] * 9, 0.2, kv, 0, d, None)
-    assert am(0, 71) == 0 and am(-1, 71) == 1 and am(3, 0) == 1 and am(1 << 20, 1 << 12) == 1  # nw * ncot < 2^31
+    assert am(0, 71) == 0 and am(-1, 71) == 1 and am(3, 0) == 1 and am(1 << 20, 1 << 12) == 1
+    assert am(945196, 71) == 1 and am(1 << 20, 64) == 1  # nw * ncot * 64 work-items < 2^32 in one launch
     assert am(3, 71, kv=2) == 1 and am(3, 71, tape=0x1004) == 1
 
 
@@ -227,3 +229,113 @@ def test_device_counter_layout_matches_the_python_names():
         (torch_ffi.NONFINITE_QPOS, torch_ffi.NONFINITE_QVEL, torch_ffi.NONFINITE_CTRL, torch_ffi.NONFINITE_COT)
     assert val("NONFINITE_SHIFT") == torch_ffi.NONFINITE_SHIFT
     assert val("ADJ_REPLAY_MISMATCH") == torch_ffi.ADJ_REPLAY_MISMATCH
+
+
+# The autograd and operator plumbing of torch_ffi, run on the CPU in a child process whose library calls are replaced
+# by stand-ins before the operators are defined (the operators are process-wide, so the stand-ins must not leak into
+# other tests). The stand-ins are linear maps with known adjoints and record the options each call received.
+_PLUMBING = r'''
+import torch
+from nablaengine_amd import torch_ffi as F
+
+seen = []
+
+def fwd(qpos, qvel, warm, ctrl, friction, com, iterations, substeps, tape, kinematics):
+    B = qpos.shape[0]
+    q1 = qpos * 2.0 + friction[:, None]
+    v1 = torch.cat([qvel[:, :6] * 3.0, qvel[:, 6:] * 3.0 + ctrl], 1)
+    tp = torch.zeros((B if tape else 0, substeps * F.rec_words()))
+    kin = [torch.full((B, *s), 0.5) * q1[:, :1].reshape(B, *([1] * len(s))) for _, s in F._KIN_OUT] if kinematics else []
+    return [q1, v1, warm + 1.0, torch.full((B, 4), iterations, dtype=torch.int32), tp] + kin
+
+def bwd(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot, substeps, clamp_kv, normal, clamp_soft):
+    seen.append((clamp_kv, normal, round(clamp_soft, 6), ctrl is not None, len(kin_state), substeps))
+    gq = g_qpos * 2.0
+    if kin_state:
+        gq = gq + sum(c.reshape(c.shape[0], -1).sum(1, keepdim=True) for c in kin_cot) * 0.5
+    w = 1.0 + clamp_soft if clamp_kv == 2 else 1.0
+    return [gq, g_qvel * 3.0, g_qvel[:, 6:] * w, torch.zeros(g_qpos.shape[0], dtype=torch.int32)]
+
+F._KERNELS["forward"] = (fwd, F._KERNELS["forward"][1])
+F._KERNELS["backward"] = (bwd, F._KERNELS["backward"][1])
+B = 5
+g = torch.Generator().manual_seed(0)
+x = [torch.randn((B, n), generator=g) for n in (36, 35, 35, 29)] + [torch.rand(B, generator=g), torch.randn((B, 3), generator=g)]
+cq, cv = torch.randn((B, 36), generator=g), torch.randn((B, 35), generator=g)
+
+def loss(q, v, w, u, fr, c, **kw):
+    out = F.step(q, v, w, u, fr, c, **kw)
+    assert not out[2].requires_grad  # warm' is not differentiable
+    extra = (out[4] * 1.5).sum() if kw.get("kinematics") else 0.0
+    return (out[0] * cq).sum() + (out[1] * cv).sum() + extra
+
+def grads(f, **kw):
+    xs = [t.clone().requires_grad_(i in (0, 1, 3)) for i, t in enumerate(x)]
+    f(*xs, **kw).backward()
+    return [xs[i].grad for i in (0, 1, 3)]
+
+# eager: the options reach the backward, grad_decay scales the state's gradients only, the soft clamp's default delta
+gq, gv, gu = grads(loss, clamp_kv=2, normal=1, grad_decay=0.98, substeps=3)
+assert seen[-1] == (2, 1, 0.2, True, 0, 3), seen[-1]
+assert torch.equal(gq, (cq * 2.0) * 0.98) and torch.equal(gv, (cv * 3.0) * 0.98)
+assert torch.equal(gu, cv[:, 6:] * 1.2)
+grads(loss, clamp_kv=2, clamp_soft=0.05)
+assert seen[-1] == (2, 3, 0.05, True, 0, 4), seen[-1]
+grads(loss, clamp_kv=1, normal=0)
+assert seen[-1] == (1, 0, 0.0, False, 0, 4), seen[-1]
+# a loss on the kinematics outputs sends their cotangents (and the state for the kinematics VJP) to the backward
+gk = grads(loss, kinematics=True)
+assert seen[-1][4] == 2 and not torch.equal(gk[0], grads(loss)[0])
+# torch.compile(fullgraph=True): no graph break, the same gradients
+for kw in (dict(), dict(clamp_kv=2, grad_decay=0.5), dict(kinematics=True)):
+    torch._dynamo.reset()
+    f = lambda *a: loss(*a, **kw)
+    ex = torch._dynamo.explain(f)(*[t.clone().requires_grad_(i in (0, 1, 3)) for i, t in enumerate(x)])
+    assert ex.graph_break_count == 0, ex.break_reasons
+    torch._dynamo.reset()
+    cf = torch.compile(f, fullgraph=True, backend="aot_eager")
+    for a, b in zip(grads(cf), grads(f)):
+        assert torch.equal(a, b)
+# forward / backward outside autograd: outputs without grad, the options checked
+r = F.forward(*[t.requires_grad_(i == 0) for i, t in enumerate(x)], tape=True, kinematics=True)
+assert len(r) == 10 and not any(t.requires_grad for t in r)
+r = F.backward(r[4], x[4], x[5], cq, cv, clamp_kv=2, ctrl=x[3])
+assert seen[-1][:4] == (2, 3, 0.2, True) and len(r) == 4
+print("PLUMBING OK")
+'''
+
+
+def test_autograd_and_operator_plumbing_on_cpu():
+    """step's autograd node and the nablaengine operators on the CPU, the library calls replaced by linear stand-ins:
+    the options (clamp_kv, normal, the soft clamp's default and explicit delta, substeps) reach the backward call, ctrl
+    goes with clamp_kv 2 only, grad_decay multiplies the qpos / qvel gradients but not ctrl's, warm' is not
+    differentiable, cotangents of the kinematics outputs reach the backward with the output state, and
+    torch.compile(fullgraph=True) traces it with no graph break and the eager gradients."""
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    r = subprocess.run([sys.executable, "-c", _PLUMBING], capture_output=True, text=True, cwd=ROOT, timeout=600)
+    assert r.returncode == 0 and "PLUMBING OK" in r.stdout, r.stdout[-2000:] + r.stderr[-4000:]
+
+
+def test_scale_grad():
+    """scale_grad is the identity on a pytree (float tensors bitwise, other leaves the same objects) whose float
+    tensors' cotangents are multiplied by gamma in float32; a non-finite gamma is a ValueError (the reference's
+    scale_grad, torch_ffi.py:868-899)."""
+    import torch
+    from nablaengine_amd import torch_ffi
+    a = torch.randn(7, 3, requires_grad=True)
+    b = torch.randn(4, dtype=torch.float64, requires_grad=True)
+    n = torch.arange(5)
+    tree = {"a": a, "pair": (b, n), "k": 3}
+    out = torch_ffi.scale_grad(tree, 0.98)
+    assert set(out) == {"a", "pair", "k"} and out["k"] == 3 and out["pair"][1] is n
+    assert torch.equal(out["a"], a) and torch.equal(out["pair"][0], b)
+    wa, wb = torch.randn(7, 3), torch.randn(4, dtype=torch.float64)
+    ((out["a"] * wa).sum() + (out["pair"][0] * wb).sum()).backward()
+    assert torch.equal(a.grad, wa * 0.98) and torch.equal(b.grad, wb * 0.98)
+    c = torch.randn(3, requires_grad=True)
+    (torch_ffi.scale_grad(torch_ffi.scale_grad(c, 0.5), 0.25) * 2.0).sum().backward()
+    assert torch.equal(c.grad, torch.full((3,), 2.0) * 0.25 * 0.5)
+    for bad in (float("nan"), float("inf")):
+        with pytest.raises(ValueError):
+            torch_ffi.scale_grad(tree, bad)

@@ -134,7 +134,7 @@ def test_fused_counters_equal_the_separate_kernels(ffi):
     the same 18 counters."""
     import ctypes
     import torch
-    lib = ffi._STATE["lib"]
+    lib = ffi.load_library()
     for name in ("dk_torch_diag_fwd", "dk_torch_diag_bwd", "dk_fwd_forward_diag", "dk_adjoint_work_diag"):
         assert hasattr(lib, name)
     B, nsub, it = 1000, 4, 10

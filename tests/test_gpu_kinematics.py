@@ -77,7 +77,7 @@ def test_kinematics_vjp_vs_oracle_fd(ffi):
     for block in (0, 1, 2, 3, 4, None):
         cot = [rng.normal(0, 1, s).astype(np.float32) if block in (None, k) else np.zeros(s, np.float32)
                for k, s in enumerate(shapes)]
-        gq, gv = ffi._kinematics_backward_impl(q, v, c3, *map(_t, cot))
+        gq, gv = ffi._ops().kinematics_backward(q, v, c3, *map(_t, cot))
         torch.cuda.synchronize()
         rq, rv = oracle.kinematics_vjp(st["qpos"].astype(np.float64), st["qvel"].astype(np.float64),
                                        st["com"].astype(np.float64), [c.astype(np.float64) for c in cot])
@@ -129,7 +129,7 @@ def test_kinematics_autograd_and_edges(ffi):
     out = ffi.kinematics(q, v, c3)
     w = [torch.randn_like(o) for o in out]
     sum((a * b).sum() for a, b in zip(out, w)).backward()
-    gq, gv = ffi._kinematics_backward_impl(q.detach(), v.detach(), c3, *w)
+    gq, gv = ffi._ops().kinematics_backward(q.detach(), v.detach(), c3, *w)
     assert torch.equal(q.grad, gq) and torch.equal(v.grad, gv)
     e = ffi.kinematics(_t(st["qpos"][:0]), _t(st["qvel"][:0]), _t(st["com"][:0]))
     assert e[1].shape == (0, 31, 3) and e[3].shape == (0, 31, 6)
