@@ -7,7 +7,7 @@ Every array is data the reference's own checks hold (MuJoCo C float64 truth and 
   (benchmarks/data/truth/README.md, benchmarks/bench/truth/fdlib.py model_job);
 - grad_<corpus>.npz (mf_s0, mf_s1): the sampled gradient states: inputs, the 3 stored output cotangents, MuJoCo C
   FD VJPs `fd_vjp` (h = 1e-6) and `fd_vjp_floor` (h = 1e-7), validity bits `bad`, groups G0/G4/G5/G6, outputs `out`;
-  the first 16 G0 states' full 71 x 99 step Jacobian `jacobian` with `jac_index`;
+  all 64 G0 states' full 71 x 99 step Jacobian `jacobian` (float32) with `jac_index` and `jacobian_dcol`;
 - mjw_<corpus>.npz (mf_s0): MuJoCo Warp 3.17 float32 contacts at the input state (`con`: pair, dist, pos[3],
   normal[3]) and per-substep counts for the first 512 states (fixtures/mjlab/mjw317_mf_s0.npz);
 - corpus_mf_s0.npz: the inputs of all 4096 states of the benchmark corpus mf_s0 (benchmarks/data/mf_s0.npz), the
@@ -35,8 +35,8 @@ def main():
                             **{k: c[k][ix] for k in INPUTS})
         if cname in ("mf_s0", "mf_s1"):
             gi = t["index"]
-            ji = t["jac_index"][:16]  # 16 of the 64 G0 Jacobians keep the fixture small
-            extra = dict(jac_index=ji, jacobian=t["jacobian"][:16], jacobian_dcol=t["jacobian_dcol"][:16])
+            ji = t["jac_index"]  # every Jacobian the truth holds (64 G0 states)
+            extra = dict(jac_index=ji, jacobian=t["jacobian"], jacobian_dcol=t["jacobian_dcol"])
             np.savez_compressed(os.path.join(OUT, f"grad_{cname}.npz"), index=gi, out=t["out"], fd_vjp=t["fd_vjp"],
                                 fd_vjp_floor=t["fd_vjp_floor"], bad=t["bad"], model_flags=t["model_flags"][gi],
                                 cot_qpos=c["cot_qpos"][gi], cot_qvel=c["cot_qvel"][gi],

@@ -428,3 +428,67 @@ def test_flop_count_closed_form():
     st = synthetic.states(32, config=1, dtype=np.float64)
     r = oracle.step(**st, **oracle.ENGINE, flops=True)
     assert (r[4] >= 4 * (2.5e4 + 6.2e4 + 5e3)).all() and (r[4] < 1e7).all()
+
+
+def _jac_state(z, j):
+    s = z["jac_index"][j]
+    return ([z[k][s].astype(np.float64) for k in ("qpos", "qvel", "qacc_warmstart", "ctrl")]
+            + [float(z["friction"][s]), z["com"][s].astype(np.float64)])
+
+
+def test_fd_vjp_is_the_contracted_fd_jacobian():
+    """fd_vjp (all perturbed steps of a batch in one step_mt call) equals the output cotangents times fd_jacobian's
+    columns (each state's perturbed steps in one step call) to 1e-12, on config-1 and contact-heavy config-4 states:
+    the batched FD the GPU's FD gates use is the textbook central difference."""
+    for config, n in ((1, 3), (4, 3)):
+        st = {k: v.astype(np.float64) for k, v in synthetic.states(n, config=config, seed=7).items()}
+        cq, cv = (x.astype(np.float64) for x in synthetic.cotangents(n, seed=8))
+        fd = oracle.fd_vjp(st["qpos"], st["qvel"], st["warm"], st["ctrl"], st["friction"], st["com"], cq, cv,
+                           threads=3, **oracle.ENGINE)
+        for b in range(n):
+            J = oracle.fd_jacobian(*(st[k][b] for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")),
+                                   **oracle.ENGINE)
+            ref = np.concatenate([cq[b], cv[b]]) @ J
+            assert np.linalg.norm(fd[b] - ref) <= 1e-12 * np.linalg.norm(ref), (config, b)
+
+
+@pytest.mark.parametrize("threads", [1, 3, 16])
+def test_step_mt_is_step_bitwise(threads):
+    """step_mt (the worlds split in contiguous shares over host threads: the CPU baseline's all-threads leg and
+    fd_vjp's engine) gives bitwise step's outputs and info, every world being independent; on 40 config-1 and
+    config-4 worlds (more threads than worlds of a share included)."""
+    st = {k: np.concatenate([synthetic.states(20, config=c, seed=11)[k] for c in (1, 4)]).astype(np.float64)
+          for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")}
+    ref = oracle.step(**st, **oracle.ENGINE)
+    got = oracle.step_mt(threads, **st, **oracle.ENGINE)
+    for a, b in zip(got, ref):
+        assert a.dtype == b.dtype and np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+@pytest.mark.parametrize("cname", ["mf_s0", "mf_s1"])
+def test_fd_jacobian_matches_the_mujoco_jacobian(cname):
+    """The oracle's central-difference Jacobian (integrate_pos qpos columns, at the truth's solver settings) against
+    MuJoCo C's float64 FD Jacobian the truth stores (float32) for all its 64 G0 states, scored as the reference's
+    jacobian_errors (benchmarks/bench/accuracy/gradient.py:193-208): per block (qpos tangent, qvel, ctrl) the
+    Frobenius relative error over the valid columns. Median <= 2e-7 per block (measured 2.4e-8 to 3.2e-8, the truth's
+    float32 storage), every state within max(3e-5, 2 x the truth's floor |J(1e-6) - J(1e-7)|) (measured max 1.5e-5);
+    a column permutation (a transposed operand) fails it."""
+    z = np.load(os.path.join(GOLD, f"grad_{cname}.npz"))
+    blocks = {"qpos": slice(0, 35), "qvel": slice(35, 70), "ctrl": slice(70, 99)}
+    errs = {name: [] for name in blocks}
+    for j in range(len(z["jac_index"])):
+        J = oracle.fd_jacobian(*_jac_state(z, j), **oracle.TRUTH)
+        Jt = z["jacobian"][j].astype(np.float64)
+        valid = z["bad"][z["jac_index"][j]] == 0
+        for name, sl in blocks.items():
+            v = valid[sl]
+            a, b = J[:, sl][:, v], Jt[:, sl][:, v]
+            nb = max(np.linalg.norm(b), 1e-9)
+            floor = np.linalg.norm(z["jacobian_dcol"][j, sl][v]) / nb
+            e = np.linalg.norm(a - b) / nb
+            errs[name].append(e)
+            assert e <= max(3e-5, 2 * floor), (cname, j, name, e, floor)
+            assert np.linalg.norm(a[:, ::-1] - b) / nb > 1e-2
+    assert len(z["jac_index"]) == 64
+    for name, e in errs.items():
+        assert np.median(e) <= 2e-7, (name, np.median(e))
