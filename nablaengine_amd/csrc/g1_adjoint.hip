@@ -534,11 +534,16 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     float rt[3];
     qrot(dq, t, rt);  // t = R(dq) t'
     for (int k = 0; k < 3; k++) s.qn[3 + k] = rt[k];
-    // J_r(phi)' t' = t' + c1 phi x t' + c2 phi x (phi x t'), c1 = (1 - cos th) / th^2, c2 = (th - sin th) / th^3, with
-    // cos th and sin th from the half angle's sine and cosine above (1 - cos th = 2 sin^2(th / 2): no cancellation)
+    // J_r(phi)' t' = t' + c1 phi x t' + c2 phi x (phi x t'), c1 = (1 - cos th) / th^2, c2 = (th - sin th) / th^3.
+    // Below th = 0.5 both are their Taylor series through th^8 (what is left out is below 5e-12 relative).
+    // Above it, cos th and sin th come from the half angle's sine and cosine: 1 - cos th = 2 sin^2(th / 2) has no
+    // cancellation, and th - sin th >= th^3 / 6 - th^5 / 120 keeps c2's rounding error below 2e-6 relative there.
     float c1, c2;
-    if (th < 1e-2f) { c1 = 0.5f - th * th / 24.f; c2 = 1.f / 6.f - th * th / 120.f; }
-    else {
+    if (th < 0.5f) {
+      const float x = th * th;
+      c1 = 0.5f + x * (-1.f / 24.f + x * (1.f / 720.f + x * (-1.f / 40320.f + x * (1.f / 3628800.f))));
+      c2 = 1.f / 6.f + x * (-1.f / 120.f + x * (1.f / 5040.f + x * (-1.f / 362880.f + x * (1.f / 39916800.f))));
+    } else {
       const float i2 = 1.f / (th * th);
       c1 = 2.f * sn * sn * i2;
       c2 = (th - 2.f * sn * cs) * i2 / th;

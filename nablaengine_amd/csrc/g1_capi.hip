@@ -210,7 +210,8 @@ int dk_adjoint_work_ordered(hipStream_t st, int nw, int nsub, const float* tape,
 int dk_adjoint_many(hipStream_t st, int nw, int ncot, int nsub, const float* tape, const float* fric, const float* com,
                     const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                     const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, unsigned long long* d) {
-  if (nw < 0 || ncot < 1 || (long long)nw * ncot > 0x7fffffffLL || nsub < 1 || nsub > 32 || clamp_kv < 0 ||
+  // one launch of nw * ncot workgroups of 64 work-items: HIP takes fewer than 2^32 work-items a launch
+  if (nw < 0 || ncot < 1 || (long long)nw * ncot * 64 >= (1LL << 32) || nsub < 1 || nsub > 32 || clamp_kv < 0 ||
       clamp_kv > 2 || normal < 0 || normal > 3)
     return (int)hipErrorInvalidValue;
   if (clamp_kv == 2 && !ctrl) return (int)hipErrorInvalidValue;
