@@ -26,7 +26,10 @@ backprop through time, checkpoint segments of 8 steps, and its capped world-step
 closed-form phase counts on the same inputs, counted once before timing, per world-step x B) divided by k_forward's
 mean duration, timed live here with HIP events around K back-to-back launches of the forward alone (the order
 computed once before, dk_fwd_forward_ordered); peak is MI355X's FP32 (157.3 TFLOP/s). `traffic` is k_forward's HBM
-bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (the committed summary). `cpu_baseline` is the float64 CPU
+bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (the committed summary). `roofline_adjoint` is the same for
+k_adjoint, the VJP's kernel: the float64 restatement's closed-form count of the adjoint's flops (default variant)
+over k_adjoint's mean duration, timed live around back-to-back launches with one dispatch order, and its HBM rate (the
+tape read plus the adjoint's interface bytes) against 8 TB/s. `cpu_baseline` is the float64 CPU
 restatement ("port"), timed with the same round protocol: one thread on the 64 worlds of config 0 (the reference's
 single-thread CPU case) and, in `all_threads`, the host's usable cores (len(os.sched_getaffinity(0)), at most 16: the
 GPU box's CPU share) on 4096 config-0 worlds (the reference's batched CPU case).
@@ -52,18 +55,22 @@ IO_BYTES_FWD = (36 + 35 + 35 + 29 + 1 + 3) * 4 + (36 + 35 + 35) * 4 + 16
 # HBM bytes per k_forward launch at 4096 worlds, measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (two runs,
 # each scaled by the same counter's reading on a copy of known size, `--copy-mib`); the summary holds the command
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_forward_4096_traffic.md")
+# the adjoint's interface bytes per world-step (cotangents 284 B and friction / com 16 B in, gradients 400 B and
+# info 4 B out) and the tape it reads (4 substeps x 1472 float32 words)
+IO_BYTES_VJP = (36 + 35 + 1 + 3) * 4 + (36 + 35 + 29) * 4 + 4
+TAPE_BYTES = 4 * 1472 * 4
 CORPUS = os.path.join(ROOT, "tests", "golden", "corpus_mf_s0.npz")
 KEYS = ("qpos", "qvel", "warm", "ctrl", "friction", "com")
 ROUNDS, WARM_CALLS, WARM_S, ROUND_S, MAX_CALLS = 5, 5, 1.0, 0.25, 200
 
 
-def measured_traffic(worlds):
-    """Bytes per k_forward launch from the committed traffic summary (line `traffic_bytes_per_launch: N`), or None
-    when there is none for this world count."""
+def measured_traffic(worlds, key="traffic_bytes_per_launch"):
+    """Bytes per launch from the committed traffic summary (line `<key>: N`; k_forward's by default,
+    traffic_bytes_per_launch_adjoint for k_adjoint), or None when there is none for this world count."""
     if worlds != 4096 or not os.path.exists(TRAFFIC_FILE):
         return None
     for line in open(TRAFFIC_FILE):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(key + ":"):
             return int(line.split(":")[1])
     return None
 
@@ -153,6 +160,18 @@ def algorithmic_flops(st):
     return float(np.mean(r[4]))
 
 
+def algorithmic_flops_vjp(st):
+    """Mean algorithmic flops per world-step of the VJP of these states' steps (the interface's default variant,
+    clamp_kv 0, normal 3; closed-form counts of the float64 restatement's adjoint)."""
+    import oracle
+    from nablaengine_amd import synthetic, torch_ffi
+    s64 = {k: v.astype(np.float64) for k, v in st.items()}
+    cq, cv = (x.astype(np.float64) for x in synthetic.cotangents(len(st["qpos"])))
+    r = oracle.vjp(**s64, g_qpos=cq, g_qvel=cv, clamp_kv=torch_ffi.CLAMP_KV, normal=torch_ffi.NORMAL,
+                   **oracle.ENGINE, flops=True)
+    return float(np.mean(r[3]))
+
+
 def timed(fn, steps, warmup, stream):
     """Mean ms per call of fn over `steps` back-to-back calls (HIP events on `stream`), after `warmup` calls."""
     import torch
@@ -187,8 +206,8 @@ def _calls(st):
 
 
 def measure(B, steps, warmup, kernel=False, rounds=True):
-    """(forward ms, fwd+VJP ms, k_forward ms or None, info of the last forward, round-protocol stats or None) at B
-    worlds of config 1."""
+    """(forward ms, fwd+VJP ms, k_forward ms or None, k_adjoint ms or None, info of the last forward, round-protocol
+    stats or None) at B worlds of config 1."""
     import torch
     from nablaengine_amd import synthetic, torch_ffi
     st = synthetic.states(B, config=1)
@@ -197,7 +216,7 @@ def measure(B, steps, warmup, kernel=False, rounds=True):
     ms = timed(fwd, steps, warmup, stream)
     info = out["r"][3].cpu().numpy()
     vjp_ms = timed(vjp, steps, warmup, stream)
-    kms = None
+    kms = ams = None
     if kernel:  # k_forward alone: the order once, then the ordered launches back to back
         lib = torch_ffi.load_library()
         st_ = ctypes.c_void_p(stream.cuda_stream)
@@ -212,8 +231,23 @@ def measure(B, steps, warmup, kernel=False, rounds=True):
             assert lib.dk_fwd_forward_ordered(st_, B, *map(p, args), 10, 4, p(q1), p(v1), p(w1), p(inf), None, None,
                                               p(work)) == 0
         kms = timed(kern, steps, warmup, stream)
+        # k_adjoint alone: one tape and the adjoint's order once, then the ordered launches back to back, with the
+        # diagnostic counting on (as torch_ffi.backward launches it)
+        tape = torch_ffi.forward(*args, tape=True)[4]
+        gq, gv = (torch.from_numpy(x).cuda() for x in synthetic.cotangents(B))
+        bq, bv, bu = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 29), **kw)
+        binf = torch.empty((B,), dtype=torch.int32, device="cuda")
+        awork = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+        counters = torch.zeros(len(torch_ffi.DIAG), dtype=torch.int64, device="cuda")
+        assert lib.dk_adjoint_order(st_, B, 4, p(tape), p(awork)) == 0
+
+        def adj():
+            assert lib.dk_adjoint_work_ordered(st_, B, 4, p(tape), p(args[4]), p(args[5]), p(gq), p(gv), p(bq), p(bv),
+                                               p(bu), p(binf), None, 0.0, torch_ffi.CLAMP_KV, torch_ffi.NORMAL,
+                                               p(awork), p(counters)) == 0
+        ams = timed(adj, steps, warmup, stream)
     rs = {"forward": protocol_gpu(fwd, stream), "fwd_vjp": protocol_gpu(vjp, stream)} if rounds else None
-    return ms, vjp_ms, kms, info, rs
+    return ms, vjp_ms, kms, ams, info, rs
 
 
 def measure_corpus():
@@ -310,10 +344,11 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     B = a.worlds
-    ms, vjp_ms, kms, info, rs = measure(B, a.steps, a.warmup, kernel=True, rounds=not a.no_rounds)
+    ms, vjp_ms, kms, ams, info, rs = measure(B, a.steps, a.warmup, kernel=True, rounds=not a.no_rounds)
     big = None
     if not a.no_16k and B != 16384:
-        bms, bvjp, _, binfo, brs = measure(16384, max(a.steps // 4, 3), max(a.warmup // 4, 2), rounds=not a.no_rounds)
+        bms, bvjp, _, _, binfo, brs = measure(16384, max(a.steps // 4, 3), max(a.warmup // 4, 2),
+                                              rounds=not a.no_rounds)
         big = {"worlds": 16384, "ms_per_step": bms, "ms_per_step_fwd_vjp": bvjp,
                "world_steps_per_s": 16384e3 / bms, "world_steps_per_s_fwd_vjp": 16384e3 / bvjp}
         if brs:
@@ -322,6 +357,9 @@ def main():
     sub = {k: v[: a.flop_sample] for k, v in st.items()}
     fl = algorithmic_flops(sub)
     achieved = fl * B / (kms * 1e-3) / 1e12
+    fla = algorithmic_flops_vjp(sub)
+    adj_achieved = fla * B / (ams * 1e-3) / 1e12
+    adj_bytes = TAPE_BYTES + IO_BYTES_VJP  # per world-step: the tape read plus the adjoint's interface bytes
     res = {
         "metric": METRIC, "value": B * 1e3 / ms, "unit": "world-steps/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -341,6 +379,20 @@ def main():
         "roofline_hbm": {"achieved": IO_BYTES_FWD * B / (kms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": IO_BYTES_FWD * B / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                          "note": f"interface bytes {IO_BYTES_FWD} per world-step"},
+        "ms_k_adjoint": ams,
+        "roofline_adjoint": {"bound": "mfma", "achieved": adj_achieved, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                             "frac": adj_achieved / PEAK_FP32_TFLOPS,
+                             "traffic": measured_traffic(B, "traffic_bytes_per_launch_adjoint"),
+                             "hbm": {"achieved": adj_bytes * B / (ams * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
+                                     "unit": "GB/s", "frac": adj_bytes * B / (ams * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                     "bytes_per_world_step": adj_bytes},
+                             "note": "k_adjoint, the VJP's kernel (FP32 vector work; fp32 MFMA for the subtree sums "
+                                     "only): achieved = closed-form algorithmic flops of the VJP (" f"{fla:.3g}"
+                                     " per world-step, the float64 restatement's adjoint count on "
+                                     f"{len(sub['qpos'])} of the worlds, default variant) x worlds / k_adjoint's mean "
+                                     "duration (HIP events around back-to-back launches with one dispatch order, its "
+                                     "stream); hbm: the tape read (4 substeps x 1472 words) plus the interface's "
+                                     f"{IO_BYTES_VJP} bytes per world-step over the same duration"},
         "capacity": {"contacts_max": int(info[:, 1].max()), "rows_max": int(info[:, 2].max()),
                      "overflow_worlds": int(((info[:, 3] & 20) != 0).sum())},
     }

@@ -68,6 +68,7 @@ def lib():
                               dp]
         L.g1o_vjp_ex.argtypes = (L.g1o_vjp.argtypes[:17] + [ctypes.c_double, ctypes.c_double]
                                  + L.g1o_vjp.argtypes[17:])
+        L.g1o_vjp_count.argtypes = L.g1o_vjp_ex.argtypes + [dp]
         L.g1o_contacts.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp]
         L.g1o_kinematics.argtypes = [ctypes.c_int] + [dp] * 8
         L.g1o_substep_hessian.argtypes = [dp, dp, dp, dp, ctypes.c_double, dp, ctypes.c_int, ctypes.c_double,
@@ -184,21 +185,23 @@ NPAIR = 502  # the model's collision pairs (the freeze hook's table rows)
 
 
 def vjp(qpos, qvel, warm, ctrl, friction, com, g_qpos, g_qvel, clamp_kv=1, normal=0, clamp_soft=0.2, iterations=10,
-        tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4, normal_eps=1e-3, parallel_eps=1.2e-3):
+        tol=1e-8, ls_max=40, ls_tol=1e-7, nsub=4, normal_eps=1e-3, parallel_eps=1.2e-3, flops=False):
     """Analytic VJP of one control step in float64 (the oracle's adjoint): (g_qpos (B, 36) qpos form, g_qvel (B, 35),
     g_ctrl (B, 29)) from the output cotangents (g_qpos' (B, 36) qpos form, g_qvel' (B, 35)). normal_eps and
     parallel_eps are the eps of the normal options 2 / 3 and the near-parallel rule's sin^2 threshold (the reference's
-    compile-time 1e-3 m and 1.2e-3, which the GPU library uses); the checker varies them to pin the options."""
+    compile-time 1e-3 m and 1.2e-3, which the GPU library uses); the checker varies them to pin the options.
+    flops=True also returns each world-step VJP's algorithmic flops (B,) last: closed-form phase counts of what the
+    adjoint computes from the records (g1_oracle.cpp VJP_FLOPS_*), the forward's step(flops=True) counterpart."""
     qpos = _c(qpos, (-1, NQ))
     B = qpos.shape[0]
     qvel, warm, ctrl = _c(qvel, (B, NV)), _c(warm, (B, NV)), _c(ctrl, (B, NU))
     friction, com = _c(friction, (B,)), _c(com, (B, 3))
     gq, gv = _c(g_qpos, (B, NQ)), _c(g_qvel, (B, NV))
-    oq, ov, ou = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NU))
-    lib().g1o_vjp_ex(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
-                     int(ls_max), float(ls_tol), int(nsub), _p(gq), _p(gv), int(clamp_kv), int(normal),
-                     float(clamp_soft), float(normal_eps), float(parallel_eps), _p(oq), _p(ov), _p(ou))
-    return oq, ov, ou
+    oq, ov, ou, fl = np.empty((B, NQ)), np.empty((B, NV)), np.empty((B, NU)), np.empty(B)
+    lib().g1o_vjp_count(B, _p(qpos), _p(qvel), _p(warm), _p(ctrl), _p(friction), _p(com), int(iterations), float(tol),
+                        int(ls_max), float(ls_tol), int(nsub), _p(gq), _p(gv), int(clamp_kv), int(normal),
+                        float(clamp_soft), float(normal_eps), float(parallel_eps), _p(oq), _p(ov), _p(ou), _p(fl))
+    return (oq, ov, ou, fl) if flops else (oq, ov, ou)
 
 
 def fd_jacobian(qpos, qvel, warm, ctrl, friction, com, h=1e-6, **kw):

@@ -53,6 +53,7 @@ struct World {
   double aadv[NV];    // implicitfast's a_adv of the last substep
   bool clamped[NV];   // dofs whose actuator force is at its limit
   double flops;  // algorithmic flops of the world-step so far (the closed-form phase counts, see count_* below)
+  double aflops;  // algorithmic flops of the world-step's VJP so far (closed form, VJP_FLOPS_* below)
   // The checker's own hooks, inert at their defaults (no part of the reference's step): qfrc, a generalized force
   // added to qfrc_smooth (NV, or NULL), so that finite differences in it measure the adjoint's lambda; freeze, per
   // capsule-capsule pair (flag, x1, x2): with freeze_mode 1 the forward records the segment parameters of every pair
@@ -1015,6 +1016,27 @@ void contact_geom_vjp(const World& s, const Contact& c, double db, const double*
 
 struct Rec { double qpos[NQ], qvel[NV], astar[NV], aadv[NV]; };
 
+// Algorithmic flops of one substep's VJP (closed form, FMA = 2; counted by substep_vjp as step counts the forward's):
+// what the adjoint computes from the substep's record, not this restatement's recomputation of the record.
+//  - pose replay (forward kinematics of the 30 hinge bodies: the hinge rotation's sincos ~20, two quaternion products
+//    56, the body offset rotated into the world and added 33): 30 x 110 = 3.3e3
+//  - integrator VJP (the root's exp map: a rotation 30, J_r' t with two cross products ~80; v bar += h q bar 70): 2e2
+//  - implicitfast and IFT solves: two triangular solve pairs with 35 x 35 factors, 2 x 2 x 35^2 = 4.9e3, and
+//    a* bar = a_adv bar - h kv y, 70: 4.97e3
+//  - twists of v, lambda, y, a*, a~ down the tree (12 per body and channel) and the RNE acceleration's velocity
+//    products (30 per body for each of the 2 channels that carry them): 30 x (5 x 12 + 2 x 30) = 3.6e3
+//  - per-body force vectors f1, P, Q, R, T, f2, P2 (inertia products ~60, cross products ~30): 30 x 350 = 1.05e4
+//  - subtree sums of 12 spatial vectors (72 floats per body): 30 x 72 = 2.2e3
+//  - per dof projections (3 motion cross products 90, 12 six-vector dot products 132, 3 force cross products 90,
+//    sums 48): 35 x 360 = 1.26e4
+//  - actuators: 29 x 8 = 2.3e2
+// plus VJP_FLOPS_LIMIT per limit row in the quadratic zone, and per contact with a row in it VJP_FLOPS_CONTACT
+// (impedance and its derivative 40, relative twists 18, the three wrench channels onto both bodies 228, the primitive
+// and frame VJP 250, the geom wrenches 34) and VJP_FLOPS_ROW per such row (its direction and moment, dot products,
+// the D terms, Psi's cotangent of the row).
+constexpr double VJP_FLOPS_SUBSTEP = 3.3e3 + 2e2 + 4.97e3 + 3.6e3 + 1.05e4 + 2.2e3 + 1.26e4 + 2.3e2;
+constexpr double VJP_FLOPS_LIMIT = 25, VJP_FLOPS_CONTACT = 570, VJP_FLOPS_ROW = 90;
+
 // one substep's VJP: (qb tangent, vb) of its output -> of its input; ub accumulates the ctrl gradient
 void substep_vjp(World& s, const Rec& rec, const double* ctrl, double* qb, double* vb, double* ub, int clamp_kv,
                  int normal, double clamp_soft) {
@@ -1025,6 +1047,7 @@ void substep_vjp(World& s, const Rec& rec, const double* ctrl, double* qb, doubl
   collision(s);
   rows(s);
   const double* as = rec.astar;
+  s.aflops += VJP_FLOPS_SUBSTEP;
   // 1. integrator: v' = v + h a_adv, q' = q (+) h v'
   double vt[NV], qn[NV];
   for (int i = 0; i < NV; i++) { vt[i] = vb[i]; qn[i] = qb[i]; }
@@ -1117,6 +1140,7 @@ void substep_vjp(World& s, const Rec& rec, const double* ctrl, double* qb, doubl
     if (!(std::fmin(dmin, dmax) < 0)) continue;
     if (r >= s.nefc) break;
     if (jar[r] < 0) {
+      s.aflops += VJP_FLOPS_LIMIT;
       double sg = dmin < dmax ? 1 : -1, pos = std::fmin(dmin, dmax), k, b, imp, dimp;
       kbimp(JNT_SOLREF, JNT_SOLIMP, pos, h, &k, &b, &imp);
       imp_d(JNT_SOLIMP, pos, &imp, &dimp);
@@ -1136,6 +1160,7 @@ void substep_vjp(World& s, const Rec& rec, const double* ctrl, double* qb, doubl
     bool act = false;
     for (int t = 0; t < nr && r0 + t < s.nefc; t++) act |= jar[r0 + t] < 0;
     if (!act) continue;
+    s.aflops += VJP_FLOPS_CONTACT;
     double k, b, imp, dimp;
     kbimp(PAIR_SOLREF, PAIR_SOLIMP, ct.dist, h, &k, &b, &imp);
     imp_d(PAIR_SOLIMP, ct.dist, &imp, &dimp);
@@ -1149,6 +1174,7 @@ void substep_vjp(World& s, const Rec& rec, const double* ctrl, double* qb, doubl
     Sv OmL = sv0(), OmA = sv0();
     for (int t = 0; t < nr && r0 + t < s.nefc; t++) {
       if (!(jar[r0 + t] < 0)) continue;
+      s.aflops += VJP_FLOPS_ROW;
       double sg = (t & 1) ? -1 : 1, u[3];
       const double* tk = ct.frame + 3 * (1 + (t >> 1));
       for (int q = 0; q < 3; q++) u[q] = ct.dim == 3 ? ct.frame[q] + sg * mu * tk[q] : ct.frame[q];
@@ -1461,10 +1487,11 @@ int g1o_contacts(const double* qpos, const double* qvel, const double* ctrl, con
 // outputs gq_out (nw, 36) qpos form, gv_out (nw, 35); gradients gq_in (nw, 36) qpos form (its quaternion part
 // 2 q (x) (0, t) of the tangent cotangent t), gv_in (nw, 35), gu (nw, 29). clamp_kv 0 / 1 / 2, normal 0..3 as the
 // reference's adjoint options; clamp_soft the soft clamp's delta.
-int g1o_vjp_ex(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
-               const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
-               const double* gq_out, const double* gv_out, int clamp_kv, int normal, double clamp_soft,
-               double normal_eps, double parallel_eps, double* gq_in, double* gv_in, double* gu) {
+// g1o_vjp_ex with the algorithmic flops of each world-step's VJP (closed form, VJP_FLOPS_*) in flops (nw) or NULL
+int g1o_vjp_count(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
+                  const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol,
+                  int nsub, const double* gq_out, const double* gv_out, int clamp_kv, int normal, double clamp_soft,
+                  double normal_eps, double parallel_eps, double* gq_in, double* gv_in, double* gu, double* flops) {
   World* s = new World;
   init_hooks(*s);
   s->normal_eps = normal_eps;
@@ -1477,6 +1504,7 @@ int g1o_vjp_ex(int nw, const double* qpos, const double* qvel, const double* war
     std::memcpy(s->com, com + (size_t)w * 3, sizeof(double) * 3);
     s->fric = fric[w];
     s->flags = 0;
+    s->aflops = 0;
     const double* u = ctrl + (size_t)w * NU;
     for (int k = 0; k < nsub; k++) {
       std::memcpy(rec[k].qpos, s->qpos, sizeof(rec[k].qpos));
@@ -1515,10 +1543,19 @@ int g1o_vjp_ex(int nw, const double* qpos, const double* qvel, const double* war
     for (int i = 6; i < NV; i++) o[i + 1] = qb[i];
     std::memcpy(gv_in + (size_t)w * NV, vb, sizeof(double) * NV);
     std::memcpy(gu + (size_t)w * NU, ub, sizeof(double) * NU);
+    if (flops) flops[w] = s->aflops;
   }
   delete[] rec;
   delete s;
   return 0;
+}
+
+int g1o_vjp_ex(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl,
+               const double* fric, const double* com, int iterations, double tol, int ls_max, double ls_tol, int nsub,
+               const double* gq_out, const double* gv_out, int clamp_kv, int normal, double clamp_soft,
+               double normal_eps, double parallel_eps, double* gq_in, double* gv_in, double* gu) {
+  return g1o_vjp_count(nw, qpos, qvel, warm, ctrl, fric, com, iterations, tol, ls_max, ls_tol, nsub, gq_out, gv_out,
+                       clamp_kv, normal, clamp_soft, normal_eps, parallel_eps, gq_in, gv_in, gu, nullptr);
 }
 
 int g1o_vjp(int nw, const double* qpos, const double* qvel, const double* warm, const double* ctrl, const double* fric,

@@ -430,6 +430,22 @@ def test_flop_count_closed_form():
     assert (r[4] >= 4 * (2.5e4 + 6.2e4 + 5e3)).all() and (r[4] < 1e7).all()
 
 
+def test_vjp_flop_count_closed_form():
+    """The VJP's algorithmic flop count: per world-step 4 x 3.76e4 for the smooth parts, plus 25 per limit row, 570 per
+    contact and 90 per row in the quadratic zone; so at least 1.5e5 and below 1e6 on config-1 and config-4 states,
+    larger where there are contacts; and counting leaves the gradients bitwise unchanged."""
+    for config in (1, 4):
+        st = synthetic.states(24, config=config, dtype=np.float64)
+        cq, cv = (x.astype(np.float64) for x in synthetic.cotangents(24))
+        r = oracle.vjp(**st, g_qpos=cq, g_qvel=cv, flops=True)
+        plain = oracle.vjp(**st, g_qpos=cq, g_qvel=cv)
+        assert all(np.array_equal(a, b) for a, b in zip(r[:3], plain))
+        fl = r[3]
+        assert (fl >= 4 * 3.76e4).all() and (fl < 1e6).all() and (fl > 4 * 3.76e4).any()
+        _, _, _, info = oracle.step(**st, **oracle.ENGINE)
+        assert np.corrcoef(fl, info[:, 1])[0, 1] > 0.5  # more contacts, more flops
+
+
 def _jac_state(z, j):
     s = z["jac_index"][j]
     return ([z[k][s].astype(np.float64) for k in ("qpos", "qvel", "qacc_warmstart", "ctrl")]
