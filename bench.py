@@ -141,8 +141,14 @@ def cpu_baseline():
     big = synthetic.states(4096, config=0, dtype=np.float64)
     many = protocol_cpu(lambda: oracle.step_mt(threads, **big, **oracle.ENGINE))
     settings = "float64 CPU restatement, not MuJoCo; Newton 10 it, tol 1e-8, line search 40 / 1e-7 (the engine's)"
+    published = {"note": "the reference's MuJoCo C 3.17 timings on an AMD EPYC 9555, 16 threads allowed "
+                         "(docs/results/paper_rtx6000/paper_bench.md:5,28-29), "
+                         "not measured here: this port, with dense constraint Jacobians and 40 line-search "
+                         "evaluations, is about 2.8x slower per thread than MuJoCo C, so a GPU / CPU ratio built on "
+                         "it overstates the GPU's advantage by about as much",
+                 "ms_64_worlds_1_thread": 8.591, "ms_4096_worlds_16_threads": 34.746}
     return dict(value=64e3 / one["median_ms"], unit="world-steps/s", cores=1, kind="port", cpu=_cpu_model(),
-                host_threads=len(os.sched_getaffinity(0)),
+                host_threads=len(os.sched_getaffinity(0)), published_mujoco=published,
                 sample=f"64 config-0 worlds per call, {one['calls_per_round']} calls per round, 5 kept rounds "
                        f"({settings}); ms per 64-world step median {one['median_ms']:.2f}",
                 rounds=one,
