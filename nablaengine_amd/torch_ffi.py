@@ -318,11 +318,11 @@ def _backward_call(tape, friction, com, g_qpos, g_qvel, ctrl, kin_state, kin_cot
     pf, pc = w.ptr("friction", friction, ()), w.ptr("com", com, (3,))
     pgq, pgv = w.ptr("g_qpos", g_qpos, (NQ,)), w.ptr("g_qvel", g_qvel, (NV,))
     pu = w.ptr("ctrl", ctrl, (NU,)) if ctrl is not None else None
-    if kin_state:
+    if kin_state or kin_cot:
+        if len(kin_state) != 2 or len(kin_cot) != len(_KIN_OUT):
+            raise _err("kin_state = [qpos', qvel'] and kin_cot = the five kinematics outputs' cotangents", ValueError)
         pks = [w.ptr(n, x, s) for n, x, s in zip(("qpos'", "qvel'"), kin_state, ((NQ,), (NV,)))]
         pkc = [w.ptr("g_" + n, x, s) for (n, s), x in zip(_KIN_OUT, kin_cot)]
-        if len(pkc) != 5:
-            raise _err("kin_cot: the cotangents of the five kinematics outputs", ValueError)
     gq, gv, gu, info = w.empty(NQ), w.empty(NV), w.empty(NU), w.empty(dtype=torch.int32)
     if w.B == 0:
         return [gq, gv, gu, info]
