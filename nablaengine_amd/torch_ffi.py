@@ -227,9 +227,9 @@ def _ready(dev):
 # ---- argument checks ------------------------------------------------------------------------------------------------
 
 class _Worlds:
-    """The worlds of one call: the device and the count B come from its first per-world array (per_world: the rank of
-    its per-world part); every array must then be a contiguous tensor of the given dtype on that device, shaped
-    (*lead, B, *per_world)."""
+    """The worlds of one call: the device and the count B come from its first per-world array (B its leading size
+    when its rank is 1 + len(per_world), else -1, which no array then matches); every array must be a contiguous
+    tensor of the given dtype on that device, shaped (*lead, B, *per_world)."""
 
     def __init__(self, name, x, per_world):
         if not isinstance(x, Tensor) or x.device.type != "cuda":
@@ -240,7 +240,7 @@ class _Worlds:
         self.B = x.shape[0] if x.dim() == 1 + len(per_world) else -1
 
     def ptr(self, name, x, per_world, dtype=torch.float32, lead=()):
-        """x's device pointer after the checks; None stays None only where the caller allows it."""
+        """x's device pointer, after the checks (a TypeError naming x when one fails)."""
         want = (*lead, self.B, *per_world)
         if (isinstance(x, Tensor) and x.dtype == dtype and tuple(x.shape) == want and x.device == self.device
                 and x.is_contiguous()):
