@@ -239,7 +239,7 @@ def case4_default(ffi, case4):
     f32 = oracle.step_f32(**st, **oracle.ENGINE)
     # the 10-iteration cap did not bind in float64: 50 iterations at the same tolerance give the same state
     conv = (_rel(o10[1], o50[1]) <= 1e-12) & (_rel(o10[0], o50[0]) <= 1e-12)
-    return dict(gpu=(_np(q1), _np(v1), info.cpu().numpy()), nonconv=nonconv, o10=o10, f32=f32, conv=conv)
+    return dict(gpu=(_np(q1), _np(v1), info.cpu().numpy()), nonconv=nonconv, o10=o10, f32=f32, conv=conv, tape=tape)
 
 
 def _yardstick_gate(name, e, e32, floor_med=2e-6, floor_p90=2e-5):
@@ -294,3 +294,39 @@ def test_config4_capped_worlds_vs_oracle(case4_default):
     assert np.isfinite(q1[cap]).all() and np.isfinite(v1[cap]).all()
     _yardstick_gate("capped qvel", _rel(v1[cap], ov[cap]), _rel(v32[cap].astype(np.float64), ov[cap]))
     _yardstick_gate("capped qpos", _rel(q1[cap], oq[cap]), _rel(q32[cap].astype(np.float64), oq[cap]), 5e-7, 5e-6)
+
+
+def test_config4_default_vjp_vs_oracle(ffi, case4, case4_default):
+    """The VJP config 4's BPTT takes: the interface's default variant (clamp_kv 0, normal 3) from the 10-iteration
+    tape, against the oracle's analytic VJP at the same settings, on the worlds without a capacity overflow. Where both
+    converge: per block median relative error <= 1e-4 and p99 within 5x the float32 restatement's p99 (vjp_f32, floor
+    2e-3); where either stops at the cap: median and p90 within 5x the float32 restatement's (floors 1e-4, 2e-3). Every
+    gradient finite, no replay mismatch."""
+    import torch
+    args, s64, st = case4["args"], case4["s64"], case4["st"]
+    cq, cv = synthetic.cotangents(B, seed=77)
+    gq, gv, gu, binfo = ffi.backward(case4_default["tape"], args[4], args[5], _t(cq), _t(cv))
+    torch.cuda.synchronize()
+    g = np.concatenate([oracle.qpos_tangent(s64["qpos"], _np(gq)), _np(gv), _np(gu)], 1)
+    assert np.isfinite(g).all() and not (binfo.cpu().numpy() & (1 << 13)).any()
+    info, oinfo = case4_default["gpu"][2], case4_default["o10"][3]
+    ok = np.nonzero(((info[:, 3] | oinfo[:, 3]) & 20) == 0)[0]
+    opts = dict(clamp_kv=ffi.CLAMP_KV, normal=ffi.NORMAL, **oracle.ENGINE)
+    sub = {k: v[ok] for k, v in s64.items()}
+    r = oracle.vjp(**sub, g_qpos=cq[ok], g_qvel=cv[ok], **opts)
+    an = np.concatenate([oracle.qpos_tangent(sub["qpos"], r[0]), r[1], r[2]], 1)
+    r32 = oracle.vjp_f32(**{k: v[ok] for k, v in st.items()}, g_qpos=cq[ok], g_qvel=cv[ok], **opts)
+    y32 = np.concatenate([oracle.qpos_tangent(sub["qpos"], r32[0].astype(np.float64)), r32[1], r32[2]], 1)
+    both = (case4_default["conv"] & ~case4_default["nonconv"])[ok]
+    g = g[ok]
+    print(f"config4 default VJP: {both.sum()} worlds converged in both, {(~both).sum()} at the cap in either")
+    for name, sl in (("qpos", slice(0, 35)), ("qvel", slice(35, 70)), ("ctrl", slice(70, 99))):
+        e, e32 = _rel(g[:, sl], an[:, sl]), _rel(y32[:, sl].astype(np.float64), an[:, sl])
+        print(f"  {name}: converged median {np.median(e[both]):.3g} p99 {np.percentile(e[both], 99):.3g} (float32 "
+              f"restatement p99 {np.percentile(e32[both], 99):.3g}); at the cap median {np.median(e[~both]):.3g} p90 "
+              f"{np.percentile(e[~both], 90):.3g} (restatement {np.median(e32[~both]):.3g} / "
+              f"{np.percentile(e32[~both], 90):.3g})")
+        assert np.median(e[both]) <= 1e-4, name
+        assert np.percentile(e[both], 99) <= max(2e-3, 5 * np.percentile(e32[both], 99)), name
+        assert np.median(e[~both]) <= max(1e-4, 5 * np.median(e32[~both])), name
+        assert np.percentile(e[~both], 90) <= max(2e-3, 5 * np.percentile(e32[~both], 90)), name
