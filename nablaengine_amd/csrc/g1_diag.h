@@ -18,4 +18,5 @@ enum {
 constexpr int NONFINITE_SHIFT = 16;
 constexpr int NONFINITE_QPOS = 1, NONFINITE_QVEL = 2, NONFINITE_CTRL = 4, NONFINITE_COT = 8;
 constexpr int ADJ_REPLAY_MISMATCH = 1 << 13;
+constexpr int OVERFLOW_CONTACTS = 4, OVERFLOW_ROWS = 16;  // forward info[3]: contacts / rows beyond capacity dropped
 }  // namespace g1k
