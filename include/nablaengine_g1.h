@@ -133,8 +133,11 @@ int dk_adjoint_work_ordered(hipStream_t st, int nw, int nsub, const float* tape,
 /* No counterpart in the reference's ABI: ncot VJPs of one tape in one launch (the step Jacobian's 71 one-hot
  * cotangents), each set bitwise what dk_adjoint_work_diag gives for it. gq_out (ncot, nw, 36), gv_out (ncot, nw, 35)
  * -> gq_in (ncot, nw, 36), gv_in (ncot, nw, 35), gctrl (ncot, nw, 29), info (ncot, nw); work as dk_adjoint_work's (one
- * dispatch order for every set); d: the counters (ncot backward calls), or NULL. One launch of nw * ncot workgroups
- * of 64 work-items: nw * ncot * 64 < 2^32 (a Jacobian's 71 sets up to 945,195 worlds), else hipErrorInvalidValue. */
+ * dispatch order for every set); d: the counters (ncot backward calls), or NULL. With ncot >= 2 a workgroup runs a
+ * group of one world's sets, the tape-only phases of each substep once for the group, and keeps the sets' running
+ * cotangents in their output rows between substeps: the outputs must not overlap the inputs. One launch of at most
+ * nw * ncot workgroups of 64 work-items: nw * ncot * 64 < 2^32 (a Jacobian's 71 sets up to 945,195 worlds), else
+ * hipErrorInvalidValue. */
 int dk_adjoint_many(hipStream_t st, int nw, int ncot, int nsub, const float* tape, const float* fric, const float* com,
                     const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                     const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, unsigned long long* d);

@@ -388,11 +388,15 @@ __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr
 }
 
 // ---------------------------------------------------------------------------------------------- one substep
-__device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int clamp_kv, int normal,
-                            float clamp_soft) {
-  // the record: every field's load issued at once, on every lane (a lane past a field reads a word inside it and
-  // drops it; a field loaded under its own lane test waited for each load in turn), with the factors' copies into LDS
-  // (load_factors): one memory round trip
+// A substep's VJP in phases. The record, the poses and the twists of v, a* and a~ depend on the tape alone; the
+// integrator's VJP, the solves, the twists of lambda and y and every phase after them on the running cotangent
+// (s.qb, s.vb, s.ub). k_adjoint runs them in turn; k_adjoint_sets runs the first group once per substep and the
+// second once per cotangent set, the same functions in the same order, so each set's result is bitwise k_adjoint's.
+
+// the record: every field's load issued at once, on every lane (a lane past a field reads a word inside it and drops
+// it; a field loaded under its own lane test waited for each load in turn), with the factors' copies into LDS
+// (load_factors): one memory round trip
+__device__ __forceinline__ void adj_record(Adj& s, const float* __restrict__ rec, int lane) {
   const int lq = min(lane, NQ - 1), lv = min(lane, NV - 1);
   const float rq = rec[REC_QPOS + lq], rv = rec[REC_QVEL + lv], ra = rec[REC_ASTAR + lv], rd = rec[REC_AADV + lv];
   const unsigned rc = __float_as_uint(rec[REC_CLAMP + (lane & 1)]), rz = __float_as_uint(rec[REC_LIMZONE + (lane & 1)]);
@@ -419,8 +423,11 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   }
   if (lane == 0) { s.ncon = min((int)(hdr & 255u), MAXCON); s.flags |= (int)rfl; }
   wsync();
-  APROF(AP_RECORD);
-  // poses: each hinge body's local transform (lane = body), then each body lane walks its chain (the chain table)
+}
+
+// poses: each hinge body's local transform (lane = body), then each body lane walks its chain (the chain table); the
+// motion subspaces and geom poses last, with no barrier after them (the caller's next phase shares their interval)
+__device__ __forceinline__ void adj_poses(Adj& s, int lane) {
   if (lane >= 2 && lane < NB) {
     float sn, cs;
     sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
@@ -514,7 +521,10 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     for (int k = 0; k < 3; k++) s.gx[lane][k] = s.X[b][k] + t[k];
     qmul(qb, gq, s.gq[lane]);
   }
-  // the integrator's VJP (tangent space): hinges and root position directly; the root rotation on lane 0
+}
+
+// the integrator's VJP (tangent space): hinges and root position directly; the root rotation on lane 0
+__device__ __forceinline__ void adj_integrator(Adj& s, int lane) {
   if (lane < NV) {
     const bool dir = lane < 3 || lane >= 6;
     s.vt[lane] = s.vb[lane] + (dir ? kH * s.qb[lane] : 0.f);
@@ -554,8 +564,10 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     for (int k = 0; k < 3; k++) s.vt[3 + k] += kH * (t[k] + c1 * pt[k] + c2 * ppt[k]);
   }
   wsync();
-  APROF(AP_POSES);
-  // y = Q^-1 a_adv bar (L_Q), a* bar = a_adv bar - h kv y; lambda = H^-1 a* bar (L_H)
+}
+
+// y = Q^-1 a_adv bar (L_Q), a* bar = a_adv bar - h kv y; lambda = H^-1 a* bar (L_H)
+__device__ __forceinline__ void adj_solves(Adj& s, int lane) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the factors' copies have landed in LDS
   wsync();
   const float aab = lane < NV ? kH * s.vt[lane] : 0.f;
@@ -566,12 +578,17 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   const float lam = ltl_solve(s.lt.h, asb, lane);
   if (lane < NV) s.lam[lane] = lam;
   wsync();
-  APROF(AP_SOLVE);
-  // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body. Every
-  // body's chain starts with the root's 6 dofs, S_0..2 = (0; e_k) and S_3..5 = (w_k; 0): their part of a twist is
-  // (sum_k w_k x_{3+k}; x_0..2), the same on every lane, and their RNE term, V x (S_r v_r) summed over r = 3..5 with
-  // V = (w; u) the root's velocity twist, is (w x w; u x w) = (0; u x w). The hinge dofs follow (chain entries 6..15);
-  // the padding byte 255 clamps to dof NV, whose S row and entries are zero, so every step is unconditional.
+}
+
+// chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body. Every
+// body's chain starts with the root's 6 dofs, S_0..2 = (0; e_k) and S_3..5 = (w_k; 0): their part of a twist is
+// (sum_k w_k x_{3+k}; x_0..2), the same on every lane, and their RNE term, V x (S_r v_r) summed over r = 3..5 with
+// V = (w; u) the root's velocity twist, is (w x w; u x w) = (0; u x w). The hinge dofs follow (chain entries 6..15);
+// the padding byte 255 clamps to dof NV, whose S row and entries are zero, so every step is unconditional.
+// STATE: the twists of v, a*, a~ and the RNE acceleration (the record's); COT: those of lambda and y (the
+// cotangent's). Each twist is its own chain of sums, the same with either part alone.
+template <bool STATE, bool COT>
+__device__ __forceinline__ void adj_twists(Adj& s, int lane) {
   if (lane >= 1 && lane < NB) {
     unsigned ch[4];
     for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
@@ -583,34 +600,78 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
       }
       return r;
     };
-    Sv V = root(s.qvel), Lm = root(s.lam), Y = root(s.y), Aw = root(s.astar), A2 = root(s.at), Ac = sv0();
-    cross(V.v, V.w, Ac.v);
+    Sv V = sv0(), Lm = sv0(), Y = sv0(), Aw = sv0(), A2 = sv0(), Ac = sv0();
+    if (STATE) {
+      V = root(s.qvel);
+      Aw = root(s.astar);
+      A2 = root(s.at);
+      cross(V.v, V.w, Ac.v);
+    }
+    if (COT) {
+      Lm = root(s.lam);
+      Y = root(s.y);
+    }
 #pragma unroll
     for (int t = NROOT; t < MAXCHAIN; t++) {
       const unsigned b = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
       const int d = (int)min(b, (unsigned)NV);
       const Sv Sd = ld_sv(s.S[d]);
       const float vd = s.qvel[d];
-      V = sv_add(V, Sd, vd);
-      Lm = sv_add(Lm, Sd, s.lam[d]);
-      Y = sv_add(Y, Sd, s.y[d]);
-      Aw = sv_add(Aw, Sd, s.astar[d]);
-      A2 = sv_add(A2, Sd, s.at[d]);
-      Ac = sv_add(Ac, cross_mm(V, Sd), vd);
+      if (STATE) V = sv_add(V, Sd, vd);
+      if (COT) {
+        Lm = sv_add(Lm, Sd, s.lam[d]);
+        Y = sv_add(Y, Sd, s.y[d]);
+      }
+      if (STATE) {
+        Aw = sv_add(Aw, Sd, s.astar[d]);
+        A2 = sv_add(A2, Sd, s.at[d]);
+        Ac = sv_add(Ac, cross_mm(V, Sd), vd);
+      }
     }
     Sv A1 = sv_add(Aw, Ac);
     for (int k = 0; k < 3; k++) A1.v[k] -= kGrav[k];
-    st_sv6(s.tw[lane][TW_V], V);
-    st_sv6(s.tw[lane][TW_L], Lm);
-    st_sv6(s.tw[lane][TW_Y], Y);
-    st_sv6(s.tw[lane][TW_AW], Aw);
-    st_sv6(s.tw[lane][TW_A2], A2);
-    st_sv6(s.tw[lane][TW_A1], A1);
+    if (STATE) st_sv6(s.tw[lane][TW_V], V);
+    if (COT) {
+      st_sv6(s.tw[lane][TW_L], Lm);
+      st_sv6(s.tw[lane][TW_Y], Y);
+    }
+    if (STATE) {
+      st_sv6(s.tw[lane][TW_AW], Aw);
+      st_sv6(s.tw[lane][TW_A2], A2);
+      st_sv6(s.tw[lane][TW_A1], A1);
+    }
   }
   if (lane == 0)
-    for (int t = 0; t < NTW; t++) st_sv6(s.tw[0][t], sv0());
+    for (int t = 0; t < NTW; t++)
+      if ((t == TW_L || t == TW_Y) ? COT : STATE) st_sv6(s.tw[0][t], sv0());
   wsync();
+}
+
+// One substep's VJP. STATE: the phases that depend on the record alone (the record, the poses, the twists of v, a*
+// and a~); COT: those on the running cotangent (s.qb, s.vb, s.ub at the substep's end -> at its start): the
+// integrator's VJP, the solves, the twists of lambda and y, then the limit rows, the contacts (replayed from the
+// record's contact table), the per-body wrench sums, body forces and subtree sums, and the dof terms. COT alone needs
+// the factors' copies issued (load_factors) after the last COT pass, which overwrote them.
+template <bool STATE, bool COT>
+__device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int clamp_kv, int normal,
+                            float clamp_soft) {
+  if (STATE) {
+    adj_record(s, rec, lane);
+    APROF(AP_RECORD);
+    adj_poses(s, lane);
+  }
+  if (COT)
+    adj_integrator(s, lane);
+  else
+    wsync();
+  APROF(AP_POSES);
+  if (COT) {
+    adj_solves(s, lane);
+    APROF(AP_SOLVE);
+  }
+  adj_twists<STATE, COT>(s, lane);
   APROF(AP_TWIST);
+  if (!COT) return;
   // limit rows (their dof's lane): through the distance only (J constant)
   float lgq = 0.f, lgv = 0.f;
   if (lane >= 6 && lane < NV) {
@@ -874,6 +935,79 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   APROF(AP_DOF);
 }
 
+// the rotation part of a set's output cotangent in the tangent space at the output state, on one lane: the output
+// root quaternion is the last substep's integration of its record's qvel, a_adv and qpos rows, replayed; g the
+// cotangent's 4 quaternion entries
+__device__ __forceinline__ void seed_rotation(Adj& s, const float* qvel, const float* aadv, const float* qpos,
+                                              const float* g) {
+  float wv[3], q[4];
+  for (int k = 0; k < 3; k++) wv[k] = qvel[3 + k] + kH * aadv[3 + k];
+  for (int k = 0; k < 4; k++) q[k] = qpos[3 + k];
+  const float nw = sqrtf(dot3(wv, wv));
+  if (nw > 0.f) {
+    float sa, ca, o[4];
+    sincosf(0.5f * kH * nw, &sa, &ca);
+    const float sw = sa / nw;
+    const float dq[4] = {ca, sw * wv[0], sw * wv[1], sw * wv[2]};
+    qmul(q, dq, o);
+    const float on = rsqrtf(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
+    for (int k = 0; k < 4; k++) q[k] = o[k] * on;
+  }
+  for (int k = 0; k < 3; k++) {
+    float e[4] = {0.f, 0.f, 0.f, 0.f}, t[4];
+    e[1 + k] = 1.f;
+    qmul(q, e, t);
+    s.qb[3 + k] = 0.5f * (t[0] * g[0] + t[1] * g[1] + t[2] * g[2] + t[3] * g[3]);
+  }
+}
+
+// a set's gradients from s.qb, s.vb, s.ub: qpos form into oq (36), qvel into ov (35), ctrl into ou (29). The
+// quaternion's entries 2 q0 (x) (0, t), q0 the step's input quaternion (the first record's qpos row, qpos), are
+// computed on every lane and written by lanes 3..6; every other entry by the lane of its dof, so no entry of the
+// three rows is written by two lanes. Returns the non-finite bits of the values written (check) or 0.
+__device__ __forceinline__ int adj_emit(const Adj& s, const float* qpos, float* __restrict__ oq,
+                                        float* __restrict__ ov, float* __restrict__ ou, int lane, bool check) {
+  bool nq = false;  // a non-finite entry among those this lane writes
+  if (lane < 3 || (lane >= 6 && lane < NV)) {
+    oq[lane < 3 ? lane : lane + 1] = s.qb[lane];
+    nq = !__builtin_isfinite(s.qb[lane]);
+  }
+  {
+    const float* q0 = qpos + 3;
+    const float n = rsqrtf(q0[0] * q0[0] + q0[1] * q0[1] + q0[2] * q0[2] + q0[3] * q0[3]);
+    const float qq[4] = {q0[0] * n, q0[1] * n, q0[2] * n, q0[3] * n}, t[4] = {0.f, s.qb[3], s.qb[4], s.qb[5]};
+    float r[4];
+    qmul(qq, t, r);
+    if (lane >= 3 && lane < 7) {
+      const float o = 2.f * (lane == 3 ? r[0] : lane == 4 ? r[1] : lane == 5 ? r[2] : r[3]);
+      oq[lane] = o;
+      nq |= !__builtin_isfinite(o);
+    }
+  }
+  const float xv = s.vb[min(lane, NV - 1)], xu = s.ub[min(lane, NU - 1)];
+  if (lane < NV) ov[lane] = xv;
+  if (lane < NU) ou[lane] = xu;
+  if (!check) return 0;
+  return (ballot(nq) ? NONFINITE_QPOS : 0) | (ballot(!__builtin_isfinite(xv)) ? NONFINITE_QVEL : 0) |
+         (ballot(!__builtin_isfinite(xu)) ? NONFINITE_CTRL : 0);
+}
+
+// a set's part of the counters, from its info word f, on one lane; once per set (one backward call each) by the
+// workgroup of the set's first dispatched world
+__device__ __forceinline__ void adj_count(unsigned long long* __restrict__ diag, int f, bool first, int nw) {
+  const int b = f >> NONFINITE_SHIFT;
+  if (b & 7) atomicAdd(&diag[D_NONFINITE], 1ull);
+  if (b & NONFINITE_QPOS) atomicAdd(&diag[D_NONFINITE_QPOS], 1ull);
+  if (b & NONFINITE_QVEL) atomicAdd(&diag[D_NONFINITE_QVEL], 1ull);
+  if (b & NONFINITE_CTRL) atomicAdd(&diag[D_NONFINITE_CTRL], 1ull);
+  if (b & NONFINITE_COT) atomicAdd(&diag[D_NONFINITE_COT], 1ull);
+  if (f & ADJ_REPLAY_MISMATCH) atomicAdd(&diag[D_REPLAY_MISMATCH], 1ull);
+  if (first) {
+    atomicAdd(&diag[D_BWD_CALLS], 1ull);
+    atomicAdd(&diag[D_BWD_ROWS], (unsigned long long)nw);
+  }
+}
+
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_adjoint(int nw, int nsub, const float* __restrict__ tape,
                                                 const float* __restrict__ fric, const float* __restrict__ com,
                                                 const float* __restrict__ gq_out, const float* __restrict__ gv_out,
@@ -914,77 +1048,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   chain_table(s.chain, lane);
   if (lane < 8) s.S[NV][lane] = 0.f;  // the twists' zero padding row and entries (nothing else writes them)
   if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
-  // the output cotangents in the tangent space at the output state (its root quaternion: the last substep's
-  // integration replayed from the record)
+  // the output cotangents in the tangent space at the output state
   if (lane < NV) s.vb[lane] = igv;
   if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = igq;
   if (lane == 0) {
     const float* rec = wt + (size_t)(nsub - 1) * REC_WORDS;
-    float wv[3], q[4];
-    for (int k = 0; k < 3; k++) wv[k] = rec[REC_QVEL + 3 + k] + kH * rec[REC_AADV + 3 + k];
-    for (int k = 0; k < 4; k++) q[k] = rec[REC_QPOS + 3 + k];
-    const float nw = sqrtf(dot3(wv, wv));
-    if (nw > 0.f) {
-      float sa, ca, o[4];
-      sincosf(0.5f * kH * nw, &sa, &ca);
-      const float sw = sa / nw;
-      const float dq[4] = {ca, sw * wv[0], sw * wv[1], sw * wv[2]};
-      qmul(q, dq, o);
-      const float on = rsqrtf(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
-      for (int k = 0; k < 4; k++) q[k] = o[k] * on;
-    }
-    const float* g = gq_out + (size_t)wr * NQ + 3;
-    for (int k = 0; k < 3; k++) {
-      float e[4] = {0.f, 0.f, 0.f, 0.f}, t[4];
-      e[1 + k] = 1.f;
-      qmul(q, e, t);
-      s.qb[3 + k] = 0.5f * (t[0] * g[0] + t[1] * g[1] + t[2] * g[2] + t[3] * g[3]);
-    }
+    seed_rotation(s, rec + REC_QVEL, rec + REC_AADV, rec + REC_QPOS, gq_out + (size_t)wr * NQ + 3);
   }
   wsync();
-  for (int k = nsub - 1; k >= 0; k--) adj_substep(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
-  // gradients: qpos form (the quaternion's 2 q (x) (0, t)), qvel, ctrl
-  float* oq = gq_in + (size_t)wr * NQ;
-  bool nq = false;  // a non-finite entry among those this lane writes
-  if (lane < 3 || (lane >= 6 && lane < NV)) {
-    oq[lane < 3 ? lane : lane + 1] = s.qb[lane];
-    nq = !__builtin_isfinite(s.qb[lane]);
-  }
-  if (lane == 0) {
-    const float* q0 = wt + REC_QPOS + 3;
-    const float n = rsqrtf(q0[0] * q0[0] + q0[1] * q0[1] + q0[2] * q0[2] + q0[3] * q0[3]);
-    const float qq[4] = {q0[0] * n, q0[1] * n, q0[2] * n, q0[3] * n}, t[4] = {0.f, s.qb[3], s.qb[4], s.qb[5]};
-    float r[4];
-    qmul(qq, t, r);
-    for (int k = 0; k < 4; k++) {
-      const float o = 2.f * r[k];
-      oq[3 + k] = o;
-      nq |= !__builtin_isfinite(o);
-    }
-  }
-  const float xv = s.vb[min(lane, NV - 1)], xu = s.ub[min(lane, NU - 1)];
-  if (lane < NV) gv_in[(size_t)wr * NV + lane] = xv;
-  if (lane < NU) gctrl[(size_t)wr * NU + lane] = xu;
-  int nb = 0;  // with the counters: the non-finite bits of the gradients (k_diag_bwd's, from the values written)
-  if (diag)
-    nb = (ballot(nq) ? NONFINITE_QPOS : 0) | (ballot(!__builtin_isfinite(xv)) ? NONFINITE_QVEL : 0)
-         | (ballot(!__builtin_isfinite(xu)) ? NONFINITE_CTRL : 0);
+  for (int k = nsub - 1; k >= 0; k--) adj_substep<true, true>(s, wt + (size_t)k * REC_WORDS, lane, clamp_kv, normal, clamp_soft);
+  // gradients, and with the counters the non-finite bits of the values written (k_diag_bwd's)
+  const int nb = adj_emit(s, wt + REC_QPOS, gq_in + (size_t)wr * NQ, gv_in + (size_t)wr * NV,
+                          gctrl + (size_t)wr * NU, lane, diag != nullptr);
   if (lane == 0) {
     const int f = s.flags | nb << NONFINITE_SHIFT;
     info[wr] = f;
-    if (diag) {  // this world's part of the counters
-      const int b = f >> NONFINITE_SHIFT;
-      if (b & 7) atomicAdd(&diag[D_NONFINITE], 1ull);
-      if (b & NONFINITE_QPOS) atomicAdd(&diag[D_NONFINITE_QPOS], 1ull);
-      if (b & NONFINITE_QVEL) atomicAdd(&diag[D_NONFINITE_QVEL], 1ull);
-      if (b & NONFINITE_CTRL) atomicAdd(&diag[D_NONFINITE_CTRL], 1ull);
-      if (b & NONFINITE_COT) atomicAdd(&diag[D_NONFINITE_COT], 1ull);
-      if (f & ADJ_REPLAY_MISMATCH) atomicAdd(&diag[D_REPLAY_MISMATCH], 1ull);
-      if (wi == 0) {  // once per set of cotangents (a backward call each)
-        atomicAdd(&diag[D_BWD_CALLS], 1ull);
-        atomicAdd(&diag[D_BWD_ROWS], (unsigned long long)nw);
-      }
-    }
+    if (diag) adj_count(diag, f, wi == 0, nw);
   }
 #ifdef G1_PROFILE
   wsync();
@@ -994,7 +1073,103 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #endif
 }
 
+// ncot sets of output cotangents on one tape, one workgroup per (world, group of per consecutive sets): per substep
+// the record's phases once, then each set's cotangent phases, the same code as k_adjoint's in the same order (each
+// set's gradients and info are bitwise k_adjoint's for it). Workgroup b takes the sets [per g, per (g + 1)) of the
+// world dispatched b - g nw-th, g = b / nw. Between substeps a set's running cotangent waits in its own output rows,
+// each entry in a slot one lane alone writes and reads: qb[d] in gq_in's slot d (d < 6) or d + 1, vb[d] in gv_in's d,
+// ub[d] in gctrl's d, and the set's non-finite-cotangent bit in its info word; the last substep writes the gradients
+// over them (adj_emit writes gq_in's slots 3..6 from lanes 3..6).
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_adjoint_sets(
+    int nw, int nsub, const float* __restrict__ tape, const float* __restrict__ fric, const float* __restrict__ com,
+    const float* __restrict__ gq_out, const float* __restrict__ gv_out, float* __restrict__ gq_in,
+    float* __restrict__ gv_in, float* __restrict__ gctrl, int* __restrict__ info, const float* __restrict__ ctrl,
+    float clamp_soft, int clamp_kv, int normal, const int* __restrict__ perm, unsigned long long* __restrict__ diag,
+    int ncot, int per) {
+  __shared__ Adj s;
+  const int lane = threadIdx.x;
+  const int ngrp = (ncot + per - 1) / per;
+  if ((int)blockIdx.x >= nw * ngrp) return;
+  const int g = (int)blockIdx.x / nw, wi = (int)blockIdx.x - g * nw;
+  const int w = perm ? perm[wi] : wi;
+  const int c0 = g * per, c1 = min(ncot, c0 + per);
+  const float* wt = tape + (size_t)w * nsub * REC_WORDS;
+  const int lc = min(lane, 2), lu = min(lane, NU - 1), lv = min(lane, NV - 1);
+  const int lqo = min(lane < 3 ? lane : lane + 1, NQ - 1);  // qpos-form entry of tangent dof lane (< 3 or >= 6)
+  const int lqs = min(lane < 6 ? lane : lane + 1, NQ - 1);  // the running qb's slot of dof lane
+  const float ic = com[(size_t)w * 3 + lc], iu = ctrl ? ctrl[(size_t)w * NU + lu] : 0.f, ifr = fric[w];
+  if (lane < 3) s.com[lane] = ic;
+  if (lane < NU) s.ctrl[lane] = iu;
+  if (lane == 0) { s.fric = ifr; s.flags = 0; }  // the tape's flags, the same for every set
+#ifdef G1_PROFILE
+  if (lane < NPHASE) s.prof_acc[lane] = 0;
+  if (lane == 0) s.prof_t = __builtin_amdgcn_s_memtime();
+#endif
+  chain_table(s.chain, lane);
+  if (lane < 8) s.S[NV][lane] = 0.f;  // the twists' zero padding row and entries (nothing else writes them)
+  if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
+  wsync();
+#pragma unroll 1
+  for (int k = nsub - 1; k >= 0; k--) {
+    const float* rec = wt + (size_t)k * REC_WORDS;
+    adj_substep<true, false>(s, rec, lane, clamp_kv, normal, clamp_soft);
+#pragma unroll 1
+    for (int c = c0; c < c1; c++) {
+      const size_t wr = (size_t)c * nw + w;
+      float* oq = gq_in + wr * NQ;
+      float* ov = gv_in + wr * NV;
+      float* ou = gctrl + wr * NU;
+      if (c > c0) load_factors(s, rec, lane);  // the first set's copies came with the record
+      if (k == nsub - 1) {  // the set's output cotangents in the tangent space at the output state
+        const float igv = gv_out[wr * NV + lv], igq = gq_out[wr * NQ + lqo];
+        bool cbad = false;  // with the counters: a non-finite entry in the output cotangents
+        if (diag) {
+          const float icq = gq_out[wr * NQ + min(lane, NQ - 1)];
+          cbad = ballot(!(__builtin_isfinite(icq) && __builtin_isfinite(igv))) != 0ull;
+        }
+        if (lane < NU) s.ub[lane] = 0.f;
+        if (lane < NV) s.vb[lane] = igv;
+        if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = igq;
+        if (lane == 0) {
+          info[wr] = cbad ? NONFINITE_COT << NONFINITE_SHIFT : 0;
+          seed_rotation(s, s.qvel, s.aadv, s.qpos, gq_out + wr * NQ + 3);  // s holds the last record
+        }
+      } else {
+        const float rq = oq[lqs], rv = ov[lv], ru = ou[lu];
+        if (lane < NV) { s.qb[lane] = rq; s.vb[lane] = rv; }
+        if (lane < NU) s.ub[lane] = ru;
+      }
+      wsync();
+      adj_substep<false, true>(s, rec, lane, clamp_kv, normal, clamp_soft);
+      if (k > 0) {
+        if (lane < NV) { oq[lqs] = s.qb[lane]; ov[lane] = s.vb[lane]; }
+        if (lane < NU) ou[lane] = s.ub[lane];
+      } else {  // s holds the first record: its qpos row is the step's input
+        const int nb = adj_emit(s, s.qpos, oq, ov, ou, lane, diag != nullptr);
+        if (lane == 0) {
+          const int f = s.flags | info[wr] | nb << NONFINITE_SHIFT;
+          info[wr] = f;
+          if (diag) adj_count(diag, f, wi == 0, nw);
+        }
+      }
+      wsync();
+    }
+  }
+}
+
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
+
+// k_adjoint_sets' sets per workgroup: all of a world's sets in one workgroup (one record phase per substep) once nw
+// alone makes G1_SETS_WAVES waves, else groups small enough that nw x groups does. Of 2048 resident waves (2 per SIMD
+// on 256 CUs), 16384 makes 8 rounds: the launch's tail is a few sets long, and the record phases repeated per group
+// cost under 2% (measured at 1024, 4096 and 16384 worlds with 4096 to 32768 waves: 16384 within 1% of the best)
+#ifndef G1_SETS_WAVES
+#define G1_SETS_WAVES 16384
+#endif
+int sets_per_group(int nw, int ncot) {
+  const long long ngrp = std::min<long long>(ncot, std::max<long long>(1, (G1_SETS_WAVES + nw - 1) / nw));
+  return (int)((ncot + ngrp - 1) / ngrp);
+}
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                    const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                    const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work, int order,
@@ -1009,8 +1184,14 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
     }
     perm = (const int*)work;
   }
-  hipLaunchKernelGGL(k_adjoint, dim3(nw * ncot), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in,
-                     gv_in, gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm, diag, ncot);
+  if (ncot == 1) {
+    hipLaunchKernelGGL(k_adjoint, dim3(nw), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out, gq_in, gv_in,
+                       gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm, diag, 1);
+  } else {
+    const int per = sets_per_group(nw, ncot), ngrp = (ncot + per - 1) / per;
+    hipLaunchKernelGGL(k_adjoint_sets, dim3(nw * ngrp), dim3(64), 0, st, nw, nsub, tape, fric, com, gq_out, gv_out,
+                       gq_in, gv_in, gctrl, info, ctrl, clamp_soft, clamp_kv, normal, perm, diag, ncot, per);
+  }
   return (int)hipGetLastError();
 }
 size_t adjoint_lds_bytes() { return sizeof(Adj); }

@@ -123,6 +123,28 @@ def test_jacobian_rows_are_the_backward_vjps(ffi, heavy, kv, n, soft):
         assert torch.equal(J[:, r, :].view(torch.int32), row.view(torch.int32)), r
 
 
+@pytest.mark.parametrize("B,substeps", [(4096, 4), (1, 4), (301, 1), (257, 2)])
+def test_jacobian_rows_at_every_grouping(ffi, B, substeps):
+    """The many-cotangent adjoint runs a world's sets in workgroups of a size set by the batch (all 71 in one at 4096
+    worlds, one each for a single world, 6 for 301 and 5 for 257 worlds, the last group shorter) and keeps each set's
+    running cotangent in its output rows between substeps. At each grouping, and with one substep (the seed and the
+    gradients in one pass), every checked row is bitwise backward()'s VJP and info is the forward's."""
+    import torch
+    from nablaengine_amd import rollout
+    st = synthetic.states(B, config=1, seed=11 + B)
+    args = [_t(st[k]) for k in KEYS]
+    J, info = rollout.jacobian(*args, substeps=substeps)
+    q1, v1, w1, info2, tape = ffi.forward(*args, substeps=substeps, tape=True)
+    assert torch.equal(info, info2)
+    for r in (0, 4, 5, 6, 7, 35, 36, 39, 70):
+        cq = torch.zeros((B, 36), device="cuda")
+        cv = torch.zeros((B, 35), device="cuda")
+        (cq if r < 36 else cv)[:, r if r < 36 else r - 36] = 1.0
+        gq, gv, gu, binfo = ffi.backward(tape, args[4], args[5], cq, cv, substeps=substeps)
+        row = torch.cat([rollout.qpos_tangent(args[0], gq), gv, gu], 1)
+        assert torch.equal(J[:, r, :].view(torch.int32), row.view(torch.int32)), r
+
+
 def test_jacobian_options_are_checked(ffi, heavy):
     """The Jacobian driver takes the backward's options with the backward's checks: a delta for clamp_kv 0 / 1, a
     negative or NaN delta are ValueErrors, before any launch."""
