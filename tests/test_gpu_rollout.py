@@ -123,12 +123,12 @@ def test_jacobian_rows_are_the_backward_vjps(ffi, heavy, kv, n, soft):
         assert torch.equal(J[:, r, :].view(torch.int32), row.view(torch.int32)), r
 
 
-@pytest.mark.parametrize("B,substeps", [(4096, 4), (1, 4), (301, 1), (257, 2)])
+@pytest.mark.parametrize("B,substeps", [(16384, 4), (4096, 2), (1, 4), (301, 1)])
 def test_jacobian_rows_at_every_grouping(ffi, B, substeps):
-    """The many-cotangent adjoint runs a world's sets in workgroups of a size set by the batch (all 71 in one at 4096
-    worlds, one each for a single world, 6 for 301 and 5 for 257 worlds, the last group shorter) and keeps each set's
-    running cotangent in its output rows between substeps. At each grouping, and with one substep (the seed and the
-    gradients in one pass), every checked row is bitwise backward()'s VJP and info is the forward's."""
+    """The many-cotangent adjoint runs a world's sets in workgroups of a size set by the batch (all 71 in one at 16384
+    worlds, 18 at 4096, 2 at 301 with a last group of one, one each for a single world) and keeps each set's running
+    cotangent in its output rows between substeps. At each grouping, and with one substep (the seed and the gradients
+    in one pass), every checked row is bitwise backward()'s VJP and info is the forward's."""
     import torch
     from nablaengine_amd import rollout
     st = synthetic.states(B, config=1, seed=11 + B)
@@ -143,6 +143,37 @@ def test_jacobian_rows_at_every_grouping(ffi, B, substeps):
         gq, gv, gu, binfo = ffi.backward(tape, args[4], args[5], cq, cv, substeps=substeps)
         row = torch.cat([rollout.qpos_tangent(args[0], gq), gv, gu], 1)
         assert torch.equal(J[:, r, :].view(torch.int32), row.view(torch.int32)), r
+
+
+@pytest.mark.parametrize("B,substeps", [(16384, 4), (4096, 3), (3, 4), (301, 1)])
+def test_vjp_sets_are_the_backward_calls(ffi, B, substeps):
+    """Nine random cotangent sets in one many-cotangent launch against nine backward() calls, with the counters on:
+    the qpos-form, qvel and ctrl gradients and the info words bitwise equal, for a set whose cotangent holds a NaN
+    too (its non-finite bits, NONFINITE_COT among them, the same), at groupings of 9, 3 and 1 sets per workgroup and
+    at 1, 3 and 4 substeps; the counters count nine backward calls."""
+    import torch
+    st = synthetic.states(B, config=4, seed=3 + B)
+    args = [_t(st[k]) for k in KEYS]
+    prev = ffi.set_diagnostics(True)
+    try:
+        q1, v1, w1, info, tape = ffi.forward(*args, substeps=substeps, tape=True)
+        g = torch.Generator(device="cpu").manual_seed(B)
+        cq = torch.randn((9, B, 36), generator=g).cuda()
+        cv = torch.randn((9, B, 35), generator=g).cuda()
+        cq[4, B // 2, 5] = float("nan")
+        ffi.read_diagnostics(reset=True)
+        many = ffi._vjp_sets(tape, args[4], args[5], cq, cv, substeps=substeps)
+        d = ffi.read_diagnostics(reset=True)
+        assert d["bwd_calls"] == 9 and d["bwd_rows"] == 9 * B and d["nonfinite_cotangent_rows"] >= 1
+        for k in range(9):
+            one = ffi.backward(tape, args[4], args[5], cq[k], cv[k], substeps=substeps)
+            for a, b in zip(many, one):
+                x = a[k]
+                assert torch.equal(x.view(torch.int32), b.view(torch.int32)), k
+        bits = many[3][4, B // 2].item() >> 16
+        assert bits & 8, "NONFINITE_COT"
+    finally:
+        ffi.set_diagnostics(prev)
 
 
 def test_jacobian_options_are_checked(ffi, heavy):
