@@ -78,8 +78,7 @@ struct __align__(16) Adj {
   float qpos[40], qvel[36], astar[36], aadv[36], at[36];
   float qb[36], vb[36], vt[36], qn[36], y[36], lam[36], ub[32], ctrl[32], com[4];
   float S[NV + 1][8];                 // row NV is zero, as the dof vectors' entry NV (the chain padding's target)
-  float Q[NB][4], X[NB][4];
-  float hl[NB][12];                  // each hinge body's local transform: q_l, p_b, a_l (as the forward's FK)
+  float Q[NB][4], X[NB][4];          // the body frames, copied from the record (X's fourth words 0)
   unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
   float O[4];
   float fric;
@@ -102,6 +101,7 @@ struct __align__(16) Adj {
 // 8 worlds per CU: the LDS of one world must stay within 160 KB / 8
 static_assert(sizeof(Adj) <= 20480, "Adj outgrew the LDS of 8 worlds per CU");
 static_assert(offsetof(Adj, lt) % 16 == 0 && 3 * 256 <= 768 && NTRI <= 3 * 256, "the factors' LDS copies");
+static_assert(offsetof(Adj, X) == offsetof(Adj, Q) + 16 * NB, "the body frames Q, X as one array (the tape's copy)");
 
 // L_Q and L_H of a record copied into LDS by the memory unit (global_load_lds_dwordx4: lane l's 16 bytes land 16 l
 // bytes past the instruction's LDS base), 3 x 1024 bytes each; lanes past the factor's end load its start again into
@@ -422,76 +422,54 @@ __device__ __forceinline__ void adj_record(Adj& s, const float* __restrict__ rec
     s.con[2 * lane + 1] = (unsigned short)(rcon >> 16);
   }
   if (lane == 0) { s.ncon = min((int)(hdr & 255u), MAXCON); s.flags |= (int)rfl; }
+  // the body frames from L_Q's off-pattern positions (g1_tape.h), which get the factor's zeros back
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the factors' copies have landed in LDS
+  wsync();
+  float* frames = &s.Q[0][0];
+  for (int q = lane; q < POSE_WORDS; q += WL) {
+    const int p = cPoseSlots.pos[q];
+    frames[q] = s.lt.q[p];
+    s.lt.q[p] = 0.f;
+  }
   wsync();
 }
 
-// poses: each hinge body's local transform (lane = body), then each body lane walks its chain (the chain table); the
-// motion subspaces and geom poses last, with no barrier after them (the caller's next phase shares their interval)
+// L_Q's off-pattern positions set to 0 again in a new copy of the factors (the frames were taken from the first)
+__device__ __forceinline__ void clear_pose_slots(Adj& s, int lane) {
+  for (int q = lane; q < POSE_WORDS; q += WL) s.lt.q[cPoseSlots.pos[q]] = 0.f;
+}
+
+// poses: the body frames came with the record (the forward's FK of the substep's qpos); per body lane its spatial
+// inertia about O, then the motion subspaces and geom poses, with no barrier after them (the caller's next phase
+// shares their interval)
 __device__ __forceinline__ void adj_poses(Adj& s, int lane) {
-  if (lane >= 2 && lane < NB) {
-    float sn, cs;
-    sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
-    const float qb[4] = {cQuat[4 * lane], cQuat[4 * lane + 1], cQuat[4 * lane + 2], cQuat[4 * lane + 3]};
-    const float ax[3] = {cAxis[3 * lane], cAxis[3 * lane + 1], cAxis[3 * lane + 2]};
-    const float ha[4] = {cs, sn * ax[0], sn * ax[1], sn * ax[2]};
-    float* h = s.hl[lane];
-    qmul(qb, ha, h);
-    for (int c = 0; c < 3; c++) h[4 + c] = cPos[3 * lane + c];
-    qrot(qb, ax, h + 8);
-  }
   if (lane < 3) s.O[lane] = s.qpos[lane];
-  wsync();
-  {
-    float Q[4], X[3];
-    const float n = rsqrtf(s.qpos[3] * s.qpos[3] + s.qpos[4] * s.qpos[4] + s.qpos[5] * s.qpos[5] + s.qpos[6] * s.qpos[6]);
-    for (int k = 0; k < 4; k++) Q[k] = s.qpos[3 + k] * n;
-    for (int k = 0; k < 3; k++) X[k] = s.qpos[k];
-    const int b = lane < NB ? lane : 0;
-    unsigned ch[4];
-    for (int k = 0; k < 4; k++) ch[k] = s.chain[b][k];
-#pragma unroll
-    for (int l = 1; l < MAXDEPTH; l++) {
-      bool on;
-      const int d = chain_dof(ch, 5 + l, &on);  // the hinge dof of the body at depth l + 1 on b's chain
-      if (on) {
-        const float* h = s.hl[d - 4];
-        const float ql[4] = {h[0], h[1], h[2], h[3]}, pb[3] = {h[4], h[5], h[6]};
-        float t[3], q1[4];
-        qrot(Q, pb, t);
-        qmul(Q, ql, q1);
-        for (int c = 0; c < 4; c++) Q[c] = q1[c];
-        for (int c = 0; c < 3; c++) X[c] += t[c];
-      }
+  if (lane >= 1 && lane < NB) {  // own spatial inertia about O
+    const float Q[4] = {s.Q[lane][0], s.Q[lane][1], s.Q[lane][2], s.Q[lane][3]};
+    const float X[3] = {s.X[lane][0], s.X[lane][1], s.X[lane][2]};
+    float ip[3], c[3], qi[4], R[9];
+    for (int k = 0; k < 3; k++) ip[k] = cIpos[3 * lane + k] + (lane == TORSO_BODY ? s.com[k] : 0.f);
+    qrot(Q, ip, c);
+    const float iq[4] = {cIquat[4 * lane], cIquat[4 * lane + 1], cIquat[4 * lane + 2], cIquat[4 * lane + 3]};
+    const float In[3] = {cInert[3 * lane], cInert[3 * lane + 1], cInert[3 * lane + 2]};
+    qmul(Q, iq, qi);
+    for (int k = 0; k < 3; k++) {
+      float e[3] = {(float)(k == 0), (float)(k == 1), (float)(k == 2)};
+      qrot(qi, e, R + 3 * k);
     }
-    if (lane < NB) {
-      for (int k = 0; k < 4; k++) s.Q[lane][k] = lane == 0 ? (k == 0 ? 1.f : 0.f) : Q[k];
-      for (int k = 0; k < 3; k++) s.X[lane][k] = lane == 0 ? 0.f : X[k];
-    }
-    if (lane >= 1 && lane < NB) {  // own spatial inertia about O
-      float ip[3], c[3], qi[4], R[9];
-      for (int k = 0; k < 3; k++) ip[k] = cIpos[3 * lane + k] + (lane == TORSO_BODY ? s.com[k] : 0.f);
-      qrot(Q, ip, c);
-      const float iq[4] = {cIquat[4 * lane], cIquat[4 * lane + 1], cIquat[4 * lane + 2], cIquat[4 * lane + 3]};
-      const float In[3] = {cInert[3 * lane], cInert[3 * lane + 1], cInert[3 * lane + 2]};
-      qmul(Q, iq, qi);
-      for (int k = 0; k < 3; k++) {
-        float e[3] = {(float)(k == 0), (float)(k == 1), (float)(k == 2)};
-        qrot(qi, e, R + 3 * k);
-      }
-      float* J = s.Ib[lane];
-      J[0] = In[0] * R[0] * R[0] + In[1] * R[3] * R[3] + In[2] * R[6] * R[6];
-      J[1] = In[0] * R[1] * R[1] + In[1] * R[4] * R[4] + In[2] * R[7] * R[7];
-      J[2] = In[0] * R[2] * R[2] + In[1] * R[5] * R[5] + In[2] * R[8] * R[8];
-      J[3] = In[0] * R[0] * R[1] + In[1] * R[3] * R[4] + In[2] * R[6] * R[7];
-      J[4] = In[0] * R[0] * R[2] + In[1] * R[3] * R[5] + In[2] * R[6] * R[8];
-      J[5] = In[0] * R[1] * R[2] + In[1] * R[4] * R[5] + In[2] * R[7] * R[8];
-      float cc3[3];
-      for (int k = 0; k < 3; k++) cc3[k] = X[k] - s.qpos[k] + c[k];
-      const float m = cMass[lane], cc = dot3(cc3, cc3);
-      J[0] += m * (cc - cc3[0] * cc3[0]); J[1] += m * (cc - cc3[1] * cc3[1]); J[2] += m * (cc - cc3[2] * cc3[2]);
-      J[3] -= m * cc3[0] * cc3[1]; J[4] -= m * cc3[0] * cc3[2]; J[5] -= m * cc3[1] * cc3[2];
-      J[6] = m * cc3[0]; J[7] = m * cc3[1]; J[8] = m * cc3[2]; J[9] = m;
-    }
+    float* J = s.Ib[lane];
+    J[0] = In[0] * R[0] * R[0] + In[1] * R[3] * R[3] + In[2] * R[6] * R[6];
+    J[1] = In[0] * R[1] * R[1] + In[1] * R[4] * R[4] + In[2] * R[7] * R[7];
+    J[2] = In[0] * R[2] * R[2] + In[1] * R[5] * R[5] + In[2] * R[8] * R[8];
+    J[3] = In[0] * R[0] * R[1] + In[1] * R[3] * R[4] + In[2] * R[6] * R[7];
+    J[4] = In[0] * R[0] * R[2] + In[1] * R[3] * R[5] + In[2] * R[6] * R[8];
+    J[5] = In[0] * R[1] * R[2] + In[1] * R[4] * R[5] + In[2] * R[7] * R[8];
+    float cc3[3];
+    for (int k = 0; k < 3; k++) cc3[k] = X[k] - s.qpos[k] + c[k];
+    const float m = cMass[lane], cc = dot3(cc3, cc3);
+    J[0] += m * (cc - cc3[0] * cc3[0]); J[1] += m * (cc - cc3[1] * cc3[1]); J[2] += m * (cc - cc3[2] * cc3[2]);
+    J[3] -= m * cc3[0] * cc3[1]; J[4] -= m * cc3[0] * cc3[2]; J[5] -= m * cc3[1] * cc3[2];
+    J[6] = m * cc3[0]; J[7] = m * cc3[1]; J[8] = m * cc3[2]; J[9] = m;
   }
   wsync();
   if (lane < NV) {  // motion subspaces about O
@@ -1138,6 +1116,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const float rq = oq[lqs], rv = ov[lv], ru = ou[lu];
         if (lane < NV) { s.qb[lane] = rq; s.vb[lane] = rv; }
         if (lane < NU) s.ub[lane] = ru;
+      }
+      if (c > c0) {  // the factors' new copies have landed: L_Q's zeros back in its frame slots
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        wsync();
+        clear_pose_slots(s, lane);
       }
       wsync();
       adj_substep<false, true>(s, rec, lane, clamp_kv, normal, clamp_soft);

@@ -41,6 +41,7 @@ struct __align__(16) Sim {
 #ifndef G1_PROFILE
 static_assert(sizeof(Sim) <= 20480, "Sim outgrew the LDS of 8 worlds per CU");
 #endif
+static_assert(offsetof(Sim, X) == offsetof(Sim, Q) + 16 * NB, "the body frames Q, X as one array (the tape's copy)");
 
 // per-lane register state of the constraint rows: lane l holds contact l's rows and dof l's limit row
 struct Rows {

@@ -1053,6 +1053,12 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
     const float adv = ltl_solve(s.L, lane < NV ? s.Ma[lane] : 0.f, lane);
     if (lane < NV) s.qvel[lane] += kH * adv;
     if (rec) {
+      // L_Q, its off-pattern positions carrying the body frames FK left at the substep's start (g1_tape.h): they
+      // are written into the factor's zeros in LDS first (s.L is factored afresh before its next use); a position's
+      // fourth word, which nothing writes in s.X, as 0
+      for (int q = lane; q < POSE_WORDS; q += WL)
+        s.L[cPoseSlots.pos[q]] = q >= 4 * NB && (q & 3) == 3 ? 0.f : (&s.Q[0][0])[q];
+      wsync();
       tape_put(rec + REC_LQ, s.L, NTRI, REC_WORDS - REC_LQ, lane);
       if (lane < REC_LH - REC_AADV) rec[REC_AADV + lane] = lane < NV ? adv : 0.f;
     }

@@ -2,6 +2,7 @@
 // adjoint needs to differentiate the substep without re-solving it. Own layout (the reference's is tape.py:28-45):
 // integer fields are bit-cast into float words.
 #pragma once
+#include "g1_device.h"
 
 namespace g1k {
 constexpr int REC_HDR = 0;        // ncon | nefc << 8 | nlim << 16 | Newton iterations << 24
@@ -17,11 +18,37 @@ constexpr int REC_QVEL = 84;      // 35: input qvel
 constexpr int REC_ASTAR = 128;    // 35: Newton's final acceleration a*
 constexpr int REC_AADV = 164;     // 35: implicitfast's a_adv = (M + h kv)^-1 M a*
 constexpr int REC_LH = 200;       // 630: factor L of H = L' L = M + J'DJ at the final zones (packed lower, row-major)
-constexpr int REC_LQ = 832;       // 630: factor L of M + h kv = L' L
+constexpr int REC_LQ = 832;       // 630: factor L of M + h kv = L' L, with the body frames in its off-pattern positions
 constexpr int REC_WORDS = 1472;
 constexpr unsigned TAPE_CON_NONE = 0xFFFFu;
 constexpr int FLAG_REFACT = 1 << 8;    // the zones changed after the last Newton factorization: H re-factored for the tape
 constexpr int FLAG_NONCONV = 1 << 9;   // the Newton iterations ran out before the stopping test held
 constexpr int FLAG_SINGULAR = 1 << 10; // a self contact whose geom centres / axes are nearer than SINGULAR_NU
 constexpr float SINGULAR_NU = 5e-3f;   // m
+
+// M + h kv has the tree's sparsity and its leaf-first factor keeps it, so the packed lower triangle of L_Q is 0 off the
+// dof chains (289 of its 630 positions). The record keeps the 341 entries on the chains at their packed positions; the
+// first POSE_WORDS off-pattern positions (in packed order) carry the body frames at the substep's qpos, as the
+// forward's FK leaves them in LDS (NB quaternions, then NB positions, 4 words each; a position's fourth word 0), and
+// the rest hold 0. The adjoint takes the frames from its copy of L_Q and writes the factor's zeros back.
+constexpr int POSE_WORDS = 8 * NB;
+struct PoseSlots {
+  short pos[POSE_WORDS];  // the packed position of frame word q
+};
+constexpr PoseSlots make_pose_slots() {
+  PoseSlots t{};
+  int q = 0;
+  for (int i = 0; i < NV; i++)
+    for (int j = 0; j <= i; j++)
+      if (!((TREE.dofanc[i] >> j) & 1ull) && q < POSE_WORDS) t.pos[q++] = (short)tri(i, j);
+  return t;
+}
+constexpr int off_pattern_positions() {
+  int n = 0;
+  for (int i = 0; i < NV; i++)
+    for (int j = 0; j <= i; j++) n += ((TREE.dofanc[i] >> j) & 1ull) ? 0 : 1;
+  return n;
+}
+static_assert(off_pattern_positions() >= POSE_WORDS, "L_Q's off-pattern positions hold the body frames");
+__constant__ inline PoseSlots cPoseSlots = make_pose_slots();
 }  // namespace g1k

@@ -138,6 +138,18 @@ def _unpack(words):
     return L
 
 
+def _tree_pattern():
+    """(35, 35) bool: dof j on dof i's chain (j's body is i's or one of its ancestors), j <= i: where M's and L_Q's
+    lower triangles can be nonzero."""
+    m = synthetic.model()
+    db, am = np.asarray(m["dof_body"]), np.asarray(m["body_ancmask"])
+    P = np.zeros((35, 35), bool)
+    for i in range(35):
+        for j in range(i + 1):
+            P[i, j] = (int(am[db[i]]) >> int(db[j])) & 1
+    return P
+
+
 @pytest.mark.parametrize("config", [1, 4])
 def test_taped_factors_vs_oracle(ffi, config):
     """The reference's tape checks T4 / T5 (docs/verification.md:131-132) at 50 Newton iterations: every record's L_Q
@@ -156,6 +168,7 @@ def test_taped_factors_vs_oracle(ffi, config):
     flags = tape[:, :, REC_FLAGS].view(np.uint32)
     m = synthetic.model()
     hkv = m["timestep"] * np.diag(np.asarray(m["dof_kv"]))
+    pattern = _tree_pattern()
     eq, eh = [], []
     for w in range(B):
         warm = st["warm"][w].astype(np.float64)
@@ -164,7 +177,7 @@ def test_taped_factors_vs_oracle(ffi, config):
             q, v = rec[REC_QPOS:REC_QPOS + 36], rec[REC_QVEL:REC_QVEL + 35]
             u, f, c = st["ctrl"][w].astype(np.float64), float(st["friction"][w]), st["com"][w].astype(np.float64)
             M, H = oracle.substep_hessian(q, v, warm, u, f, c)
-            LQ, LH = _unpack(rec[REC_LQ:]), _unpack(rec[REC_LH:])
+            LQ, LH = _unpack(rec[REC_LQ:]) * pattern, _unpack(rec[REC_LH:])  # L_Q's other positions: frames
             ref = oracle.ltl(M + hkv)
             eq.append(np.abs(LQ - ref).max() / np.abs(ref).max())
             if not flags[w, k] & (4 | 16 | (1 << 9)):
@@ -176,3 +189,34 @@ def test_taped_factors_vs_oracle(ffi, config):
           f"max {eh.max():.3g}")
     assert eq.max() <= 1e-5
     assert len(eh) >= 3 * B and np.median(eh) <= 1e-5 and np.percentile(eh, 95) <= 1e-4
+
+
+def test_taped_frames_vs_oracle(ffi):
+    """L_Q is 0 off the tree's pattern, and the record carries the body frames at the substep's qpos in those
+    positions (packed order: 31 quaternions, then 31 positions with a fourth word 0; the positions past them 0). On
+    contact-heavy states, every record's frames against the float64 oracle's FK of the record's qpos (xquat, xpos of
+    oracle.kinematics): max error <= 2e-6 (quaternions) and 2e-6 m (positions); and the adjoint, which takes its
+    poses from them, is the VJP (the adjoint tests)."""
+    import torch
+    B = 64
+    st = synthetic.states(B, config=4, seed=5)
+    args = [_t(st[k]) for k in KEYS]
+    r = ffi.forward(*args, tape=True)
+    torch.cuda.synchronize()
+    tape = r[4].cpu().numpy().reshape(B, 4, -1)
+    pattern = _tree_pattern()
+    rows, cols = np.tril_indices(35)
+    off = np.flatnonzero(~pattern[rows, cols])  # packed positions off the pattern, in packed order
+    nf = 8 * 31
+    assert len(off) >= nf
+    eq = ep = 0.0
+    for k in range(4):
+        q = tape[:, k, REC_QPOS:REC_QPOS + 36].astype(np.float64)
+        _, xpos, xquat, _, _ = oracle.kinematics(q, np.zeros((B, 35)), st["com"])
+        fr = tape[:, k, REC_LQ:REC_LQ + NTRI][:, off[:nf]].astype(np.float64)
+        Q, X = fr[:, :124].reshape(B, 31, 4), fr[:, 124:].reshape(B, 31, 4)
+        assert np.all(X[:, :, 3] == 0) and np.all(tape[:, k, REC_LQ:REC_LQ + NTRI][:, off[nf:]] == 0)
+        eq = max(eq, np.abs(Q - xquat).max())
+        ep = max(ep, np.abs(X[:, :, :3] - xpos).max())
+    print(f"record frames vs float64 FK: quaternions max {eq:.3g}, positions max {ep:.3g} m")
+    assert eq <= 2e-6 and ep <= 2e-6
