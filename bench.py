@@ -24,11 +24,12 @@ backprop through time, checkpoint segments of 8 steps, and its capped world-step
 
 `roofline` is the dominant kernel's, k_forward: algorithmic flops per launch (the float64 CPU restatement's
 closed-form phase counts on the same inputs, counted once before timing, per world-step x B) divided by k_forward's
-mean duration, timed live here with HIP events around K back-to-back launches of the forward alone (the order
-computed once before, dk_fwd_forward_ordered); peak is MI355X's FP32 (157.3 TFLOP/s). `traffic` is k_forward's HBM
+mean duration, timed live here with HIP events around K back-to-back launches of the forward alone
+(dk_fwd_forward_ordered, cycling through 8 dispatch orders computed before: one order's kernel time differs from
+another's by up to 2%, and the step computes a new order every call); peak is MI355X's FP32 (157.3 TFLOP/s). `traffic` is k_forward's HBM
 bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (the committed summary). `roofline_adjoint` is the same for
 k_adjoint, the VJP's kernel: the float64 restatement's closed-form count of the adjoint's flops (default variant)
-over k_adjoint's mean duration, timed live around back-to-back launches with one dispatch order, and its HBM rate (the
+over k_adjoint's mean duration, timed live around back-to-back launches over 8 dispatch orders, and its HBM rate (the
 tape read plus the adjoint's interface bytes) against 8 TB/s. `cpu_baseline` is the float64 CPU
 restatement ("port"), timed with the same round protocol: one thread on the 64 worlds of config 0 (the reference's
 single-thread CPU case) and, in `all_threads`, the host's usable cores (len(os.sched_getaffinity(0)), at most 16: the
@@ -59,6 +60,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_forward_4096_traffic.md")
 # info 4 B out) and the tape it reads (4 substeps x 1472 float32 words)
 IO_BYTES_VJP = (36 + 35 + 1 + 3) * 4 + (36 + 35 + 29) * 4 + 4
 TAPE_BYTES = 4 * 1472 * 4
+ORDERS = 8  # dispatch orders the kernel-alone timings cycle through
 CORPUS = os.path.join(ROOT, "tests", "golden", "corpus_mf_s0.npz")
 KEYS = ("qpos", "qvel", "warm", "ctrl", "friction", "com")
 ROUNDS, WARM_CALLS, WARM_S, ROUND_S, MAX_CALLS = 5, 5, 1.0, 0.25, 200
@@ -223,35 +225,49 @@ def measure(B, steps, warmup, kernel=False, rounds=True):
     info = out["r"][3].cpu().numpy()
     vjp_ms = timed(vjp, steps, warmup, stream)
     kms = ams = None
-    if kernel:  # k_forward alone: the order once, then the ordered launches back to back
+    if kernel:
+        # k_forward alone: ORDERS dispatch orders computed first, then ordered launches back to back, cycling through
+        # them. An order's ties within a cost bucket fall as its atomics do, and one order's kernel time differs from
+        # another's by up to 2% (the XCDs' queues get different worlds); the step computes a new order every call,
+        # so the kernel's time is taken over several, as the step sees it
         lib = torch_ffi.load_library()
         st_ = ctypes.c_void_p(stream.cuda_stream)
         p = lambda t: ctypes.c_void_p(t.data_ptr())
         kw = dict(dtype=torch.float32, device="cuda")
         q1, v1, w1 = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 35), **kw)
         inf = torch.empty((B, 4), dtype=torch.int32, device="cuda")
-        work = torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device="cuda")
-        assert lib.dk_fwd_order(st_, B, p(args[0]), p(work)) == 0
+        works = [torch.empty((int(lib.dk_fwd_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+                 for _ in range(ORDERS)]
+        for work in works:
+            assert lib.dk_fwd_order(st_, B, p(args[0]), p(work)) == 0
+        nk = [0]
 
         def kern():
+            work = works[nk[0] % ORDERS]
+            nk[0] += 1
             assert lib.dk_fwd_forward_ordered(st_, B, *map(p, args), 10, 4, p(q1), p(v1), p(w1), p(inf), None, None,
                                               p(work)) == 0
-        kms = timed(kern, steps, warmup, stream)
-        # k_adjoint alone: one tape and the adjoint's order once, then the ordered launches back to back, with the
-        # diagnostic counting on (as torch_ffi.backward launches it)
+        kms = timed(kern, max(steps, 2 * ORDERS), warmup, stream)
+        # k_adjoint alone: one tape and ORDERS adjoint orders, then the ordered launches back to back, cycling
+        # through them, with the diagnostic counting on (as torch_ffi.backward launches it)
         tape = torch_ffi.forward(*args, tape=True)[4]
         gq, gv = (torch.from_numpy(x).cuda() for x in synthetic.cotangents(B))
         bq, bv, bu = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 29), **kw)
         binf = torch.empty((B,), dtype=torch.int32, device="cuda")
-        awork = torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+        aworks = [torch.empty((int(lib.dk_adjoint_work_bytes(B)),), dtype=torch.uint8, device="cuda")
+                  for _ in range(ORDERS)]
         counters = torch.zeros(len(torch_ffi.DIAG), dtype=torch.int64, device="cuda")
-        assert lib.dk_adjoint_order(st_, B, 4, p(tape), p(awork)) == 0
+        for awork in aworks:
+            assert lib.dk_adjoint_order(st_, B, 4, p(tape), p(awork)) == 0
+        na = [0]
 
         def adj():
+            awork = aworks[na[0] % ORDERS]
+            na[0] += 1
             assert lib.dk_adjoint_work_ordered(st_, B, 4, p(tape), p(args[4]), p(args[5]), p(gq), p(gv), p(bq), p(bv),
                                                p(bu), p(binf), None, 0.0, torch_ffi.CLAMP_KV, torch_ffi.NORMAL,
                                                p(awork), p(counters)) == 0
-        ams = timed(adj, steps, warmup, stream)
+        ams = timed(adj, max(steps, 2 * ORDERS), warmup, stream)
     rs = {"forward": protocol_gpu(fwd, stream), "fwd_vjp": protocol_gpu(vjp, stream)} if rounds else None
     return ms, vjp_ms, kms, ams, info, rs
 
@@ -380,8 +396,8 @@ def main():
                      "note": "FP32 vector (VALU) work, no MFMA in the Newton path's bulk: achieved = closed-form "
                              f"algorithmic flops ({fl:.3g} per world-step, float64 restatement on {len(sub['qpos'])} "
                              "of the worlds) x worlds / k_forward's mean duration (HIP events around back-to-back "
-                             "launches of the forward kernel alone, its stream); the step also runs the dispatch-order "
-                             "pre-pass (ms_per_step - ms_k_forward)"},
+                             "launches of the forward kernel alone over 8 dispatch orders, its stream); the step also "
+                             "runs the dispatch-order pre-pass (ms_per_step - ms_k_forward)"},
         "roofline_hbm": {"achieved": IO_BYTES_FWD * B / (kms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": IO_BYTES_FWD * B / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                          "note": f"interface bytes {IO_BYTES_FWD} per world-step"},
@@ -396,7 +412,7 @@ def main():
                                      "only): achieved = closed-form algorithmic flops of the VJP (" f"{fla:.3g}"
                                      " per world-step, the float64 restatement's adjoint count on "
                                      f"{len(sub['qpos'])} of the worlds, default variant) x worlds / k_adjoint's mean "
-                                     "duration (HIP events around back-to-back launches with one dispatch order, its "
+                                     "duration (HIP events around back-to-back launches over 8 dispatch orders, its "
                                      "stream); hbm: the tape read (4 substeps x 1472 words) plus the interface's "
                                      f"{IO_BYTES_VJP} bytes per world-step over the same duration"},
         "capacity": {"contacts_max": int(info[:, 1].max()), "rows_max": int(info[:, 2].max()),

@@ -79,6 +79,7 @@ struct __align__(16) Adj {
   float qb[36], vb[36], vt[36], qn[36], y[36], lam[36], ub[32], ctrl[32], com[4];
   float S[NV + 1][8];                 // row NV is zero, as the dof vectors' entry NV (the chain padding's target)
   float Q[NB][4], X[NB][4];          // the body frames, copied from the record (X's fourth words 0)
+  unsigned short pslot[POSE_WORDS];  // L_Q's packed positions that carry the frames (cPoseSlots, loaded at start)
   unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
   float O[4];
   float fric;
@@ -427,7 +428,7 @@ __device__ __forceinline__ void adj_record(Adj& s, const float* __restrict__ rec
   wsync();
   float* frames = &s.Q[0][0];
   for (int q = lane; q < POSE_WORDS; q += WL) {
-    const int p = cPoseSlots.pos[q];
+    const int p = s.pslot[q];
     frames[q] = s.lt.q[p];
     s.lt.q[p] = 0.f;
   }
@@ -436,7 +437,7 @@ __device__ __forceinline__ void adj_record(Adj& s, const float* __restrict__ rec
 
 // L_Q's off-pattern positions set to 0 again in a new copy of the factors (the frames were taken from the first)
 __device__ __forceinline__ void clear_pose_slots(Adj& s, int lane) {
-  for (int q = lane; q < POSE_WORDS; q += WL) s.lt.q[cPoseSlots.pos[q]] = 0.f;
+  for (int q = lane; q < POSE_WORDS; q += WL) s.lt.q[s.pslot[q]] = 0.f;
 }
 
 // poses: the body frames came with the record (the forward's FK of the substep's qpos); per body lane its spatial
@@ -545,9 +546,14 @@ __device__ __forceinline__ void adj_integrator(Adj& s, int lane) {
 }
 
 // y = Q^-1 a_adv bar (L_Q), a* bar = a_adv bar - h kv y; lambda = H^-1 a* bar (L_H)
-__device__ __forceinline__ void adj_solves(Adj& s, int lane) {
+// clear: L_Q's frame slots set to 0 first (a copy of the factors made after the record's, whose frames were taken)
+__device__ __forceinline__ void adj_solves(Adj& s, int lane, bool clear) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the factors' copies have landed in LDS
   wsync();
+  if (clear) {
+    clear_pose_slots(s, lane);
+    wsync();
+  }
   const float aab = lane < NV ? kH * s.vt[lane] : 0.f;
   const float y = ltl_solve(s.lt.q, aab, lane);
   if (lane < NV) s.y[lane] = y;
@@ -629,10 +635,11 @@ __device__ __forceinline__ void adj_twists(Adj& s, int lane) {
 // and a~); COT: those on the running cotangent (s.qb, s.vb, s.ub at the substep's end -> at its start): the
 // integrator's VJP, the solves, the twists of lambda and y, then the limit rows, the contacts (replayed from the
 // record's contact table), the per-body wrench sums, body forces and subtree sums, and the dof terms. COT alone needs
-// the factors' copies issued (load_factors) after the last COT pass, which overwrote them.
+// the factors' copies issued (load_factors) after the last COT pass, which overwrote them; recopied: they were, so
+// L_Q's frame slots are set to 0 again before the solves.
 template <bool STATE, bool COT>
 __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int clamp_kv, int normal,
-                            float clamp_soft) {
+                            float clamp_soft, bool recopied = false) {
   if (STATE) {
     adj_record(s, rec, lane);
     APROF(AP_RECORD);
@@ -644,7 +651,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     wsync();
   APROF(AP_POSES);
   if (COT) {
-    adj_solves(s, lane);
+    adj_solves(s, lane, recopied);
     APROF(AP_SOLVE);
   }
   adj_twists<STATE, COT>(s, lane);
@@ -1024,6 +1031,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   }
 #endif
   chain_table(s.chain, lane);
+  for (int q = lane; q < POSE_WORDS; q += WL) s.pslot[q] = (unsigned short)cPoseSlots.pos[q];
   if (lane < 8) s.S[NV][lane] = 0.f;  // the twists' zero padding row and entries (nothing else writes them)
   if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
   // the output cotangents in the tangent space at the output state
@@ -1084,6 +1092,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane == 0) s.prof_t = __builtin_amdgcn_s_memtime();
 #endif
   chain_table(s.chain, lane);
+  for (int q = lane; q < POSE_WORDS; q += WL) s.pslot[q] = (unsigned short)cPoseSlots.pos[q];
   if (lane < 8) s.S[NV][lane] = 0.f;  // the twists' zero padding row and entries (nothing else writes them)
   if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
   wsync();
@@ -1117,13 +1126,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         if (lane < NV) { s.qb[lane] = rq; s.vb[lane] = rv; }
         if (lane < NU) s.ub[lane] = ru;
       }
-      if (c > c0) {  // the factors' new copies have landed: L_Q's zeros back in its frame slots
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        wsync();
-        clear_pose_slots(s, lane);
-      }
       wsync();
-      adj_substep<false, true>(s, rec, lane, clamp_kv, normal, clamp_soft);
+      adj_substep<false, true>(s, rec, lane, clamp_kv, normal, clamp_soft, c > c0);
       if (k > 0) {
         if (lane < NV) { oq[lqs] = s.qb[lane]; ov[lane] = s.vb[lane]; }
         if (lane < NU) ou[lane] = s.ub[lane];
