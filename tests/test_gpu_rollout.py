@@ -176,6 +176,29 @@ def test_vjp_sets_are_the_backward_calls(ffi, B, substeps):
         ffi.set_diagnostics(prev)
 
 
+def test_empty_batch_everywhere(ffi):
+    """B = 0 through every entry: the taped forward's empty tape, backward(), step() under autograd (its backward),
+    the many-cotangent VJPs and jacobian() give empty outputs of the right shapes, and nothing is launched on 0
+    worlds."""
+    import torch
+    from nablaengine_amd import rollout
+    st = synthetic.states(2, config=1)
+    a = [_t(st[k])[:0] for k in KEYS]
+    q1, v1, w1, info, tape = ffi.forward(*a, tape=True)
+    assert q1.shape == (0, 36) and v1.shape == (0, 35) and info.shape == (0, 4) and tape.shape[0] == 0
+    gq, gv, gu, binfo = ffi.backward(tape, a[4], a[5], q1, v1)
+    assert gq.shape == (0, 36) and gv.shape == (0, 35) and gu.shape == (0, 29) and binfo.shape == (0,)
+    x = [t.clone().requires_grad_(True) for t in a[:2]] + [a[2], a[3].clone().requires_grad_(True)] + a[4:]
+    out = ffi.step(*x)
+    (out[0].sum() + out[1].sum()).backward()
+    assert x[0].grad.shape == (0, 36) and x[1].grad.shape == (0, 35) and x[3].grad.shape == (0, 29)
+    many = ffi._vjp_sets(tape, a[4], a[5], torch.zeros((3, 0, 36), device="cuda"), torch.zeros((3, 0, 35), device="cuda"))
+    assert [t.shape for t in many] == [(3, 0, 36), (3, 0, 35), (3, 0, 29), (3, 0)]
+    J, jinfo = rollout.jacobian(*a)
+    assert J.shape == (0, 71, 99) and jinfo.shape == (0, 4)
+    torch.cuda.synchronize()
+
+
 def test_jacobian_options_are_checked(ffi, heavy):
     """The Jacobian driver takes the backward's options with the backward's checks: a delta for clamp_kv 0 / 1, a
     negative or NaN delta are ValueErrors, before any launch."""
