@@ -20,11 +20,12 @@ struct __align__(16) Sim {
   float fric;
   int ncon, ncon_raw, nlim, nefc, flags, niter;
   int dcnt;  // the records' flags counted over the substeps: refactored | not converged << 8 | singular << 16
+  int acost;  // the adjoint's dispatch cost summed over the substeps so far (taped forward)
   unsigned clampm[2];  // dofs whose actuator force is at its limit (tape)
 #ifdef G1_PROFILE
   unsigned long long prof_t, prof_acc[NPHASE];
 #endif
-  union {
+  union __align__(16) {  // 16-byte aligned whatever the scalars above add up to (its rows are read as float4s)
     struct { float F[NB][4], T[NB][4], Ic[NB][12], hl[NB][12]; } sm;  // smooth dynamics: subtree force, moment about O,
                                                                      // inertia; bodies' local transforms
     struct { float gx[NGEOM][4], gq[NGEOM][4]; float stage[MAXCON][16]; unsigned short cand[NPAIR + 2]; } col;

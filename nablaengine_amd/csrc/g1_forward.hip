@@ -1036,7 +1036,17 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
       rec[REC_LIMROW + lane] = __uint_as_float((unsigned)(lane ? lr >> 32 : lr));
     }
     tape_put(rec + REC_ASTAR, s.qacc, NV, REC_AADV - REC_ASTAR, lane);
+    // the adjoint's dispatch cost of this substep: its contacts, the distinct robot bodies they touch and the contacts
+    // between two robot bodies (4 each: the per-body wrench sums, the two-body contact VJPs), and the primitive classes
+    // present (8 each: a lane's class branches run for the whole wave), in units of 4 (measured on config-1 worlds:
+    // the adjoint's launch in this order ends 3.4% earlier than ordered by the records' constraint rows)
+    const unsigned pwc = cPairW[con ? pair : 0];
+    const unsigned cbod = wor(con ? (1u << R.b1) | (1u << R.b2) : 0u) & ~1u;
+    const unsigned ccls = wor(con ? 1u << ((pwc >> 21) & 7u) : 0u);
+    const int cself = wsumi(con && R.b1 != 0 ? 1 : 0);
     if (lane == 0) {
+      s.acost += s.ncon + 4 * (__popc(cbod) + cself) + 8 * __popc(ccls);
+      rec[REC_ADJCOST] = __int_as_float(min(s.acost >> 2, COST_BUCKETS - 1));
       rec[REC_HDR] = __uint_as_float((unsigned)s.ncon | (unsigned)s.nefc << 8 | (unsigned)s.nlim << 16
                                      | (unsigned)min(no.it, 255) << 24);
       rec[REC_FLAGS] = __uint_as_float((unsigned)(s.flags & 20) | (no.fresh ? 0u : (unsigned)FLAG_REFACT)
@@ -1059,7 +1069,7 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
       for (int q = lane; q < POSE_WORDS; q += WL)
         s.L[cPoseSlots.pos[q]] = q >= 4 * NB && (q & 3) == 3 ? 0.f : (&s.Q[0][0])[q];
       wsync();
-      tape_put(rec + REC_LQ, s.L, NTRI, REC_WORDS - REC_LQ, lane);
+      tape_put(rec + REC_LQ, s.L, NTRI, REC_ADJCOST - REC_LQ, lane);
       if (lane < REC_LH - REC_AADV) rec[REC_AADV + lane] = lane < NV ? adv : 0.f;
     }
     wsync();
@@ -1126,7 +1136,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane < NV) { s.qvel[lane] = iv; s.qacc[lane] = iw; }
   if (lane < NU) s.ctrl[lane] = iu;
   if (lane < 3) s.com[lane] = ic;
-  if (lane == 0) { s.fric = ifr; s.flags = 0; s.niter = 0; s.dcnt = 0; }
+  if (lane == 0) { s.fric = ifr; s.flags = 0; s.niter = 0; s.dcnt = 0; s.acost = 0; }
   s.dsub[lane] = lane < NV ? cTree.dofmask32[lane] : 0u;
   chain_table(s.chain, lane);
   if (lane < 8) s.S[NV][lane] = 0.f;  // body_vel's zero padding row and entries

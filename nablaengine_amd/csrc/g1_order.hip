@@ -8,8 +8,9 @@
 // The cost is estimated per world before the launch, in the caller's work buffer:
 //   forward  contacts at the input state (the main kernel's broadphase and narrowphase): their constraint rows, and a
 //            weight per contact between two robot bodies (each makes the Newton Hessian dense);
-//   adjoint  the tape's contacts per substep: their count, the robot bodies they touch, the contacts between two
-//            robot bodies and the primitive classes present.
+//   adjoint  the taped forward's contacts per substep: their count, the robot bodies they touch, the contacts between
+//            two robot bodies and the primitive classes present, summed by the forward itself into its records
+//            (REC_ADJCOST, g1_forward.hip), so the adjoint's order needs no pass over the tape of its own.
 // Then one workgroup buckets the costs (LDS histogram, descending prefix) into the permutation the main kernel reads
 // as blockIdx.x -> world. Results do not depend on the order: every world's computation is the same wherever and
 // whenever it runs, so the permutation only moves work in time (its order inside a bucket is free).
@@ -19,7 +20,7 @@
 
 namespace g1k {
 
-constexpr int NBKT = 128;  // cost buckets
+constexpr int NBKT = COST_BUCKETS;
 
 // contacts at the input state: FK of body poses (each body lane walks its chain from the root), geom poses, the main
 // kernel's broadphase and narrowphase (the same code); the cost counts the contacts' constraint rows (4 per pyramid
@@ -107,56 +108,14 @@ __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict
   if (lane == 0) cost[w] = tot < NBKT ? tot : NBKT - 1;
 }
 
-// the adjoint's cost from the tape, one wave per world (4 worlds per workgroup of 256): per substep record its contacts
-// (the header word's ncon, the contact table's pairs: 16 bits each, lane l < 32 reading word l), the distinct robot
-// bodies they touch and the contacts between two robot bodies (4 each: the per-body wrench sums and the two-body
-// contact VJPs), and the primitive classes present (8 each: a lane's class branches run for the whole wave), in units
-// of 4. Measured on config-1 worlds (the profile build's per-world adjoint durations): the list schedule of the
-// launch in this order ends 3.4% earlier than ordered by the records' constraint rows, whose correlation with a
-// world's duration is 0.29. All records' loads are issued before the first is used, 4 records at a time.
-__global__ __launch_bounds__(256) void k_cost_adj(int nw, int nsub, const float* __restrict__ tape,
-                                                   int* __restrict__ cost) {
-  const int lane = threadIdx.x & 63, w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (w >= nw) return;  // wave-uniform
-  const int wl = lane & 31;
-  int c = 0;
-  for (int k0 = 0; k0 < nsub; k0 += 4) {
-    unsigned h[4], cw[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const float* rec = tape + ((size_t)w * nsub + min(k0 + u, nsub - 1)) * REC_WORDS;
-      h[u] = __float_as_uint(rec[REC_HDR]);
-      cw[u] = __float_as_uint(rec[REC_CON + wl]);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      if (k0 + u >= nsub) break;  // uniform
-      const int ncon = min((int)(h[u] & 255u), MAXCON);
-      unsigned bodies = 0u, cls = 0u;
-      int self = 0;
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        const unsigned v = (cw[u] >> (16 * e)) & 0xFFFFu;
-        if (lane < 32 && 2 * wl + e < ncon && v != TAPE_CON_NONE) {
-          const unsigned pw = cPairW[min((int)(v & 511u), NPAIR - 1)];
-          const int b1 = cGbody[pw & 255u], b2 = cGbody[(pw >> 8) & 255u];
-          bodies |= (1u << b1) | (1u << b2);
-          cls |= 1u << ((pw >> 21) & 7u);
-          self += b1 != 0;
-        }
-      }
-      c += ncon + 4 * (__popc(wor(bodies) & ~1u) + wsumi(self)) + 8 * __popc(wor(cls));
-    }
-  }
-  c >>= 2;
-  if (lane == 0) cost[w] = c < NBKT ? c : NBKT - 1;
-}
-
 // one workgroup of ORDER_THREADS: histogram of the costs, descending prefix (a suffix scan on one wave), scatter
 // (perm[slot] = world, heaviest first). Each thread takes its worlds ORDER_LOADS at a time, every load issued before
 // the first is used (one memory round trip per batch, not per world).
 constexpr int ORDER_THREADS = 1024, ORDER_LOADS = 8;
-__global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __restrict__ cost, int* __restrict__ perm) {
+// cost[w * cstride] is world w's bucket (the forward's estimates: contiguous; the adjoint's: a word of each world's
+// last record)
+__global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __restrict__ cost, size_t cstride,
+                                                         int* __restrict__ perm) {
   static_assert(NBKT == 128, "the bucket prefix: two buckets per lane of one wave");
   __shared__ int cnt[NBKT], cur[NBKT];
   const int t = threadIdx.x;
@@ -170,7 +129,7 @@ __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __re
 #pragma unroll
     for (int u = 0; u < ORDER_LOADS; u++) {
       const int w = w0 + u * ORDER_THREADS;
-      c[u] = w < nw ? cost[w] : -1;
+      c[u] = w < nw ? cost[w * cstride] : -1;
     }
 #pragma unroll
     for (int u = 0; u < ORDER_LOADS; u++) {
@@ -199,7 +158,7 @@ __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __re
 #pragma unroll
     for (int u = 0; u < ORDER_LOADS; u++) {
       const int w = w0 + u * ORDER_THREADS;
-      c[u] = w0 == t ? c0[u] : (w < nw ? cost[w] : -1);
+      c[u] = w0 == t ? c0[u] : (w < nw ? cost[w * cstride] : -1);
     }
 #pragma unroll
     for (int u = 0; u < ORDER_LOADS; u++)
@@ -208,22 +167,21 @@ __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __re
 }
 static_assert(NBKT <= ORDER_THREADS, "one thread clears each bucket");
 
-// work buffer: perm (nw int32), cost (nw int32)
+// work buffer: perm (nw int32), cost (nw int32: the forward's estimates; the adjoint's are in the tape)
 size_t order_work_bytes(int nw) { return nw > 0 ? ((8 * (size_t)nw + 255) & ~(size_t)255) : 0; }
 
 int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work) {
   int* perm = (int*)work;
   int* cost = perm + nw;
   hipLaunchKernelGGL(k_cost_fwd, dim3(nw), dim3(64), 0, st, nw, qpos, cost);
-  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, cost, perm);
+  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, (const int*)cost, (size_t)1, perm);
   return (int)hipGetLastError();
 }
 
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work) {
   int* perm = (int*)work;
-  int* cost = perm + nw;
-  hipLaunchKernelGGL(k_cost_adj, dim3((nw + 3) / 4), dim3(256), 0, st, nw, nsub, tape, cost);
-  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, cost, perm);
+  const int* cost = reinterpret_cast<const int*>(tape + (size_t)(nsub - 1) * REC_WORDS + REC_ADJCOST);
+  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, cost, (size_t)nsub * REC_WORDS, perm);
   return (int)hipGetLastError();
 }
 

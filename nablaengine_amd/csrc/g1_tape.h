@@ -19,7 +19,10 @@ constexpr int REC_ASTAR = 128;    // 35: Newton's final acceleration a*
 constexpr int REC_AADV = 164;     // 35: implicitfast's a_adv = (M + h kv)^-1 M a*
 constexpr int REC_LH = 200;       // 630: factor L of H = L' L = M + J'DJ at the final zones (packed lower, row-major)
 constexpr int REC_LQ = 832;       // 630: factor L of M + h kv = L' L, with the body frames in its off-pattern positions
+constexpr int REC_ADJCOST = 1471; // the adjoint's dispatch cost of the substeps up to this one (g1_order.hip): the last
+                                  // record's is the world's, which the adjoint's ordering reads
 constexpr int REC_WORDS = 1472;
+constexpr int COST_BUCKETS = 128; // dispatch costs are buckets 0 .. COST_BUCKETS - 1
 constexpr unsigned TAPE_CON_NONE = 0xFFFFu;
 constexpr int FLAG_REFACT = 1 << 8;    // the zones changed after the last Newton factorization: H re-factored for the tape
 constexpr int FLAG_NONCONV = 1 << 9;   // the Newton iterations ran out before the stopping test held

@@ -21,10 +21,10 @@ def ffi():
     return torch_ffi
 
 
-def _check(work, nw):
+def _check(work, nw, cost=None):
     import torch
     w = work.view(torch.int32)[:2 * nw].cpu().numpy()
-    perm, cost = w[:nw], w[nw:]
+    perm, cost = w[:nw], (w[nw:] if cost is None else cost)
     assert np.array_equal(np.sort(perm), np.arange(nw)), "not a permutation"
     assert cost.min() >= 0 and cost.max() < 128
     assert np.all(np.diff(cost[perm]) <= 0), "not heaviest first"
@@ -45,7 +45,8 @@ def test_forward_order_is_a_heaviest_first_bijection(ffi, nw):
 
 @pytest.mark.parametrize("nw", [7, 1000, 4096, 9001])
 def test_adjoint_order_is_a_heaviest_first_bijection(ffi, nw):
-    """dk_adjoint_order on a taped step's tape."""
+    """dk_adjoint_order on a taped step's tape, whose last record carries each world's cost (its last word, the
+    taped forward's estimate of the adjoint's work)."""
     import torch
     lib = ffi.load_library()
     st = synthetic.states(nw, config=4, seed=nw)
@@ -55,4 +56,5 @@ def test_adjoint_order_is_a_heaviest_first_bijection(ffi, nw):
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert lib.dk_adjoint_order(stream, nw, 4, ctypes.c_void_p(tape.data_ptr()),
                                 ctypes.c_void_p(work.data_ptr())) == 0
-    _check(work, nw)
+    cost = tape.view(torch.int32).reshape(nw, 4, -1)[:, 3, -1].cpu().numpy()
+    _check(work, nw, cost)

@@ -220,3 +220,32 @@ def test_taped_frames_vs_oracle(ffi):
         ep = max(ep, np.abs(X[:, :, :3] - xpos).max())
     print(f"record frames vs float64 FK: quaternions max {eq:.3g}, positions max {ep:.3g} m")
     assert eq <= 2e-6 and ep <= 2e-6
+
+
+def test_taped_adjoint_cost(ffi):
+    """Each record's last word is the adjoint's dispatch-cost bucket of the substeps up to it (the adjoint's ordering
+    reads the last record's): per substep its contacts, plus 4 per distinct robot body they touch and per contact
+    between two robot bodies, plus 8 per primitive class present (plane-sphere, sphere-sphere, sphere-capsule,
+    capsule-capsule, plane-capsule), summed, in units of 4, at most 127. Restated here from the records' own headers
+    and contact tables on contact-heavy states."""
+    import torch
+    B = 256
+    st = synthetic.states(B, config=4, seed=9)
+    args = [_t(st[k]) for k in KEYS]
+    tape = ffi.forward(*args, tape=True)[4].view(torch.int32).cpu().numpy().reshape(B, 4, -1).astype(np.int64)
+    m = synthetic.model()
+    g1, g2 = np.asarray(m["pair_g1"]), np.asarray(m["pair_g2"])
+    gb, gt = np.asarray(m["geom_body"]), np.asarray(m["geom_type"])
+    for w in range(B):
+        c = 0
+        for k in range(4):
+            rec = tape[w, k]
+            ncon = int(rec[REC_HDR] & 255)
+            half = rec[REC_CON:REC_CON + 32].astype(np.uint32).view(np.uint16).reshape(64)[:ncon]
+            prs = (half & 511).astype(int)
+            bodies = set(gb[g1[prs]]) | set(gb[g2[prs]])
+            bodies.discard(0)
+            self_n = int((gb[g1[prs]] != 0).sum())
+            classes = {(gt[g1[p]], gt[g2[p]]) for p in prs}
+            c += ncon + 4 * (len(bodies) + self_n) + 8 * len(classes)
+            assert rec[-1] == min(c >> 2, 127), (w, k, rec[-1], c)
