@@ -83,7 +83,9 @@ struct __align__(16) Adj {
   unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
   float O[4];
   float fric;
-  float Ib[NB][12];
+  // 16-byte aligned after the scalar above, and with it tw, gx, gq (their sizes are multiples of 16 bytes): the
+  // compiler merges their float loads and stores into 64- to 128-bit LDS accesses only where it knows the alignment
+  __align__(16) float Ib[NB][12];
   float tw[NB][NTW][6];              // per-body twists (6 floats each)
   float gx[NGEOM][4], gq[NGEOM][4];
   union {
