@@ -112,8 +112,7 @@ __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict
 // (perm[slot] = world, heaviest first). Each thread takes its worlds ORDER_LOADS at a time, every load issued before
 // the first is used (one memory round trip per batch, not per world).
 constexpr int ORDER_THREADS = 1024, ORDER_LOADS = 8;
-// cost[w * cstride] is world w's bucket (the forward's estimates: contiguous; the adjoint's: a word of each world's
-// last record)
+// cost[w * cstride] is world w's bucket
 __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __restrict__ cost, size_t cstride,
                                                          int* __restrict__ perm) {
   static_assert(NBKT == 128, "the bucket prefix: two buckets per lane of one wave");
@@ -167,7 +166,7 @@ __global__ __launch_bounds__(ORDER_THREADS) void k_order(int nw, const int* __re
 }
 static_assert(NBKT <= ORDER_THREADS, "one thread clears each bucket");
 
-// work buffer: perm (nw int32), cost (nw int32: the forward's estimates; the adjoint's are in the tape)
+// work buffer: perm (nw int32), cost (nw int32)
 size_t order_work_bytes(int nw) { return nw > 0 ? ((8 * (size_t)nw + 255) & ~(size_t)255) : 0; }
 
 int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work) {
@@ -178,10 +177,21 @@ int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work) {
   return (int)hipGetLastError();
 }
 
+// the adjoint's costs gathered from the tape into the work buffer, one thread per world: the words lie a world's
+// tape apart (23.5 KB at 4 substeps), and the ordering workgroup's 1024 threads alone, loading them where they lie,
+// took 42 us at 16384 worlds (this gather and the order from the gathered costs: a fraction of that)
+__global__ __launch_bounds__(256) void k_gather_cost(int nw, const int* __restrict__ src, size_t stride,
+                                                      int* __restrict__ cost) {
+  const int w = blockIdx.x * 256 + threadIdx.x;
+  if (w < nw) cost[w] = src[w * stride];
+}
+
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work) {
   int* perm = (int*)work;
-  const int* cost = reinterpret_cast<const int*>(tape + (size_t)(nsub - 1) * REC_WORDS + REC_ADJCOST);
-  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, cost, (size_t)nsub * REC_WORDS, perm);
+  int* cost = perm + nw;
+  const int* src = reinterpret_cast<const int*>(tape + (size_t)(nsub - 1) * REC_WORDS + REC_ADJCOST);
+  hipLaunchKernelGGL(k_gather_cost, dim3((nw + 255) / 256), dim3(256), 0, st, nw, src, (size_t)nsub * REC_WORDS, cost);
+  hipLaunchKernelGGL(k_order, dim3(1), dim3(ORDER_THREADS), 0, st, nw, (const int*)cost, (size_t)1, perm);
   return (int)hipGetLastError();
 }
 
