@@ -817,53 +817,25 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   }
   wsync();
   APROF(AP_FORCES);
-  // per body B: the subtree sums T[B] = sum of fb[b] over the bodies b of B's subtree (54 floats each), as the product
-  // T = A F (32 x 32 x 64, A[B][b] = 1 for b in B's subtree, 0 for the world and the padding) on the matrix cores:
-  // v_mfma_f32_16x16x4f32, lane l giving A[l % 16][l / 16] and F[l / 16][l % 16] and holding C[4 (l / 16) + e][l % 16];
-  // 2 x 4 tiles, 8 steps of k = 4, in two passes over 32 columns each. A pass reads only its own columns of F, every
-  // load before its first store, so T overwrites fb in place.
+  // per body B: the subtree sums T[B] = sum of fb[b] over the bodies b of B's subtree (54 floats each), a column per
+  // lane: lane c < 54 loads column c of every body and adds each body into its parent, highest id first (a body's id
+  // is above its parent's, so each body is complete when it is added), then stores the sums in place. The tree is
+  // compile-time: 29 adds a lane, no masks. Lanes past the columns compute a copy of the last one and do not store.
   {
     constexpr int NF = NFB * 6;
-    float* F = &s.fb[0][0][0];
-    const int lr = lane & 15, lk = lane >> 4;
-    const unsigned sm[2] = {lr >= 1 ? cTree.submask[lr] : 0u, 16 + lr < NB ? cTree.submask[16 + lr] : 0u};
-#pragma unroll 1
-    for (int half = 0; half < 2; half++) {
-      mfma4 acc[2][2];
+    static_assert(NF <= WL, "a column per lane");
+    float* F = &s.fb[0][0][0] + (lane < NF ? lane : NF - 1);
+    float v[NB];
 #pragma unroll
-      for (int m = 0; m < 2; m++)
+    for (int b = 1; b < NB; b++) v[b] = F[b * NF];
+    static_for<NB - 1, 1, -1>([&](auto bc) {
+      constexpr int b = decltype(bc)::value;
+      static_assert(BODY_PARENT[b] >= 1 && BODY_PARENT[b] < b, "bodies numbered parents first");
+      v[BODY_PARENT[b]] += v[b];
+    });
+    if (lane < NF)
 #pragma unroll
-        for (int n = 0; n < 2; n++) acc[m][n] = mfma4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const int kb = 4 * t + lk;  // the body of this lane's k index
-        const bool kin = kb >= 1 && kb < NB;
-        float bv[2];
-#pragma unroll
-        for (int n = 0; n < 2; n++) {
-          const int c = 32 * half + 16 * n + lr;
-          const bool ok = kin && c < NF;
-          const float x = F[ok ? kb * NF + c : 0];
-          bv[n] = ok ? x : 0.f;
-        }
-#pragma unroll
-        for (int m = 0; m < 2; m++) {
-          const float av = kin && ((sm[m] >> kb) & 1u) ? 1.f : 0.f;
-#pragma unroll
-          for (int n = 0; n < 2; n++)
-            acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[n], acc[m][n], 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < 2; m++)
-#pragma unroll
-        for (int n = 0; n < 2; n++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int B = 16 * m + 4 * lk + e, c = 32 * half + 16 * n + lr;
-            if (B >= 1 && B < NB && c < NF) F[B * NF + c] = acc[m][n][e];
-          }
-    }
+      for (int b = 1; b < NB; b++) F[b * NF] = v[b];
   }
   wsync();
   APROF(AP_SUBTREE);

@@ -5,6 +5,8 @@
 namespace g1k {
 
 constexpr int MSTRIDE = 36;
+// the smooth dynamics' per-body row: force, moment about O, spatial inertia (10 of 12), each 16-byte aligned
+constexpr int SM_F = 0, SM_T = 4, SM_I = 8, SMW = 20;
 
 struct __align__(16) Sim {
   // the dof vectors have a 36th entry, 0 (body_vel reads entry NV for a chain's padding)
@@ -26,8 +28,9 @@ struct __align__(16) Sim {
   unsigned long long prof_t, prof_acc[NPHASE];
 #endif
   union __align__(16) {  // 16-byte aligned whatever the scalars above add up to (its rows are read as float4s)
-    struct { float F[NB][4], T[NB][4], Ic[NB][12], hl[NB][12]; } sm;  // smooth dynamics: subtree force, moment about O,
-                                                                     // inertia; bodies' local transforms
+    // smooth dynamics: per body its force (SM_F + 0..2), moment about O (SM_T + 0..2) and spatial inertia about O
+    // (SM_I + 0..9), summed over its subtree in place; the bodies' local transforms
+    struct { float V[NB][SMW], hl[NB][12]; } sm;
     struct { float gx[NGEOM][4], gq[NGEOM][4]; float stage[MAXCON][16]; unsigned short cand[NPAIR + 2]; } col;
     struct {
       float bw[NB][8];  // body spatial velocity of a dof vector: angular (0..2), velocity of O (4..6)

@@ -179,14 +179,14 @@ __device__ void smooth(Sim& s, int lane) {
     // moment about O
     float xo[3] = {X[0] - s.qpos[0], X[1] - s.qpos[1], X[2] - s.qpos[2]}, xf[3];
     cross(xo, F, xf);
-    for (int k = 0; k < 3; k++) { s.u.sm.F[lane][k] = F[k]; s.u.sm.T[lane][k] = N[k] + xf[k]; }
+    for (int k = 0; k < 3; k++) { s.u.sm.V[lane][SM_F + k] = F[k]; s.u.sm.V[lane][SM_T + k] = N[k] + xf[k]; }
     // spatial inertia about O (source.py:280-302 body_inertia)
     float R[9];
     for (int k = 0; k < 3; k++) {
       float e[3] = {(float)(k == 0), (float)(k == 1), (float)(k == 2)};
       qrot(qi, e, R + 3 * k);
     }
-    float* J = s.u.sm.Ic[lane];
+    float* J = s.u.sm.V[lane] + SM_I;
     J[0] = In[0] * R[0] * R[0] + In[1] * R[3] * R[3] + In[2] * R[6] * R[6];
     J[1] = In[0] * R[1] * R[1] + In[1] * R[4] * R[4] + In[2] * R[7] * R[7];
     J[2] = In[0] * R[2] * R[2] + In[1] * R[5] * R[5] + In[2] * R[8] * R[8];
@@ -202,34 +202,24 @@ __device__ void smooth(Sim& s, int lane) {
   }
   wsync();
   PROF(PH_SBF);
-  // subtree sums per body B of the force, the moment about O and the spatial inertia (16 floats), as the product
-  // T = A V (32 x 32 x 16, A[B][b] = 1 for b in B's subtree, 0 for the world and the padding; V[b] = body b's 16
-  // floats) on the matrix cores: v_mfma_f32_16x16x4f32, lane l giving A[l % 16][l / 16] and V[l / 16][l % 16] and
-  // holding C[4 (l / 16) + e][l % 16]; 2 row tiles, 8 steps of k = 4. Every load is issued before the first store, so
-  // the sums overwrite the bodies' own values in place.
+  // subtree sums per body B of the force, the moment about O and the spatial inertia (16 floats), a column per lane:
+  // lane c < 16 loads column c of every body and adds each body into its parent, highest id first (a body's id is
+  // above its parent's, so each body is complete when it is added), then stores the sums in place. The tree is
+  // compile-time: 29 adds a lane, no masks. Lanes past the columns compute a copy of the last one and do not store.
   {
-    const int lr = lane & 15, lk = lane >> 4;
-    float* col = lr < 3 ? &s.u.sm.F[0][lr] : (lr < 6 ? &s.u.sm.T[0][lr - 3] : &s.u.sm.Ic[0][lr - 6]);  // column lr
-    const int cs = lr < 6 ? 4 : 12;  // its stride
-    const unsigned sm[2] = {lr >= 1 ? cTree.submask[lr] : 0u, 16 + lr < NB ? cTree.submask[16 + lr] : 0u};
-    mfma4 acc[2] = {mfma4{0.f, 0.f, 0.f, 0.f}, mfma4{0.f, 0.f, 0.f, 0.f}};
+    const int c = lane < 16 ? lane : 15;
+    float* col = &s.u.sm.V[0][c < 3 ? SM_F + c : (c < 6 ? SM_T + c - 3 : SM_I + c - 6)];
+    float v[NB];
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const int kb = 4 * t + lk;  // the body of this lane's k index
-      const bool kin = kb >= 1 && kb < NB;
-      const float x = col[(kin ? kb : 1) * cs];
-      const float bv = kin ? x : 0.f;
+    for (int b = 1; b < NB; b++) v[b] = col[b * SMW];
+    static_for<NB - 1, 1, -1>([&](auto bc) {
+      constexpr int b = decltype(bc)::value;
+      static_assert(BODY_PARENT[b] >= 1 && BODY_PARENT[b] < b, "bodies numbered parents first");
+      v[BODY_PARENT[b]] += v[b];
+    });
+    if (lane < 16)
 #pragma unroll
-      for (int m = 0; m < 2; m++)
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(kin && ((sm[m] >> kb) & 1u) ? 1.f : 0.f, bv, acc[m], 0, 0, 0);
-    }
-#pragma unroll
-    for (int m = 0; m < 2; m++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int B = 16 * m + 4 * lk + e;
-        if (B >= 1 && B < NB) col[B * cs] = acc[m][e];
-      }
+      for (int b = 1; b < NB; b++) col[b * SMW] = v[b];
   }
   PROF(PH_SSUB);
   // motion subspaces
@@ -248,10 +238,10 @@ __device__ void smooth(Sim& s, int lane) {
     // subtree force / moment about the body origin X_b: N_b = T - (X_b - O) x F; the projection on a dof through O:
     // S . (T, F) with S = (w, w x (O - X_b)) equals w . N_b
     float Fb[3], Tb[3];
-    for (int k = 0; k < 3; k++) { Fb[k] = s.u.sm.F[bi][k]; Tb[k] = s.u.sm.T[bi][k]; }
+    for (int k = 0; k < 3; k++) { Fb[k] = s.u.sm.V[bi][SM_F + k]; Tb[k] = s.u.sm.V[bi][SM_T + k]; }
     bias = dot3(w, Tb) + dot3(v, Fb);
     float Jb[10], n[3], f[3];
-    for (int k = 0; k < 10; k++) Jb[k] = s.u.sm.Ic[bi][k];
+    for (int k = 0; k < 10; k++) Jb[k] = s.u.sm.V[bi][SM_I + k];
     apply_inertia(Jb, w, v, n, f);
     // M[i][j] = S_j . I_c(body i) S_i on the chain of dof i's body (its ancestor dofs j <= i), both halves; the
     // rest of M is zero (zero-filled above, earlier in this wave's LDS order). Two lanes never store the same entry:

@@ -26,7 +26,7 @@ FWD_GROUPS = {
 FWD_COUNTS = {"Newton iterations": 12, "line-search evaluations": 13, "factorizations with self-contact fill": 14}
 ADJ_GROUPS = {  # g1_adjoint.hip AP_*
     "record": [0], "poses": [1], "solves": [2], "twists": [3], "contacts": [4], "per-body wrench sums": [5],
-    "body forces": [6], "dof terms": [7], "subtree sums (MFMA)": [10],
+    "body forces": [6], "dof terms": [7], "subtree sums": [10],
 }
 
 
