@@ -706,28 +706,37 @@ __device__ __forceinline__ int hessian(Sim& s, const Rows& R, int lane, bool con
       }
     }
     wsync();
-    {  // H += U U' on the matrix cores: 16 x 16 tiles (ti, tj <= ti) of the 48-row padding, k = 16 rows in steps of 4
-      // (v_mfma_f32_16x16x4f32: lane l gives A[l % 16][l / 16] and B[l / 16][l % 16], holds C[4 (l / 16) + e][l % 16])
+    {  // H += U U' on the matrix cores: 16 x 16 tiles (ti, tj <= ti) of the 48-row padding, k = the batch's edge rows
+      // in steps of 4 (v_mfma_f32_16x16x4f32: lane l gives A[l % 16][l / 16] and B[l / 16][l % 16], holds
+      // C[4 (l / 16) + e][l % 16]). Step kk takes U's columns 4 kk .. 4 kk + 3, contact kk's 4 edge rows, so a batch
+      // of nb contacts needs nb steps: the 6 tiles' chains are nb deep, not SELF_BATCH
       const int lr = lane & 15, lk = lane >> 4;
-      float op[3][4];
+      const int nb = __popcll(bm);
+      mfma4 acc[6];
 #pragma unroll
-      for (int t = 0; t < 3; t++)
+      for (int n = 0; n < 6; n++) acc[n] = mfma4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+      for (int kk = 0; kk < nb; kk++) {
+        float op[3];
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) op[t][kk] = s.u.nt.h.U[16 * t + lr][4 * kk + lk];
+        for (int t = 0; t < 3; t++) op[t] = s.u.nt.h.U[16 * t + lr][4 * kk + lk];
+        int n = 0;
 #pragma unroll
-      for (int ti = 0; ti < 3; ti++) {
+        for (int ti = 0; ti < 3; ti++)
 #pragma unroll
-        for (int tj = 0; tj <= ti; tj++) {
-          mfma4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int tj = 0; tj <= ti; tj++, n++)
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(op[ti], op[tj], acc[n], 0, 0, 0);
+      }
+      int n = 0;
 #pragma unroll
-          for (int kk = 0; kk < 4; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(op[ti][kk], op[tj][kk], acc, 0, 0, 0);
+      for (int ti = 0; ti < 3; ti++)
+#pragma unroll
+        for (int tj = 0; tj <= ti; tj++, n++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             const int i = 16 * ti + 4 * lk + e, j = 16 * tj + lr;
-            s.L[i < NV && j <= i ? tri(i, j) : LSINK + lane] += acc[e];  // off the triangle: the lane's sink
+            s.L[i < NV && j <= i ? tri(i, j) : LSINK + lane] += acc[n][e];  // off the triangle: the lane's sink
           }
-        }
-      }
     }
     wsync();
   }
