@@ -566,70 +566,101 @@ __device__ __forceinline__ void adj_solves(Adj& s, int lane, bool clear) {
   wsync();
 }
 
-// chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body. Every
-// body's chain starts with the root's 6 dofs, S_0..2 = (0; e_k) and S_3..5 = (w_k; 0): their part of a twist is
-// (sum_k w_k x_{3+k}; x_0..2), the same on every lane, and their RNE term, V x (S_r v_r) summed over r = 3..5 with
-// V = (w; u) the root's velocity twist, is (w x w; u x w) = (0; u x w). The hinge dofs follow (chain entries 6..15);
-// the padding byte 255 clamps to dof NV, whose S row and entries are zero, so every step is unconditional.
+// chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body.
+// The twist of a dof vector x is T[b] = T[parent(b)] + S_d x_d down the tree (d = b + 4, a hinge body's one dof)
+// from the root body's T[1] = (sum_k S_{3+k}.w x_{3+k}; x_0..2) (S_0..2 = (0; e_k), S_3..5 = (w_k; 0)): a column per
+// lane, lane 6 k + e holding component e of kind k for every body in registers, 2 loads and an FMA a body in
+// ascending id order (a body's id is above its parent's; the parent table is compile-time). These are the sums
+// along each body's chain in its order, root first. The RNE acceleration's velocity-product term is
+// Ac[b] = (0; u x w) + sum over b's hinge chain of (V[body(d)] x S_d) v_d, V = (w; u) the root's velocity twist in
+// the first term: each body lane stages its own cross product once, then sums its chain's in chain order; the
+// padding byte 255 clamps to dof NV, whose entry of v is zero (its staged product is the last body's, finite).
 // STATE: the twists of v, a*, a~ and the RNE acceleration (the record's); COT: those of lambda and y (the
-// cotangent's). Each twist is its own chain of sums, the same with either part alone.
+// cotangent's). Each twist is its own chain of sums in the same order either way, so the results are the same with
+// either part alone, and the same as adj_twists_cot's.
 template <bool STATE, bool COT>
 __device__ __forceinline__ void adj_twists(Adj& s, int lane) {
+  constexpr int NK = (STATE ? 3 : 0) + (COT ? 2 : 0);  // kinds: STATE's v, a*, a~, then COT's lambda, y
+  static_assert(6 * NK <= WL, "a column per lane");
+  if (lane < 6 * NK) {
+    const int k = lane / 6, e = lane - 6 * k;
+    const int kk = STATE ? k : k + 3;  // 0 v, 1 a*, 2 a~, 3 lambda, 4 y
+    const float* x = kk == 0 ? s.qvel : kk == 1 ? s.astar : kk == 2 ? s.at : kk == 3 ? s.lam : s.y;
+    const int slot = kk == 0 ? TW_V : kk == 1 ? TW_AW : kk == 2 ? TW_A2 : kk == 3 ? TW_L : TW_Y;
+    const int so = e < 3 ? e : e + 1;  // the component's place in a row of S: w at 0..2, v at 4..6
+    float T[NB];
+    const float tw = s.S[3][so] * x[3] + s.S[4][so] * x[4] + s.S[5][so] * x[5];
+    T[1] = e < 3 ? tw : x[e < 3 ? 0 : e - 3];
+    static_for<2, NB, 1>([&](auto bc) {
+      constexpr int b = decltype(bc)::value;
+      static_assert(BODY_PARENT[b] >= 1 && BODY_PARENT[b] < b, "bodies numbered parents first");
+      T[b] = fmaf(s.S[b + 4][so], x[b + 4], T[BODY_PARENT[b]]);
+    });
+    float* out = &s.tw[0][slot][e];
+    out[0] = 0.f;  // the world body
+#pragma unroll
+    for (int b = 1; b < NB; b++) out[b * NTW * 6] = T[b];
+  }
+  if (STATE) {
+    if (lane == 0) st_sv6(s.tw[0][TW_A1], sv0());
+    wsync();  // the velocity twists stored
+    if (lane >= 1 && lane < NB) {  // this body's term of the chain sums: (V[b] x S_d) for its dof d, the root's (0; u x w)
+      const Sv V = ld_sv6(s.tw[lane][TW_V]);
+      Sv c = sv0();
+      if (lane == 1) cross(V.v, V.w, c.v);
+      else c = cross_mm(V, ld_sv(s.S[lane + 4]));
+      st_sv6(s.tw[lane][TW_A1], c);
+    }
+    wsync();
+    if (lane >= 1 && lane < NB) {
+      unsigned ch[4];
+      for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
+      Sv Ac = ld_sv6(s.tw[1][TW_A1]);
+#pragma unroll
+      for (int t = NROOT; t < MAXCHAIN; t++) {
+        const unsigned b = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
+        const int d = (int)min(b, (unsigned)NV);
+        Ac = sv_add(Ac, ld_sv6(s.tw[min(d - 4, NB - 1)][TW_A1]), s.qvel[d]);
+      }
+      Sv A1 = sv_add(ld_sv6(s.tw[lane][TW_AW]), Ac);
+      for (int k = 0; k < 3; k++) A1.v[k] -= kGrav[k];
+      st_sv6(s.tw[lane][TW_A1], A1);  // after every lane's reads of the staged terms (one wave, program order)
+    }
+  }
+  wsync();
+}
+
+// The twists of lambda and y alone (the cotangent passes of k_adjoint_sets) as each body lane's walk down its chain
+// (the root's part as in adj_twists, then the hinge dofs in chain order; the padding byte 255 clamps to dof NV,
+// whose S row and entries are zero): the same sums in the same order as adj_twists. For these two kinds the walk
+// (12 running values a lane) runs the Jacobian faster than the column pass (31 a lane): k_adjoint_sets is at 256
+// VGPRs.
+__device__ __forceinline__ void adj_twists_cot(Adj& s, int lane) {
   if (lane >= 1 && lane < NB) {
     unsigned ch[4];
     for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
-    const auto root = [&](const float* x) {
-      Sv r;
-      for (int k = 0; k < 3; k++) {
-        r.w[k] = s.S[3][k] * x[3] + s.S[4][k] * x[4] + s.S[5][k] * x[5];
-        r.v[k] = x[k];
-      }
-      return r;
-    };
-    Sv V = sv0(), Lm = sv0(), Y = sv0(), Aw = sv0(), A2 = sv0(), Ac = sv0();
-    if (STATE) {
-      V = root(s.qvel);
-      Aw = root(s.astar);
-      A2 = root(s.at);
-      cross(V.v, V.w, Ac.v);
-    }
-    if (COT) {
-      Lm = root(s.lam);
-      Y = root(s.y);
+    Sv Lm, Y;
+    for (int k = 0; k < 3; k++) {
+      Lm.w[k] = s.S[3][k] * s.lam[3] + s.S[4][k] * s.lam[4] + s.S[5][k] * s.lam[5];
+      Y.w[k] = s.S[3][k] * s.y[3] + s.S[4][k] * s.y[4] + s.S[5][k] * s.y[5];
+      Lm.v[k] = s.lam[k];
+      Y.v[k] = s.y[k];
     }
 #pragma unroll
     for (int t = NROOT; t < MAXCHAIN; t++) {
       const unsigned b = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
       const int d = (int)min(b, (unsigned)NV);
       const Sv Sd = ld_sv(s.S[d]);
-      const float vd = s.qvel[d];
-      if (STATE) V = sv_add(V, Sd, vd);
-      if (COT) {
-        Lm = sv_add(Lm, Sd, s.lam[d]);
-        Y = sv_add(Y, Sd, s.y[d]);
-      }
-      if (STATE) {
-        Aw = sv_add(Aw, Sd, s.astar[d]);
-        A2 = sv_add(A2, Sd, s.at[d]);
-        Ac = sv_add(Ac, cross_mm(V, Sd), vd);
-      }
+      Lm = sv_add(Lm, Sd, s.lam[d]);
+      Y = sv_add(Y, Sd, s.y[d]);
     }
-    Sv A1 = sv_add(Aw, Ac);
-    for (int k = 0; k < 3; k++) A1.v[k] -= kGrav[k];
-    if (STATE) st_sv6(s.tw[lane][TW_V], V);
-    if (COT) {
-      st_sv6(s.tw[lane][TW_L], Lm);
-      st_sv6(s.tw[lane][TW_Y], Y);
-    }
-    if (STATE) {
-      st_sv6(s.tw[lane][TW_AW], Aw);
-      st_sv6(s.tw[lane][TW_A2], A2);
-      st_sv6(s.tw[lane][TW_A1], A1);
-    }
+    st_sv6(s.tw[lane][TW_L], Lm);
+    st_sv6(s.tw[lane][TW_Y], Y);
   }
-  if (lane == 0)
-    for (int t = 0; t < NTW; t++)
-      if ((t == TW_L || t == TW_Y) ? COT : STATE) st_sv6(s.tw[0][t], sv0());
+  if (lane == 0) {
+    st_sv6(s.tw[0][TW_L], sv0());
+    st_sv6(s.tw[0][TW_Y], sv0());
+  }
   wsync();
 }
 
@@ -656,7 +687,8 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     adj_solves(s, lane, recopied);
     APROF(AP_SOLVE);
   }
-  adj_twists<STATE, COT>(s, lane);
+  if constexpr (STATE) adj_twists<STATE, COT>(s, lane);
+  else adj_twists_cot(s, lane);
   APROF(AP_TWIST);
   if (!COT) return;
   // limit rows (their dof's lane): through the distance only (J constant)
