@@ -630,36 +630,36 @@ __device__ __forceinline__ void adj_twists(Adj& s, int lane) {
   wsync();
 }
 
-// The twists of lambda and y alone (the cotangent passes of k_adjoint_sets) as each body lane's walk down its chain
-// (the root's part as in adj_twists, then the hinge dofs in chain order; the padding byte 255 clamps to dof NV,
-// whose S row and entries are zero): the same sums in the same order as adj_twists. For these two kinds the walk
-// (12 running values a lane) runs the Jacobian faster than the column pass (31 a lane): k_adjoint_sets is at 256
-// VGPRs.
+// The twists of lambda and y alone (the cotangent passes of k_adjoint_sets) down the tree along the G1's four
+// root-to-leaf paths (the two legs; the waist and then either arm), one group of 16 lanes a path, lane c < 12 of a
+// group carrying component c % 6 of lambda's (c < 6) or y's twist: from the root body's (as in adj_twists) each
+// path's bodies in order, an FMA of the body's one dof each (2 loads, an FMA and a store a step, every address a
+// per-lane base plus a compile-time offset): the same sums in the same order as adj_twists. Both arm groups compute
+// the waist's bodies (the same values); the legs' groups run 4 steps past their 6 bodies, and lanes c >= 12 every
+// step, into a sink (the factors' copies, read by the solves before this).
 __device__ __forceinline__ void adj_twists_cot(Adj& s, int lane) {
-  if (lane >= 1 && lane < NB) {
-    unsigned ch[4];
-    for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
-    Sv Lm, Y;
-    for (int k = 0; k < 3; k++) {
-      Lm.w[k] = s.S[3][k] * s.lam[3] + s.S[4][k] * s.lam[4] + s.S[5][k] * s.lam[5];
-      Y.w[k] = s.S[3][k] * s.y[3] + s.S[4][k] * s.y[4] + s.S[5][k] * s.y[5];
-      Lm.v[k] = s.lam[k];
-      Y.v[k] = s.y[k];
-    }
+  const int g = lane >> 4, c = lane & 15;
+  const bool comp = c < 12;
+  const int e = c < 6 ? c : (comp ? c - 6 : 0);
+  const float* x = c < 6 ? s.lam : s.y;
+  const int slot = c < 6 ? TW_L : TW_Y;
+  const int so = e < 3 ? e : e + 1;  // the component's place in a row of S: w at 0..2, v at 4..6
+  const int lo = g == 0 ? PATHS.lo[0] : g == 1 ? PATHS.lo[1] : g == 2 ? PATHS.lo[2] : PATHS.lo[3];
+  const int hi = g == 0 ? PATHS.hi[0] : g == 1 ? PATHS.hi[1] : g == 2 ? PATHS.hi[2] : PATHS.hi[3];
+  constexpr int TWB = NTW * 6;  // a body's twist row
+  float* sink = s.lt.q + (lane & 7);
+  static_assert(TWB * (PATH_STEPS - 1) + 8 <= 768, "the sink inside the factors' copy");
+  const float rw = s.S[3][so] * x[3] + s.S[4][so] * x[4] + s.S[5][so] * x[5];
+  float T = e < 3 ? rw : x[e < 3 ? 0 : e - 3];
+  (comp && g < 2 ? &s.tw[1 - g][slot][e] : sink)[0] = g == 0 ? T : 0.f;  // the root body; the world body 0
+  const float *Sa = &s.S[4 + lo][so], *Sb = &s.S[4 + hi][so], *xa = x + 4 + lo, *xb = x + 4 + hi;
+  float* oa = comp ? &s.tw[lo][slot][e] : sink;
+  float* ob = comp ? &s.tw[hi][slot][e] : sink;
+  float* oc = comp && g >= 2 ? ob : sink;  // past the legs' 6 bodies only the arm groups' are real
 #pragma unroll
-    for (int t = NROOT; t < MAXCHAIN; t++) {
-      const unsigned b = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
-      const int d = (int)min(b, (unsigned)NV);
-      const Sv Sd = ld_sv(s.S[d]);
-      Lm = sv_add(Lm, Sd, s.lam[d]);
-      Y = sv_add(Y, Sd, s.y[d]);
-    }
-    st_sv6(s.tw[lane][TW_L], Lm);
-    st_sv6(s.tw[lane][TW_Y], Y);
-  }
-  if (lane == 0) {
-    st_sv6(s.tw[0][TW_L], sv0());
-    st_sv6(s.tw[0][TW_Y], sv0());
+  for (int i = 0; i < PATH_STEPS; i++) {
+    T = fmaf((i < 3 ? Sa : Sb)[8 * i], (i < 3 ? xa : xb)[i], T);
+    (i < 3 ? oa : i < 6 ? ob : oc)[TWB * i] = T;
   }
   wsync();
 }

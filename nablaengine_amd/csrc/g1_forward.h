@@ -9,12 +9,12 @@ constexpr int MSTRIDE = 36;
 constexpr int SM_F = 0, SM_T = 4, SM_I = 8, SMW = 20;
 
 struct __align__(16) Sim {
-  // the dof vectors have a 36th entry, 0 (body_vel reads entry NV for a chain's padding)
+  // the dof vectors padded to 36 entries (16-byte multiples; matvec reads them as float4s)
   float qpos[40], qvel[36], qacc[36], ctrl[32], com[4];
   float qsm[36], qacc0[36], Ma[36], grad[36], p[36], Mp[36];
   float M[NV][MSTRIDE];  // the mass matrix, full and symmetric, row-major (rows 16-byte aligned; column 35 unused)
   float L[LSINK + 64];  // the packed factor (NTRI + 2 padding), then the per-lane sink of masked stores
-  float S[NV + 1][8];         // dof motion subspaces about O: angular (0..2), velocity of O (4..6); row NV zero
+  float S[NV + 1][8];         // dof motion subspaces about O: angular (0..2), velocity of O (4..6); row NV unused
   float Q[NB][4], X[NB][4];   // body poses
   unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
   unsigned dsub[WL];                 // bodies moved by dof i (bit b), 0 past the dofs

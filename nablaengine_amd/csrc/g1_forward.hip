@@ -367,26 +367,32 @@ __constant__ inline Arr<float, 2> cPSolref = to_float(PAIR_SOLREF);
 __constant__ inline Arr<float, 5> cPSolimp = to_float(PAIR_SOLIMP);
 static_assert(JNT_SOLIMP[4] == 2.0 && PAIR_SOLIMP[4] == 2.0, "kbimp assumes the solimp power 2");
 
-// body spatial velocities of the dof vector v (LDS, NV + 1 entries, v[NV] = 0): bw[b] = sum over b's chain of S_d v_d.
-// Every body's chain starts with the root's 6 dofs, whose subspaces are S_0..2 = (0; e_k) and S_3..5 = (S_k's
-// angular part; 0): their part is v[0..2] and 3 columns, the same on every lane (broadcast loads). The hinge dofs
-// follow (chain entries 6..15); the table's padding byte 255 clamps to dof NV, whose S row and v entry are zero, so
-// every step is unconditional and needs no mask. The world body (lane 0) gets 0.
+// body spatial velocities of the dof vector v (LDS): bw[b] = sum over b's chain of S_d v_d, down the tree: the root
+// body's from the root's 6 dofs (S_0..2 = (0; e_k), S_3..5 = (w_k; 0): v[0..2] and 3 columns), then each hinge body's
+// is its parent's plus S_d v_d of its one dof d = b + 4. Four groups of 16 lanes walk the four paths from the root to
+// the leaves (PATHS), lane c < 6 of a group carrying component c: the sums of each body's chain in its order, 10 steps
+// of 2 loads, an FMA and a store, every address a per-lane base plus a compile-time offset. Both arm groups compute
+// the waist's bodies (the same values); the legs' groups run 4 steps past their 6 bodies, and lanes c >= 6 every
+// step, into a sink (the Hessian's self-contact staging, unused outside the Hessian). The world body gets 0.
 __device__ __forceinline__ void body_vel(Sim& s, const float* v, int lane) {
-  if (lane < NB) {
-    unsigned ch[4];
-    for (int k = 0; k < 4; k++) ch[k] = s.chain[lane][k];
-    float w[3], u[3] = {v[0], v[1], v[2]};
-    for (int k = 0; k < 3; k++) w[k] = s.S[3][k] * v[3] + s.S[4][k] * v[4] + s.S[5][k] * v[5];
+  const int g = lane >> 4, c = lane & 15;
+  const bool comp = c < 6;
+  const int so = comp ? (c < 3 ? c : c + 1) : 0;  // the component's place in a row of S and bw: w 0..2, v 4..6
+  const int lo = g == 0 ? PATHS.lo[0] : g == 1 ? PATHS.lo[1] : g == 2 ? PATHS.lo[2] : PATHS.lo[3];
+  const int hi = g == 0 ? PATHS.hi[0] : g == 1 ? PATHS.hi[1] : g == 2 ? PATHS.hi[2] : PATHS.hi[3];
+  float* sink = &s.u.nt.h.psi[0][0] + (lane & 7);  // 8 * PATH_STEPS + 7 floats: inside psi
+  static_assert(8 * PATH_STEPS + 8 <= 16 * 8, "the sink inside psi");
+  const float rw = s.S[3][so] * v[3] + s.S[4][so] * v[4] + s.S[5][so] * v[5];
+  float T = c < 3 ? rw : v[comp ? c - 3 : 0];
+  (comp && g < 2 ? &s.u.nt.bw[1 - g][so] : sink)[0] = g == 0 ? T : 0.f;  // the root body; the world body 0
+  const float *Sa = &s.S[4 + lo][so], *Sb = &s.S[4 + hi][so], *va = v + 4 + lo, *vb = v + 4 + hi;
+  float* oa = comp ? &s.u.nt.bw[lo][so] : sink;
+  float* ob = comp ? &s.u.nt.bw[hi][so] : sink;
+  float* oc = comp && g >= 2 ? ob : sink;  // past the legs' 6 bodies only the arm groups' are real
 #pragma unroll
-    for (int t = NROOT; t < MAXCHAIN; t++) {
-      const unsigned b = (ch[t >> 2] >> (8 * (t & 3))) & 255u;
-      const int d = (int)min(b, (unsigned)NV);
-      const float vd = v[d];
-      for (int k = 0; k < 3; k++) { w[k] = fmaf(s.S[d][k], vd, w[k]); u[k] = fmaf(s.S[d][4 + k], vd, u[k]); }
-    }
-    const float z = lane > 0 ? 1.f : 0.f;
-    for (int k = 0; k < 3; k++) { s.u.nt.bw[lane][k] = z * w[k]; s.u.nt.bw[lane][4 + k] = z * u[k]; }
+  for (int i = 0; i < PATH_STEPS; i++) {
+    T = fmaf((i < 3 ? Sa : Sb)[8 * i], (i < 3 ? va : vb)[i], T);
+    (i < 3 ? oa : i < 6 ? ob : oc)[8 * i] = T;
   }
   wsync();
 }
@@ -1138,8 +1144,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (lane == 0) { s.fric = ifr; s.flags = 0; s.niter = 0; s.dcnt = 0; s.acost = 0; }
   s.dsub[lane] = lane < NV ? cTree.dofmask32[lane] : 0u;
   chain_table(s.chain, lane);
-  if (lane < 8) s.S[NV][lane] = 0.f;  // body_vel's zero padding row and entries
-  if (lane == 0) { s.qvel[NV] = 0.f; s.qacc[NV] = 0.f; s.p[NV] = 0.f; }
 #ifdef G1_PROFILE
   if (lane < NPHASE) s.prof_acc[lane] = 0;
   if (lane == 0) {

@@ -104,6 +104,34 @@ constexpr bool check_orders() {
 }
 static_assert(check_orders(), "dofs' subtrees as body-id runs; floor pairs first, sorted by body");
 
+// The tree as four root-to-leaf paths below the root body 1 (the two legs; the waist and then either arm), for the
+// kernels' path walks (body velocities, twists): group g's step i is body i < 3 ? lo + i : hi + i for i < len, and
+// each step's parent is the step before it (the first's the root). The two arm paths share the waist's 3 bodies.
+// Checked against the parent table: every hinge body on a path, and every step's dof b + 4 (also past a path's end,
+// where the leg groups' walks run on into a sink) a dof.
+struct PathGroups { int lo[4], hi[4], len[4]; };  // group g's step i: body i < 3 ? lo + i : hi + i, for i < len
+constexpr int PATH_STEPS = 10;
+constexpr PathGroups PATHS = {{2, 8, 14, 14}, {2, 8, 14, 21}, {6, 6, 10, 10}};
+constexpr int path_body(int g, int i) { return i < 3 ? PATHS.lo[g] + i : PATHS.hi[g] + i; }
+constexpr bool check_paths() {  // each a path from the root body 1, together every hinge body; every read in bounds
+  bool seen[NB] = {};
+  for (int g = 0; g < 4; g++) {
+    if (PATHS.len[g] != (g < 2 ? 6 : PATH_STEPS)) return false;  // the walks store steps 6.. of groups 2, 3 only
+    for (int i = 0; i < PATH_STEPS; i++) {
+      const int b = path_body(g, i);
+      if (b < 2 || b + 4 >= NV) return false;
+      if (i < PATHS.len[g]) {
+        if (BODY_PARENT[b] != (i == 0 ? 1 : path_body(g, i - 1))) return false;
+        seen[b] = true;
+      }
+    }
+  }
+  for (int b = 2; b < NB; b++)
+    if (!seen[b]) return false;
+  return true;
+}
+static_assert(check_paths(), "the G1's root-to-leaf paths: legs 2..7, 8..13; waist 14..16 then arms 17..23, 24..30");
+
 // geom type codes (mjtGeom): plane 0, sphere 2, capsule 3
 constexpr int GPLANE = 0, GSPHERE = 2, GCAPSULE = 3;
 
