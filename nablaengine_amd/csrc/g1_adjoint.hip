@@ -225,12 +225,13 @@ __device__ __forceinline__ void sphere_core_vjp(const float* p1, float r1, const
 // geoms' world position and rotation cotangents
 __device__ void contact_geom_vjp(const Adj& s, int pr, int slot, const float* fr, float db, const float* posb,
                                  const float* frb, int normal, float* x1b, float* t1b, float* x2b, float* t2b) {
-  const unsigned w = cPairW[pr];
+  const unsigned w = cPair[pr].w;
+  const PairSz psz = cPairSz[pr];
   const int g1 = w & 255u, g2 = (w >> 8) & 255u, cls = (w >> 21) & 7u;
   float p1[3], q1[4], p2[3], q2[4];
   for (int k = 0; k < 3; k++) { p1[k] = s.gx[g1][k]; p2[k] = s.gx[g2][k]; }
   for (int k = 0; k < 4; k++) { q1[k] = s.gq[g1][k]; q2[k] = s.gq[g2][k]; }
-  const float r1 = cGsize[3 * g1], h1 = cGsize[3 * g1 + 1], r2 = cGsize[3 * g2], h2 = cGsize[3 * g2 + 1];
+  const float r1 = psz.r1, h1 = psz.hl1, r2 = psz.r2, h2 = psz.hl2;
   for (int k = 0; k < 3; k++) x1b[k] = t1b[k] = x2b[k] = t2b[k] = 0.f;
   if (cls == 0 || cls == 4) {  // the floor: n constant
     float n[3];
@@ -719,8 +720,9 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
   if (lane < ncon) {
     const unsigned zc = (s.czone[lane >> 3] >> (4 * (lane & 7))) & 15u;
     const int pr = min((int)(s.con[lane] & 511u), NPAIR - 1), slot = s.con[lane] >> 9;
-    const unsigned w = cPairW[pr];
-    const int b1 = cGbody[w & 255u], b2 = cGbody[(w >> 8) & 255u], dim = (w >> 16) & 15u;
+    const PairC pc = cPair[pr];
+    const unsigned w = pc.w;
+    const int b1 = pc.bodies & 255u, b2 = pc.bodies >> 8, dim = (w >> 16) & 15u;
     cb1 = b1;
     cb2 = b2;
     if (zc) {

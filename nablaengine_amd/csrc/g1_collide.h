@@ -72,11 +72,12 @@ __device__ __forceinline__ int broadphase(const float (*gx)[4], const float* fn,
 #pragma unroll
   for (int k = 0; k < (NPAIR + WL - 1) / WL; k++) {
     const int pr = lane + WL * k;
-    const unsigned w = cPairW[pr < NPAIR ? pr : NPAIR - 1];
+    const PairC pc = cPair[pr < NPAIR ? pr : NPAIR - 1];
+    const unsigned w = pc.w;
     const int g1 = w & 255u, g2 = (w >> 8) & 255u;
     const float dif[3] = {gx[g2][0] - gx[g1][0], gx[g2][1] - gx[g1][1], gx[g2][2] - gx[g1][2]};
     const unsigned cls = (w >> 21) & 7u;
-    const float r1 = cGrb[g1], r2 = cGrb[g2], rb = r1 + r2;
+    const float r2 = pc.rb2, rb = pc.rb;
     const bool plane = cls == 0u || cls == 4u;
     const bool keep = pr < NPAIR && (plane ? dot3(dif, fn) <= r2 * (1.f + 1e-5f) + 1e-6f
                                            : dot3(dif, dif) <= rb * rb * (1.f + 1e-5f) + 1e-12f);
@@ -90,17 +91,19 @@ __device__ __forceinline__ int broadphase(const float (*gx)[4], const float* fn,
 // narrowphase of pair pr (step.py:1042-1143 collide_pair), zero margin
 __device__ void collide_pair(const float (*gx)[4], const float (*gq)[4], int pr, Cand& o) {
   o.has[0] = o.has[1] = false;
-  const unsigned w = cPairW[pr];
+  const PairC pc = cPair[pr];
+  const PairSz psz = cPairSz[pr];
+  const unsigned w = pc.w;
   const int g1 = w & 255u, g2 = (w >> 8) & 255u, cls = (w >> 21) & 7u;
   float p1[3], q1[4], p2[3], q2[4];
   for (int k = 0; k < 3; k++) { p1[k] = gx[g1][k]; p2[k] = gx[g2][k]; }
   for (int k = 0; k < 4; k++) { q1[k] = gq[g1][k]; q2[k] = gq[g2][k]; }
-  const float r1 = cGsize[3 * g1], hl1 = cGsize[3 * g1 + 1], r2 = cGsize[3 * g2], hl2 = cGsize[3 * g2 + 1];
+  const float r1 = psz.r1, hl1 = psz.hl1, r2 = psz.r2, hl2 = psz.hl2;
   float pos[3], fr[9], n[3], dist;
   if (cls == 0 || cls == 4) {  // plane (the floor) against a sphere or a capsule
     zaxis(q1, n);
     float dif[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]};
-    if (dot3(dif, n) > cGrb[g2]) return;
+    if (dot3(dif, n) > pc.rb2) return;
     if (cls == 0) {
       dist = plane_point(p1, n, p2, r2, pos);
       make_frame(n, fr);
@@ -135,7 +138,7 @@ __device__ void collide_pair(const float (*gx)[4], const float (*gq)[4], int pr,
     return;
   }
   {
-    float dif[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]}, rb = cGrb[g1] + cGrb[g2];
+    float dif[3] = {p2[0] - p1[0], p2[1] - p1[1], p2[2] - p1[2]}, rb = pc.rb;
     if (dot3(dif, dif) > rb * rb) return;
   }
   if (cls == 1) {  // sphere-sphere

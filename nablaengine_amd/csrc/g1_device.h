@@ -40,13 +40,36 @@ __constant__ inline Arr<float, NV> cKp = to_float(DOF_KP);
 __constant__ inline Arr<float, NV> cKv = to_float(DOF_KV);
 __constant__ inline Arr<float, NV> cFrclim = to_float(DOF_FRCLIM);
 __constant__ inline Arr<float, NV * 2> cRange = to_float(DOF_RANGE);
-__constant__ inline Arr<float, NGEOM * 3> cGsize = to_float(GEOM_SIZE);
 __constant__ inline Arr<float, NGEOM * 3> cGpos = to_float(GEOM_POS);
 __constant__ inline Arr<float, NGEOM * 4> cGquat = to_float(GEOM_QUAT);
-__constant__ inline Arr<float, NGEOM> cGrb = to_float(GEOM_RBOUND);
 __constant__ inline Arr<int, NGEOM> cGbody = to_int(GEOM_BODY);
-__constant__ inline Arr<unsigned, NPAIR> cPairW = PAIRW;
 __constant__ inline Arr<float, NPAIR> cPairMu = to_float(PAIR_MU);
+// Per pair, the words its tests read together, each table one 16-byte load indexed by the pair (where the pair word
+// and then loads indexed by its geoms were two dependent round trips): the pair word (PAIRW), the two geoms' bodies
+// (b1 | b2 << 8), the bounding radii's sum (the floats added in float) and the second geom's bounding radius; the
+// two geoms' radius and half-length (GEOM_SIZE 0 and 1).
+struct __align__(16) PairC { unsigned w, bodies; float rb, rb2; };
+struct __align__(16) PairSz { float r1, hl1, r2, hl2; };
+constexpr Arr<PairC, NPAIR> make_pairc() {
+  Arr<PairC, NPAIR> r{};
+  for (int p = 0; p < NPAIR; p++) {
+    const int g1 = PAIR_G1[p], g2 = PAIR_G2[p];
+    const float a = (float)GEOM_RBOUND[g1], b = (float)GEOM_RBOUND[g2];
+    r.v[p] = PairC{PAIRW[p], (unsigned)GEOM_BODY[g1] | (unsigned)GEOM_BODY[g2] << 8, a + b, b};
+  }
+  return r;
+}
+constexpr Arr<PairSz, NPAIR> make_pairsz() {
+  Arr<PairSz, NPAIR> r{};
+  for (int p = 0; p < NPAIR; p++) {
+    const int g1 = PAIR_G1[p], g2 = PAIR_G2[p];
+    r.v[p] = PairSz{(float)GEOM_SIZE[3 * g1], (float)GEOM_SIZE[3 * g1 + 1], (float)GEOM_SIZE[3 * g2],
+                    (float)GEOM_SIZE[3 * g2 + 1]};
+  }
+  return r;
+}
+__constant__ inline Arr<PairC, NPAIR> cPair = make_pairc();
+__constant__ inline Arr<PairSz, NPAIR> cPairSz = make_pairsz();
 __constant__ inline Tree cTree = TREE;
 // each body's chain (the dofs moving it, ascending) packed one byte a dof into 4 words, 255 past its end (a 16-byte row
 // per body: one load each)
@@ -212,15 +235,19 @@ __device__ __forceinline__ float lane_of(float x, int src) {
 __device__ __forceinline__ int wsumi(int v) {  // small counts: exact in float
   return (int)wsum((float)v);
 }
-// exclusive prefix sum of small non-negative ints over the wave (Hillis-Steele on shuffles)
-__device__ __forceinline__ int wscan_excl(int v, int lane) {
-  int x = v;
+// exclusive prefix sum and wave total of a count 0 <= v < 2^NBITS, bit by bit from ballots (each bit's lanes below
+// this one by v_mbcnt, the total by a scalar popcount): no cross-lane data movement, exact
+template <int NBITS>
+__device__ __forceinline__ int wscan_bits(int v, int lane, int* total) {
+  int r = 0, t = 0;
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
+  for (int b = 0; b < NBITS; b++) {
+    const unsigned long long m = ballot((v >> b) & 1);
+    r += prefix_count(m, lane) << b;
+    t += __popcll(m) << b;
   }
-  return x - v;
+  *total = t;
+  return r;
 }
 // The LDS barrier of a workgroup of one wave (every kernel that calls it has 64 threads): a wave's LDS instructions
 // execute in issue order, so a lane's LDS write is seen by every later LDS read of the wave with no hardware barrier

@@ -318,7 +318,8 @@ __device__ void collision(Sim& s, int lane) {
       collide_pair(s.u.col.gx, s.u.col.gq, pr, o);
     }
     const int n = (int)o.has[0] + (int)o.has[1];
-    const int off = total + wscan_excl(n, lane);
+    int tn;
+    const int off = total + wscan_bits<2>(n, lane, &tn);
 #pragma unroll
     for (int e = 0; e < 2; e++) {
       const int idx = off + (e == 1 ? (int)o.has[0] : 0);
@@ -331,7 +332,7 @@ __device__ void collision(Sim& s, int lane) {
         st[14] = __int_as_float(o.slot[e]);
       }
     }
-    total += wsumi(n);
+    total += tn;
   }
   if (lane == 0) {
     s.ncon_raw = total;
@@ -955,9 +956,10 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
     for (int k = 0; k < 3; k++) R.r[k] = st[1 + k] - s.O[k];
     for (int k = 0; k < 9; k++) R.fr[k] = st[4 + k];
     pair = __float_as_int(st[13]);
-    const unsigned w = cPairW[pair];
-    R.b1 = cGbody[w & 255u];
-    R.b2 = cGbody[(w >> 8) & 255u];
+    const PairC pc = cPair[pair];
+    const unsigned w = pc.w;
+    R.b1 = pc.bodies & 255u;
+    R.b2 = pc.bodies >> 8;
     R.dim = (w >> 16) & 15u;
     R.mu = ((w >> 20) & 1u) ? s.fric : cPairMu[pair];
   }
@@ -973,9 +975,10 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   const unsigned long long lm = ballot(R.lsg != 0.f);
   const int nlim = __popcll(lm);
   const int nrf = con ? (R.dim == 3 ? 4 : 1) : 0;
-  const int r0 = nlim + wscan_excl(nrf, lane);
+  int trf;
+  const int r0 = nlim + wscan_bits<3>(nrf, lane, &trf);
   R.nr = con ? max(0, min(nrf, NEFC - r0)) : 0;
-  const int need = nlim + wsumi(nrf);
+  const int need = nlim + trf;
   if (lane == 0) {
     s.nlim = nlim;
     s.nefc = need < NEFC ? need : NEFC;
@@ -1015,8 +1018,8 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   if (rec) {
     float nu = 1e30f;
     if (con && R.b1 != 0) {
-      const unsigned pw = cPairW[pair];
-      nu = dist + cGsize[3 * (pw & 255u)] + cGsize[3 * ((pw >> 8) & 255u)];
+      const PairSz psz = cPairSz[pair];
+      nu = dist + psz.r1 + psz.r2;
     }
     sing = ballot(nu < SINGULAR_NU) != 0ull;
   }
@@ -1045,7 +1048,7 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
     // between two robot bodies (4 each: the per-body wrench sums, the two-body contact VJPs), and the primitive classes
     // present (8 each: a lane's class branches run for the whole wave), in units of 4 (measured on config-1 worlds:
     // the adjoint's launch in this order ends 3.4% earlier than ordered by the records' constraint rows)
-    const unsigned pwc = cPairW[con ? pair : 0];
+    const unsigned pwc = cPair[con ? pair : 0].w;
     const unsigned cbod = wor(con ? (1u << R.b1) | (1u << R.b2) : 0u) & ~1u;
     const unsigned ccls = wor(con ? 1u << ((pwc >> 21) & 7u) : 0u);
     const int cself = wsumi(con && R.b1 != 0 ? 1 : 0);

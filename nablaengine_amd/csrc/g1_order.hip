@@ -97,7 +97,7 @@ __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict
       const int pr = cand[c0 + lane];
       Cand o;
       collide_pair(gx, gq, pr, o);
-      const unsigned pw = cPairW[pr];
+      const unsigned pw = cPair[pr].w;
       const unsigned cls = (pw >> 21) & 7u;
       const int n = (int)o.has[0] + (int)o.has[1];
       const int rows = ((pw >> 16) & 15u) == 3u ? 4 : 1;
