@@ -495,7 +495,7 @@ __device__ __forceinline__ void adj_poses(Adj& s, int lane) {
     for (int k = 0; k < 3; k++) { s.S[lane][k] = w[k]; s.S[lane][4 + k] = v[k]; }
   }
   if (lane < NGEOM) {  // geom poses
-    const int b = cGbody[lane];
+    const int b = geom_body(lane);
     float t[3], qb[4] = {s.Q[b][0], s.Q[b][1], s.Q[b][2], s.Q[b][3]};
     const float gp[3] = {cGpos[3 * lane], cGpos[3 * lane + 1], cGpos[3 * lane + 2]};
     const float gq[4] = {cGquat[4 * lane], cGquat[4 * lane + 1], cGquat[4 * lane + 2], cGquat[4 * lane + 3]};
@@ -721,6 +721,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     const unsigned zc = (s.czone[lane >> 3] >> (4 * (lane & 7))) & 15u;
     const int pr = min((int)(s.con[lane] & 511u), NPAIR - 1), slot = s.con[lane] >> 9;
     const PairC pc = cPair[pr];
+    const PairRow prow = cPairRow[pr];
     const unsigned w = pc.w;
     const int b1 = pc.bodies & 255u, b2 = pc.bodies >> 8, dim = (w >> 16) & 15u;
     cb1 = b1;
@@ -736,11 +737,11 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
         float pos[3], fr[9];
         for (int k = 0; k < 3; k++) pos[k] = which ? cd.pos[1][k] : cd.pos[0][k];
         for (int k = 0; k < 9; k++) fr[k] = which ? cd.fr[1][k] : cd.fr[0][k];
-        const float mu = ((w >> 20) & 1u) ? s.fric : cPairMu[pr];
+        const float mu = ((w >> 20) & 1u) ? s.fric : prow.mu;
         float k, b, imp, dimp;
         kb_consts(caPSolref.v, caPSolimp.v, &k, &b);
         imp_d(caPSolimp.v, dist, &imp, &dimp);
-        float iw = cBinvw[b1] + cBinvw[b2];
+        float iw = prow.iw;
         if (dim == 3) iw = (mu * mu * iw + iw) * 2.f * mu * mu / kImpratio;
         const float D = 1.f / fmaxf(iw * (1.f - imp) / imp, 1e-15f), dD = dimp / (iw * (1.f - imp) * (1.f - imp));
         float rr[3];
@@ -888,7 +889,7 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
         A1o.v[k] += s.astar[k]; A2o.v[k] = s.at[k];
       }
     } else if (j >= 6) {
-      const int p = cParent[bj];
+      const int p = body_parent(bj);
       Vo = ld_sv6(s.tw[p][TW_V]); Lo = ld_sv6(s.tw[p][TW_L]); Yo = ld_sv6(s.tw[p][TW_Y]);
       Awo = ld_sv6(s.tw[p][TW_AW]); A1o = ld_sv6(s.tw[p][TW_A1]); A2o = ld_sv6(s.tw[p][TW_A2]);
     }

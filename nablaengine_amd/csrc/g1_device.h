@@ -30,7 +30,6 @@ __constant__ inline Arr<float, NB * 3> cIpos = to_float(BODY_IPOS);
 __constant__ inline Arr<float, NB * 4> cIquat = to_float(BODY_IQUAT);
 __constant__ inline Arr<float, NB> cMass = to_float(BODY_MASS);
 __constant__ inline Arr<float, NB * 3> cInert = to_float(BODY_INERTIA);
-__constant__ inline Arr<float, NB> cBinvw = to_float(BODY_INVWEIGHT0);
 __constant__ inline Arr<int, NB> cParent = to_int(BODY_PARENT);
 __constant__ inline Arr<int, NB> cDepth = to_int(BODY_DEPTH);
 __constant__ inline Arr<int, NB> cQadr = to_int(BODY_QADR);
@@ -43,7 +42,6 @@ __constant__ inline Arr<float, NV * 2> cRange = to_float(DOF_RANGE);
 __constant__ inline Arr<float, NGEOM * 3> cGpos = to_float(GEOM_POS);
 __constant__ inline Arr<float, NGEOM * 4> cGquat = to_float(GEOM_QUAT);
 __constant__ inline Arr<int, NGEOM> cGbody = to_int(GEOM_BODY);
-__constant__ inline Arr<float, NPAIR> cPairMu = to_float(PAIR_MU);
 // Per pair, the words its tests read together, each table one 16-byte load indexed by the pair (where the pair word
 // and then loads indexed by its geoms were two dependent round trips): the pair word (PAIRW), the two geoms' bodies
 // (b1 | b2 << 8), the bounding radii's sum (the floats added in float) and the second geom's bounding radius; the
@@ -68,8 +66,54 @@ constexpr Arr<PairSz, NPAIR> make_pairsz() {
   }
   return r;
 }
+// the rows' per-pair constants: the two bodies' inverse weights summed (in float) and the friction coefficient
+struct __align__(8) PairRow { float iw, mu; };
+constexpr Arr<PairRow, NPAIR> make_pairrow() {
+  Arr<PairRow, NPAIR> r{};
+  for (int p = 0; p < NPAIR; p++) {
+    const float a = (float)BODY_INVWEIGHT0[GEOM_BODY[PAIR_G1[p]]], b = (float)BODY_INVWEIGHT0[GEOM_BODY[PAIR_G2[p]]];
+    r.v[p] = PairRow{a + b, (float)PAIR_MU[p]};
+  }
+  return r;
+}
 __constant__ inline Arr<PairC, NPAIR> cPair = make_pairc();
 __constant__ inline Arr<PairSz, NPAIR> cPairSz = make_pairsz();
+__constant__ inline Arr<PairRow, NPAIR> cPairRow = make_pairrow();
+// A small table of 5-bit entries as three 64-bit compile-time words (12 entries a word): a lane's entry by selects
+// and a shift, with no memory access (a lane-indexed table in constant memory is a global load, and an LDS address
+// taken from it waits for that round trip).
+struct Packed5 { uint64_t w[3]; };
+template <int N>
+constexpr Packed5 pack5(const int (&a)[N]) {
+  static_assert(N <= 36, "three words of 12 entries");
+  Packed5 p{};
+  for (int i = 0; i < N; i++) p.w[i / 12] |= (uint64_t)(a[i] & 31) << (5 * (i % 12));
+  return p;
+}
+template <int N>
+constexpr bool fits5(const int (&a)[N]) {
+  for (int i = 0; i < N; i++)
+    if (a[i] < 0 || a[i] > 31) return false;
+  return true;
+}
+static_assert(fits5(GEOM_BODY) && fits5(BODY_PARENT), "5-bit entries");
+constexpr Packed5 GEOM_BODY5 = pack5(GEOM_BODY), BODY_PARENT5 = pack5(BODY_PARENT);
+template <const Packed5& P>
+__device__ __forceinline__ int unpack5(int i) {
+  constexpr uint64_t w0 = P.w[0], w1 = P.w[1], w2 = P.w[2];
+  const uint64_t x = i < 12 ? w0 : (i < 24 ? w1 : w2);
+  const int sh = 5 * (i < 12 ? i : (i < 24 ? i - 12 : i - 24));
+  return (int)((x >> sh) & 31u);
+}
+__device__ __forceinline__ int geom_body(int g) { return unpack5<GEOM_BODY5>(g); }
+__device__ __forceinline__ int body_parent(int b) { return unpack5<BODY_PARENT5>(b); }
+// a hinge body's joint angle is qpos[b + 5] (the root's 7 coordinates first, one per hinge body in body order)
+constexpr bool check_qadr() {
+  for (int b = 2; b < NB; b++)
+    if (BODY_QADR[b] != b + 5) return false;
+  return true;
+}
+static_assert(check_qadr(), "one hinge per body, in body order");
 __constant__ inline Tree cTree = TREE;
 // each body's chain (the dofs moving it, ascending) packed one byte a dof into 4 words, 255 past its end (a 16-byte row
 // per body: one load each)

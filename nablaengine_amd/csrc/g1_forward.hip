@@ -100,7 +100,7 @@ __device__ void smooth(Sim& s, int lane) {
   // parent's frame p_b, and the hinge axis in the parent's frame a_l = quat a (the hinge rotation keeps its own axis)
   if (lane >= 2 && lane < NB) {
     float sn, cs;
-    sincosf(0.5f * s.qpos[cQadr[lane]], &sn, &cs);
+    sincosf(0.5f * s.qpos[lane + 5], &sn, &cs);
     const float qb[4] = {cQuat[4 * lane], cQuat[4 * lane + 1], cQuat[4 * lane + 2], cQuat[4 * lane + 3]};
     const float ax[3] = {cAxis[3 * lane], cAxis[3 * lane + 1], cAxis[3 * lane + 2]};
     const float ha[4] = {cs, sn * ax[0], sn * ax[1], sn * ax[2]};
@@ -949,7 +949,7 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   R.nr = 0; R.b1 = 0; R.b2 = 0; R.dim = 1; R.mu = 0.f; R.D = 0.f;
   for (int k = 0; k < 3; k++) R.r[k] = 0.f;
   for (int k = 0; k < 9; k++) R.fr[k] = 0.f;
-  float dist = 0.f;
+  float dist = 0.f, piw = 0.f;
   if (con) {
     const float* st = s.u.col.stage[lane];
     dist = st[0];
@@ -957,11 +957,13 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
     for (int k = 0; k < 9; k++) R.fr[k] = st[4 + k];
     pair = __float_as_int(st[13]);
     const PairC pc = cPair[pair];
+    const PairRow prow = cPairRow[pair];
     const unsigned w = pc.w;
     R.b1 = pc.bodies & 255u;
     R.b2 = pc.bodies >> 8;
     R.dim = (w >> 16) & 15u;
-    R.mu = ((w >> 20) & 1u) ? s.fric : cPairMu[pair];
+    R.mu = ((w >> 20) & 1u) ? s.fric : prow.mu;
+    piw = prow.iw;
   }
   floor_run(s, R, lane);
   wsync();
@@ -998,7 +1000,7 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
   if (con) {
     float k, b, imp;
     kbimp(cPSolref.v, cPSolimp.v, dist, &k, &b, &imp);
-    float iw = cBinvw[R.b1] + cBinvw[R.b2];
+    float iw = piw;
     if (R.dim == 3) iw = (R.mu * R.mu * iw + iw) * 2.f * R.mu * R.mu / kImpratio;
     R.D = 1.f / fmaxf(iw * (1.f - imp) / imp, 1e-15f);
 #pragma unroll

@@ -39,7 +39,7 @@ __global__ __launch_bounds__(64) void k_cost_fwd(int nw, const float* __restrict
   wsync();
   if (lane >= 2 && lane < NB) {  // one hinge rotation per body, then the chain walks use products only
     float sn, cs;
-    sincosf(0.5f * q[cQadr[lane]], &sn, &cs);
+    sincosf(0.5f * q[lane + 5], &sn, &cs);
     const float qb[4] = {cQuat[4 * lane], cQuat[4 * lane + 1], cQuat[4 * lane + 2], cQuat[4 * lane + 3]};
     const float ha[4] = {cs, sn * cAxis[3 * lane], sn * cAxis[3 * lane + 1], sn * cAxis[3 * lane + 2]};
     qmul(qb, ha, hl[lane]);
