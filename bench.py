@@ -408,8 +408,8 @@ def main():
                              "hbm": {"achieved": adj_bytes * B / (ams * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
                                      "unit": "GB/s", "frac": adj_bytes * B / (ams * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                      "bytes_per_world_step": adj_bytes},
-                             "note": "k_adjoint, the VJP's kernel (FP32 vector work; fp32 MFMA for the subtree sums "
-                                     "only): achieved = closed-form algorithmic flops of the VJP (" f"{fla:.3g}"
+                             "note": "k_adjoint, the VJP's kernel (FP32 vector work, no MFMA): achieved = closed-form "
+                                     "algorithmic flops of the VJP (" f"{fla:.3g}"
                                      " per world-step, the float64 restatement's adjoint count on "
                                      f"{len(sub['qpos'])} of the worlds, default variant) x worlds / k_adjoint's mean "
                                      "duration (HIP events around back-to-back launches over 8 dispatch orders, its "
