@@ -77,7 +77,7 @@ __device__ __forceinline__ void st_sv6(float* p, const Sv& x) {
 struct __align__(16) Adj {
   float qpos[40], qvel[36], astar[36], aadv[36], at[36];
   float qb[36], vb[36], vt[36], qn[36], y[36], lam[36], ub[32], ctrl[32], com[4];
-  float S[NV + 1][8];                 // row NV is zero, as the dof vectors' entry NV (the chain padding's target)
+  float S[NV + 1][8];                 // dof motion subspaces about O (row NV unused); qvel[NV] = 0 pads the chains
   float Q[NB][4], X[NB][4];          // the body frames, copied from the record (X's fourth words 0)
   unsigned short pslot[POSE_WORDS];  // L_Q's packed positions that carry the frames (cPoseSlots, loaded at start)
   unsigned chain[NB][MAXCHAIN / 4];  // the dofs moving each body, ascending, one byte each; 255 past the chain
@@ -1041,8 +1041,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #endif
   chain_table(s.chain, lane);
   for (int q = lane; q < POSE_WORDS; q += WL) s.pslot[q] = (unsigned short)cPoseSlots.pos[q];
-  if (lane < 8) s.S[NV][lane] = 0.f;  // the twists' zero padding row and entries (nothing else writes them)
-  if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
+  if (lane == 0) s.qvel[NV] = 0.f;  // the chain padding's entry (adj_twists' velocity-product walk)
   // the output cotangents in the tangent space at the output state
   if (lane < NV) s.vb[lane] = igv;
   if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = igq;
@@ -1102,8 +1101,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #endif
   chain_table(s.chain, lane);
   for (int q = lane; q < POSE_WORDS; q += WL) s.pslot[q] = (unsigned short)cPoseSlots.pos[q];
-  if (lane < 8) s.S[NV][lane] = 0.f;  // the twists' zero padding row and entries (nothing else writes them)
-  if (lane == 0) { s.qvel[NV] = 0.f; s.lam[NV] = 0.f; s.y[NV] = 0.f; s.astar[NV] = 0.f; s.at[NV] = 0.f; }
+  if (lane == 0) s.qvel[NV] = 0.f;  // the chain padding's entry (adj_twists' velocity-product walk)
   wsync();
 #pragma unroll 1
   for (int k = nsub - 1; k >= 0; k--) {

@@ -156,8 +156,11 @@ __device__ __forceinline__ int prefix_count(unsigned long long m, int lane) {  /
   return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
 }
 // Sum over the wave's 64 lanes by DPP: an inclusive scan within each row of 16 lanes (row_shr 1, 2, 4, 8), then
-// row_bcast 15 / 31 carry the row totals up, so lane 63 holds the total; v_readlane broadcasts it as a wave-uniform
-// scalar. A fixed order on every call (bitwise deterministic); lanes without a DPP source add +0.
+// row_bcast 15 / 31 carry the row totals up, so lane 63 holds the total (T3 + T2) + (T1 + T0); v_readlane broadcasts
+// it as a wave-uniform scalar. A fixed order on every call (bitwise deterministic); lanes without a DPP source add +0.
+// The two broadcasts run on every row (row mask 0xf): only lanes 31 and 63 are read after them, and what the other
+// rows add does not reach those lanes, while a row mask other than 0xf keeps each step from folding into one
+// v_add_f32_dpp (a zero move, a v_mov_b32_dpp and an add instead). The prefix scans (wscan_nw) need the masks.
 #define G1_DPP(x, ctrl, rmask) \
   __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), (ctrl), (rmask), 0xf, false))
 // A reduction's input as an opaque value: its first step then stays one v_add_f32_dpp, where otherwise a product
@@ -172,8 +175,8 @@ __device__ __forceinline__ float wsum(float v) {
   v += G1_DPP(v, 0x112, 0xf);  // row_shr:2
   v += G1_DPP(v, 0x114, 0xf);  // row_shr:4
   v += G1_DPP(v, 0x118, 0xf);  // row_shr:8
-  v += G1_DPP(v, 0x142, 0xa);  // row_bcast:15 into rows 1, 3
-  v += G1_DPP(v, 0x143, 0xc);  // row_bcast:31 into rows 2, 3
+  v += G1_DPP(v, 0x142, 0xf);  // row_bcast:15: lane 31 = T1 + T0, lane 63 = T3 + T2
+  v += G1_DPP(v, 0x143, 0xf);  // row_bcast:31: lane 63 += lane 31
   return rdl(v, 63);
 }
 __device__ __forceinline__ float2 wsum2(float a, float b) {
@@ -183,8 +186,8 @@ __device__ __forceinline__ float2 wsum2(float a, float b) {
   a += G1_DPP(a, 0x112, 0xf); b += G1_DPP(b, 0x112, 0xf);
   a += G1_DPP(a, 0x114, 0xf); b += G1_DPP(b, 0x114, 0xf);
   a += G1_DPP(a, 0x118, 0xf); b += G1_DPP(b, 0x118, 0xf);
-  a += G1_DPP(a, 0x142, 0xa); b += G1_DPP(b, 0x142, 0xa);
-  a += G1_DPP(a, 0x143, 0xc); b += G1_DPP(b, 0x143, 0xc);
+  a += G1_DPP(a, 0x142, 0xf); b += G1_DPP(b, 0x142, 0xf);
+  a += G1_DPP(a, 0x143, 0xf); b += G1_DPP(b, 0x143, 0xf);
   return make_float2(rdl(a, 63), rdl(b, 63));
 }
 // the wave totals of n values at once (a masked sum passes 0 on the lanes outside the set): wsum's DPP steps with
@@ -202,9 +205,9 @@ __device__ __forceinline__ void wsum_n(float* x) {
 #pragma unroll
   for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x118, 0xf);
 #pragma unroll
-  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x142, 0xa);
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x142, 0xf);
 #pragma unroll
-  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x143, 0xc);
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x143, 0xf);
 #pragma unroll
   for (int e = 0; e < N; e++) x[e] = rdl(x[e], 63);
 }
@@ -215,8 +218,8 @@ __device__ __forceinline__ unsigned wor(unsigned v) {
   v |= G1_DPPI(v, 0x112, 0xf);
   v |= G1_DPPI(v, 0x114, 0xf);
   v |= G1_DPPI(v, 0x118, 0xf);
-  v |= G1_DPPI(v, 0x142, 0xa);
-  v |= G1_DPPI(v, 0x143, 0xc);
+  v |= G1_DPPI(v, 0x142, 0xf);
+  v |= G1_DPPI(v, 0x143, 0xf);
 #undef G1_DPPI
   return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
 }
@@ -240,14 +243,14 @@ __device__ __forceinline__ void wsum_nw(float* x, int width) {
     return;
   }
 #pragma unroll
-  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x142, 0xa);
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x142, 0xf);
   if (width <= 32) {
 #pragma unroll
     for (int e = 0; e < N; e++) x[e] = rdl(x[e], 31);
     return;
   }
 #pragma unroll
-  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x143, 0xc);
+  for (int e = 0; e < N; e++) x[e] += G1_DPP(x[e], 0x143, 0xf);
 #pragma unroll
   for (int e = 0; e < N; e++) x[e] = rdl(x[e], 63);
 }
