@@ -160,7 +160,8 @@ __device__ __forceinline__ int prefix_count(unsigned long long m, int lane) {  /
 // it as a wave-uniform scalar. A fixed order on every call (bitwise deterministic); lanes without a DPP source add +0.
 // The two broadcasts run on every row (row mask 0xf): only lanes 31 and 63 are read after them, and what the other
 // rows add does not reach those lanes, while a row mask other than 0xf keeps each step from folding into one
-// v_add_f32_dpp (a zero move, a v_mov_b32_dpp and an add instead). The prefix scans (wscan_nw) need the masks.
+// v_add_f32_dpp (a zero move, a v_mov_b32_dpp and an add instead). The prefix scans (wscan_nw) need the masks: with
+// row 0 enabled, row_bcast 15 changes row 0 too (measured: the scan's first lanes went wrong).
 #define G1_DPP(x, ctrl, rmask) \
   __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), (ctrl), (rmask), 0xf, false))
 // A reduction's input as an opaque value: its first step then stays one v_add_f32_dpp, where otherwise a product
