@@ -511,14 +511,15 @@ __device__ float newton_grad(Sim& s, const Rows& R, int lane, bool con) {
     for (int e = 0; e < 6; e++) x[e] = run_sum(x[e], R);
     tau = w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
   }
-  // contacts between two robot bodies: per distinct body (body 2 +, body 1 -)
+  // contacts between two robot bodies, one at a time: the contact's (T, F) broadcast to every lane, each dof adding
+  // it with the sign of the body it moves (body 2 +, body 1 -; neither or both 0)
   const bool selfc = act && R.b1 != 0;
-  for (unsigned m = ballot(selfc) ? wor(selfc ? (1u << R.b1) | (1u << R.b2) : 0u) : 0u; m; m &= m - 1u) {
-    const int B = __builtin_ctz(m);
-    const float sd = (selfc && R.b2 == B) ? 1.f : ((selfc && R.b1 == B) ? -1.f : 0.f);
-    float x[6] = {sd * T[0], sd * T[1], sd * T[2], sd * F[0], sd * F[1], sd * F[2]};
-    wsum_nw<6>(x, s.ncon);  // contact lanes only
-    if ((dm >> B) & 1u) tau += w[0] * x[0] + w[1] * x[1] + w[2] * x[2] + v[0] * x[3] + v[1] * x[4] + v[2] * x[5];
+  for (unsigned long long m = ballot(selfc); m; m &= m - 1ull) {
+    const int c = __builtin_ctzll(m);
+    const int b1 = rdli(R.b1, c), b2 = rdli(R.b2, c);
+    const float sg = (float)((int)((dm >> b2) & 1u) - (int)((dm >> b1) & 1u));
+    tau += sg * (w[0] * rdl(T[0], c) + w[1] * rdl(T[1], c) + w[2] * rdl(T[2], c) + v[0] * rdl(F[0], c)
+                 + v[1] * rdl(F[1], c) + v[2] * rdl(F[2], c));
   }
   float g = 0.f;
   if (lane < NV) {
