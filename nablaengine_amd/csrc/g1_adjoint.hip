@@ -807,23 +807,25 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
     }
   }
   APROF(AP_CONTACT);
-  // per body: the contacts' wrenches and row sums, summed over the contact lanes once per distinct contact body
-  // (masked wave sums, a fixed order); body lane B keeps its totals
+  // per body: the contacts' wrenches and row sums (body 2 +, body 1 -); body lane B keeps its totals. The floor
+  // contacts (body 1 the world) summed over the contact lanes once per distinct body they touch (masked wave sums,
+  // a fixed order); a contact between two robot bodies taken one at a time, its values broadcast to every lane and
+  // added by the two body lanes (a wave sum per body it touches cost 24 sums of up to 6 steps each)
   Sv EG = sv0(), OL = sv0(), OA = sv0(), OV = sv0();
-  for (unsigned m = wor(cact ? (1u << cb1) | (1u << cb2) : 0u) & ~1u; m; m &= m - 1u) {
+  const bool cself = cact && cb1 != 0;
+  for (unsigned m = wor(cact && !cself ? 1u << cb2 : 0u) & ~1u; m; m &= m - 1u) {
     const int B = __builtin_ctz(m);
-    const bool on2 = cact && cb2 == B, on1 = cact && cb1 == B;
-    const float sd = on2 ? 1.f : (on1 ? -1.f : 0.f);
+    const bool on = cact && !cself && cb2 == B;
     float x[24];
     for (int k = 0; k < 3; k++) {
-      x[k] = on2 ? cW2.w[k] : (on1 ? cW1.w[k] : 0.f);
-      x[3 + k] = on2 ? cW2.v[k] : (on1 ? cW1.v[k] : 0.f);
-      x[6 + k] = sd * cOmL.w[k];
-      x[9 + k] = sd * cOmL.v[k];
-      x[12 + k] = sd * cOmA.w[k];
-      x[15 + k] = sd * cOmA.v[k];
-      x[18 + k] = sd * cbb * cOmA.w[k];
-      x[21 + k] = sd * cbb * cOmA.v[k];
+      x[k] = on ? cW2.w[k] : 0.f;
+      x[3 + k] = on ? cW2.v[k] : 0.f;
+      x[6 + k] = on ? cOmL.w[k] : 0.f;
+      x[9 + k] = on ? cOmL.v[k] : 0.f;
+      x[12 + k] = on ? cOmA.w[k] : 0.f;
+      x[15 + k] = on ? cOmA.v[k] : 0.f;
+      x[18 + k] = on ? cbb * cOmA.w[k] : 0.f;
+      x[21 + k] = on ? cbb * cOmA.v[k] : 0.f;
     }
     wsum_nw<24>(x, ncon);  // contact lanes only
     if (lane == B)
@@ -831,6 +833,23 @@ __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int
         EG.w[k] = x[k]; EG.v[k] = x[3 + k]; OL.w[k] = x[6 + k]; OL.v[k] = x[9 + k];
         OA.w[k] = x[12 + k]; OA.v[k] = x[15 + k]; OV.w[k] = x[18 + k]; OV.v[k] = x[21 + k];
       }
+  }
+  for (unsigned long long m = ballot(cself); m; m &= m - 1ull) {
+    const int c = __builtin_ctzll(m);
+    const int b1 = rdli(cb1, c), b2 = rdli(cb2, c);
+    const float s2 = lane == b2 ? 1.f : 0.f, s1 = lane == b1 ? 1.f : 0.f, sd = s2 - s1;
+    const float bb = rdl(cbb, c);
+    for (int k = 0; k < 3; k++) {
+      EG.w[k] += s2 * rdl(cW2.w[k], c) + s1 * rdl(cW1.w[k], c);
+      EG.v[k] += s2 * rdl(cW2.v[k], c) + s1 * rdl(cW1.v[k], c);
+      OL.w[k] += sd * rdl(cOmL.w[k], c);
+      OL.v[k] += sd * rdl(cOmL.v[k], c);
+      const float aw = rdl(cOmA.w[k], c), av = rdl(cOmA.v[k], c);
+      OA.w[k] += sd * aw;
+      OA.v[k] += sd * av;
+      OV.w[k] += sd * (bb * aw);
+      OV.v[k] += sd * (bb * av);
+    }
   }
   APROF(AP_BODYSUM);
   if (lane >= 1 && lane < NB) {
