@@ -567,6 +567,32 @@ __device__ __forceinline__ void adj_solves(Adj& s, int lane, bool clear) {
   wsync();
 }
 
+// A cotangent set's values between its passes in k_adjoint_sets: the integrator's results, the running control
+// cotangent and the solves' results (LDS of its own, beside the Adj of the world)
+struct __align__(16) SetStage { float vt[36], qn[36], y[36], lam[36], ub[32]; };
+constexpr int SET_CHUNK = 2;  // cotangent sets whose solves run together (two right-hand sides a pass)
+
+// adj_solves for the staged sets st[0 .. nc) at once (nc <= 2): the same expressions for each set, the pair of
+// right-hand sides through ltl_solve2, so each set's y and lambda are bitwise adj_solves' for it
+__device__ __forceinline__ void adj_solves_sets(Adj& s, SetStage* st, int nc, int lane, bool clear) {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the factors' copies have landed in LDS
+  wsync();
+  if (clear) {
+    clear_pose_slots(s, lane);
+    wsync();
+  }
+  const float aab0 = lane < NV ? kH * st[0].vt[lane] : 0.f, aab1 = lane < NV && nc > 1 ? kH * st[1].vt[lane] : 0.f;
+  float y0, y1;
+  ltl_solve2(s.lt.q, aab0, aab1, lane, &y0, &y1);
+  if (lane < NV) { st[0].y[lane] = y0; st[1].y[lane] = y1; }
+  wsync();
+  const float asb0 = lane < NV ? aab0 - kH * cKv[lane] * y0 : 0.f, asb1 = lane < NV ? aab1 - kH * cKv[lane] * y1 : 0.f;
+  float l0, l1;
+  ltl_solve2(s.lt.h, asb0, asb1, lane, &l0, &l1);
+  if (lane < NV) { st[0].lam[lane] = l0; st[1].lam[lane] = l1; }
+  wsync();
+}
+
 // chain twists of v, lambda, y, a*, a~ and the RNE acceleration (gravity, S a*, V_c(d) x S_d v_d) per body.
 // The twist of a dof vector x is T[b] = T[parent(b)] + S_d x_d down the tree (d = b + 4, a hinge body's one dof)
 // from the root body's T[1] = (sum_k S_{3+k}.w x_{3+k}; x_0..2) (S_0..2 = (0; e_k), S_3..5 = (w_k; 0)): a column per
@@ -670,21 +696,24 @@ __device__ __forceinline__ void adj_twists_cot(Adj& s, int lane) {
 // integrator's VJP, the solves, the twists of lambda and y, then the limit rows, the contacts (replayed from the
 // record's contact table), the per-body wrench sums, body forces and subtree sums, and the dof terms. COT alone needs
 // the factors' copies issued (load_factors) after the last COT pass, which overwrote them; recopied: they were, so
-// L_Q's frame slots are set to 0 again before the solves.
-template <bool STATE, bool COT>
+// L_Q's frame slots are set to 0 again before the solves. SOLVED (COT alone): the caller ran the integrator's VJP and
+// the solves (s.vt, s.qn, s.y, s.lam in place), so the pass starts at the twists. (The phases after the twists stay
+// in this body: as a function of their own they were optimized before inlining and k_adjoint grew by 69 v_movs.)
+template <bool STATE, bool COT, bool SOLVED = false>
 __device__ void adj_substep(Adj& s, const float* __restrict__ rec, int lane, int clamp_kv, int normal,
                             float clamp_soft, bool recopied = false) {
+  static_assert(!(SOLVED && STATE), "SOLVED is a cotangent pass alone");
   if (STATE) {
     adj_record(s, rec, lane);
     APROF(AP_RECORD);
     adj_poses(s, lane);
   }
-  if (COT)
+  if (COT && !SOLVED)
     adj_integrator(s, lane);
   else
     wsync();
   APROF(AP_POSES);
-  if (COT) {
+  if (COT && !SOLVED) {
     adj_solves(s, lane, recopied);
     APROF(AP_SOLVE);
   }
@@ -1100,6 +1129,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     float clamp_soft, int clamp_kv, int normal, const int* __restrict__ perm, unsigned long long* __restrict__ diag,
     int ncot, int per) {
   __shared__ Adj s;
+  __shared__ SetStage st[SET_CHUNK];
   const int lane = threadIdx.x;
   const int ngrp = (ncot + per - 1) / per;
   if ((int)blockIdx.x >= nw * ngrp) return;
@@ -1127,45 +1157,66 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const float* rec = wt + (size_t)k * REC_WORDS;
     adj_substep<true, false>(s, rec, lane, clamp_kv, normal, clamp_soft);
 #pragma unroll 1
-    for (int c = c0; c < c1; c++) {
-      const size_t wr = (size_t)c * nw + w;
-      float* oq = gq_in + wr * NQ;
-      float* ov = gv_in + wr * NV;
-      float* ou = gctrl + wr * NU;
-      if (c > c0) load_factors(s, rec, lane);  // the first set's copies came with the record
-      if (k == nsub - 1) {  // the set's output cotangents in the tangent space at the output state
-        const float igv = gv_out[wr * NV + lv], igq = gq_out[wr * NQ + lqo];
-        bool cbad = false;  // with the counters: a non-finite entry in the output cotangents
-        if (diag) {
-          const float icq = gq_out[wr * NQ + min(lane, NQ - 1)];
-          cbad = ballot(!(__builtin_isfinite(icq) && __builtin_isfinite(igv))) != 0ull;
+    for (int cc = c0; cc < c1; cc += SET_CHUNK) {
+      const int nc = min(SET_CHUNK, c1 - cc);
+      // each set's running cotangent and the integrator's VJP, staged
+#pragma unroll 1
+      for (int q = 0; q < nc; q++) {
+        const int c = cc + q;
+        const size_t wr = (size_t)c * nw + w;
+        if (k == nsub - 1) {  // the set's output cotangents in the tangent space at the output state
+          const float igv = gv_out[wr * NV + lv], igq = gq_out[wr * NQ + lqo];
+          bool cbad = false;  // with the counters: a non-finite entry in the output cotangents
+          if (diag) {
+            const float icq = gq_out[wr * NQ + min(lane, NQ - 1)];
+            cbad = ballot(!(__builtin_isfinite(icq) && __builtin_isfinite(igv))) != 0ull;
+          }
+          if (lane < NU) s.ub[lane] = 0.f;
+          if (lane < NV) s.vb[lane] = igv;
+          if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = igq;
+          if (lane == 0) {
+            info[wr] = cbad ? NONFINITE_COT << NONFINITE_SHIFT : 0;
+            seed_rotation(s, s.qvel, s.aadv, s.qpos, gq_out + wr * NQ + 3);  // s holds the last record
+          }
+        } else {
+          const float rq = gq_in[wr * NQ + lqs], rv = gv_in[wr * NV + lv], ru = gctrl[wr * NU + lu];
+          if (lane < NV) { s.qb[lane] = rq; s.vb[lane] = rv; }
+          if (lane < NU) s.ub[lane] = ru;
         }
-        if (lane < NU) s.ub[lane] = 0.f;
-        if (lane < NV) s.vb[lane] = igv;
-        if (lane < NV && (lane < 3 || lane >= 6)) s.qb[lane] = igq;
-        if (lane == 0) {
-          info[wr] = cbad ? NONFINITE_COT << NONFINITE_SHIFT : 0;
-          seed_rotation(s, s.qvel, s.aadv, s.qpos, gq_out + wr * NQ + 3);  // s holds the last record
-        }
-      } else {
-        const float rq = oq[lqs], rv = ov[lv], ru = ou[lu];
-        if (lane < NV) { s.qb[lane] = rq; s.vb[lane] = rv; }
-        if (lane < NU) s.ub[lane] = ru;
+        wsync();
+        adj_integrator(s, lane);
+        if (lane < NV) { st[q].vt[lane] = s.vt[lane]; st[q].qn[lane] = s.qn[lane]; }
+        if (lane < NU) st[q].ub[lane] = s.ub[lane];
+        wsync();
       }
-      wsync();
-      adj_substep<false, true>(s, rec, lane, clamp_kv, normal, clamp_soft, c > c0);
-      if (k > 0) {
-        if (lane < NV) { oq[lqs] = s.qb[lane]; ov[lane] = s.vb[lane]; }
-        if (lane < NU) ou[lane] = s.ub[lane];
-      } else {  // s holds the first record: its qpos row is the step's input
-        const int nb = adj_emit(s, s.qpos, oq, ov, ou, lane, diag != nullptr);
-        if (lane == 0) {
-          const int f = s.flags | info[wr] | nb << NONFINITE_SHIFT;
-          info[wr] = f;
-          if (diag) adj_count(diag, f, wi == 0, nw);
+      // the sets' solves together: the substep's first chunk on the record's copies of the factors, a later one on a
+      // fresh copy (the previous chunk's tails overwrote them)
+      if (cc > c0) load_factors(s, rec, lane);
+      adj_solves_sets(s, st, nc, lane, cc > c0);
+      // each set's remaining phases
+#pragma unroll 1
+      for (int q = 0; q < nc; q++) {
+        const int c = cc + q;
+        const size_t wr = (size_t)c * nw + w;
+        float* oq = gq_in + wr * NQ;
+        float* ov = gv_in + wr * NV;
+        float* ou = gctrl + wr * NU;
+        if (lane < NV) { s.vt[lane] = st[q].vt[lane]; s.qn[lane] = st[q].qn[lane]; s.y[lane] = st[q].y[lane]; s.lam[lane] = st[q].lam[lane]; }
+        if (lane < NU) s.ub[lane] = st[q].ub[lane];
+        adj_substep<false, true, true>(s, rec, lane, clamp_kv, normal, clamp_soft);
+        if (k > 0) {
+          if (lane < NV) { oq[lqs] = s.qb[lane]; ov[lane] = s.vb[lane]; }
+          if (lane < NU) ou[lane] = s.ub[lane];
+        } else {  // s holds the first record: its qpos row is the step's input
+          const int nb = adj_emit(s, s.qpos, oq, ov, ou, lane, diag != nullptr);
+          if (lane == 0) {
+            const int f = s.flags | info[wr] | nb << NONFINITE_SHIFT;
+            info[wr] = f;
+            if (diag) adj_count(diag, f, wi == 0, nw);
+          }
         }
+        wsync();
       }
-      wsync();
     }
   }
 }

@@ -554,4 +554,43 @@ __device__ __forceinline__ float ltl_solve(const float* Lp, float b, int lane_) 
   return z;
 }
 
+// ltl_solve for two right-hand sides at once (the step Jacobian's cotangent sets): every step's broadcast and FMA
+// for each, the coefficients shared, so each result is bitwise ltl_solve's for its right-hand side; the two chains
+// are independent, so each step's latency is taken once for both
+__device__ __forceinline__ void ltl_solve2(const float* Lp, float b0, float b1, int lane_, float* x0, float* x1) {
+  const int lane = opaque_lane(lane_);
+  const int r = lane < NV ? lane : NV - 1;
+  const float dself = lane < NV ? 1.f / Lp[tri(r, r)] : 0.f;
+  float z0 = b0 * dself, z1 = b1 * dself;
+  const float* col = Lp + r;
+  float lv[NV];
+#pragma unroll
+  for (int i = NV - 1; i >= 1; i--) lv[i] = col[tri(i, 0)];
+  __builtin_amdgcn_sched_barrier(0);
+  float dm = dself;
+  static_for<NV - 1, 0, -1>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    dm = zero_lane<i>(dm);
+    const float cf = -(lv[i] * dm);
+    z0 = fmaf(cf, rdl(z0, i), z0);
+    z1 = fmaf(cf, rdl(z1, i), z1);
+  });
+  z0 *= dself;
+  z1 *= dself;
+  const float* row = Lp + tri(r, 0);
+#pragma unroll
+  for (int k = 0; k < NV - 1; k++) lv[k] = row[k];
+  __builtin_amdgcn_sched_barrier(0);
+  dm = dself;
+  static_for<0, NV - 1, 1>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    dm = zero_lane<k>(dm);
+    const float cf = -(lv[k] * dm);
+    z0 = fmaf(cf, rdl(z0, k), z0);
+    z1 = fmaf(cf, rdl(z1, k), z1);
+  });
+  *x0 = z0;
+  *x1 = z1;
+}
+
 }  // namespace g1k
