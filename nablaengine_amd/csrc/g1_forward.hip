@@ -1115,8 +1115,14 @@ __device__ __forceinline__ void substep(Sim& s, int lane_, int iterations, float
 // clock) times the substeps left, one level per PRIO_STEP. The longest remaining work goes first, as the dispatch
 // order's heaviest-first does at launch: a world whose cost the launch's estimate missed (a self contact appearing
 // within the step, more Newton iterations) catches up on its co-resident light world instead of finishing last.
-// 4e5 cycles (about 1.4 mean substeps) was the best of 2e5 .. 1e6 at 4096 worlds.
+// 4e5 cycles (about two mean substeps) was the best of 2e5 .. 1e6 at 4096 worlds, and 3e5 .. 4e5 again on the later
+// build with PRIO_START.
 constexpr float PRIO_STEP = 4e5f;
+// A world's level for its first substep, before it has a rate of its own: a world dispatched into the launch's second
+// round then has all its substeps left (at the mean rate about 2 PRIO_STEP), where its co-resident wave has part of
+// one world left. Starting at level 0 held it behind that wave for a substep: 1.5% slower forward at 4096 worlds than
+// starting at 1, 2 or 3, which measured alike.
+constexpr int PRIO_START = 2;
 __device__ __forceinline__ void set_priority_by_remaining(unsigned long long t_start, int k, int nsub) {
   const float rem = (float)(__builtin_amdgcn_s_memtime() - t_start) * (float)(nsub - k) / (float)k;
   if (rem > 3.f * PRIO_STEP) __builtin_amdgcn_s_setprio(3);
@@ -1163,6 +1169,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const unsigned long long t_start = __builtin_amdgcn_s_memtime();
   for (int k = 0; k < nsub; k++) {
     if (k > 0) set_priority_by_remaining(t_start, k, nsub);
+    else __builtin_amdgcn_s_setprio(PRIO_START);
     substep(s, lane, iterations, tape ? tape + ((size_t)w * nsub + k) * REC_WORDS : nullptr,
             ocon && k == nsub - 1 ? ocon + (size_t)w * MAXCON * 8 : nullptr);
   }
