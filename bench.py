@@ -1,8 +1,8 @@
 """Benchmark of the MI355X G1 control step (BASELINE.json metric): ms per 20 ms control step and world-steps/s, forward
 and forward+VJP, at 4096 worlds (and 16384), on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu] [--no-16k] [--no-configs]
-                    [--no-corpus] [--no-rounds]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--worlds 4096] [--no-cpu] [--no-16k] [--no-small]
+                    [--no-configs] [--no-corpus] [--no-rounds]
 
 A step is one control step (4 substeps of 5 ms, Newton 10 iterations) of B worlds of BASELINE config 1 (seeded
 synthetic states, inputs resident in HBM before the timed region), exactly what torch_ffi.forward runs: the dispatch
@@ -14,8 +14,9 @@ way.
 `rounds` restates the reference's timing protocol (scripts/paper_bench/common.py:1-10,154-187): a warm-up of at least
 5 calls and 1 s, then 6 rounds of n back-to-back calls with one synchronization each (n chosen so that a round lasts
 about 0.25 s, at most 200 calls), round 0 dropped; ms per call median / p10 / p90 / min / max over the 5 kept rounds.
-It covers the forward and forward+VJP at 4096 and 16384 synthetic worlds and at the 4096 states of the reference's
-corpus mf_s0 (`corpus_mf_s0`: the inputs its published 1.214 / 1.784 ms are measured on,
+It covers the forward and forward+VJP at 4096 and 16384 synthetic worlds (and at 512 and 1024: `worlds_512`,
+`worlds_1024`, the other batch sizes the reference publishes, docs/results/paper_rtx6000/paper_bench.md:80-81, whose
+numbers each of these entries carries) and at the 4096 states of the reference's corpus mf_s0 (`corpus_mf_s0`: the inputs its published 1.214 / 1.784 ms are measured on,
 docs/results/paper_rtx6000/paper_bench.md:91-92; a committed fixture, tests/golden/corpus_mf_s0.npz).
 
 Also reported: config 3 (`config3_jacobian`: full 71 x 99 step Jacobians of the 4096 worlds from one taped forward
@@ -48,6 +49,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# the reference's published ms per step (forward, fwd+VJP) on an RTX PRO 6000 Blackwell at each batch size,
+# docs/results/paper_rtx6000/paper_bench.md:80-81
+REF_RTX6000_MS = {512: {"forward": 0.609, "fwd_vjp": 0.797}, 1024: {"forward": 0.723, "fwd_vjp": 0.943},
+                  4096: {"forward": 1.201, "fwd_vjp": 1.783}, 16384: {"forward": 3.962, "fwd_vjp": 5.938}}
 METRIC = "ms per 20 ms control step @4096 worlds, forward and fwd+VJP; world-steps/s"
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
@@ -343,6 +348,7 @@ def main():
     ap.add_argument("--worlds", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-16k", action="store_true", help="skip the 16384-world forward and fwd+VJP lines")
+    ap.add_argument("--no-small", action="store_true", help="skip the 512- and 1024-world forward and fwd+VJP lines")
     ap.add_argument("--no-configs", action="store_true", help="skip the config 3 (Jacobian) and 4 (BPTT) lines")
     ap.add_argument("--no-corpus", action="store_true", help="skip the mf_s0 corpus line")
     ap.add_argument("--no-rounds", action="store_true", help="skip the round-protocol statistics")
@@ -372,9 +378,21 @@ def main():
         bms, bvjp, _, _, binfo, brs = measure(16384, max(a.steps // 4, 3), max(a.warmup // 4, 2),
                                               rounds=not a.no_rounds)
         big = {"worlds": 16384, "ms_per_step": bms, "ms_per_step_fwd_vjp": bvjp,
-               "world_steps_per_s": 16384e3 / bms, "world_steps_per_s_fwd_vjp": 16384e3 / bvjp}
+               "world_steps_per_s": 16384e3 / bms, "world_steps_per_s_fwd_vjp": 16384e3 / bvjp,
+               "reference_rtx_pro_6000_ms": REF_RTX6000_MS[16384]}
         if brs:
             big["rounds"] = brs
+    small = {}
+    if not a.no_small:
+        for b in (512, 1024):
+            if b == B:
+                continue
+            sms, svjp, _, _, _, srs = measure(b, a.steps, a.warmup, rounds=not a.no_rounds)
+            small[b] = {"worlds": b, "ms_per_step": sms, "ms_per_step_fwd_vjp": svjp,
+                        "world_steps_per_s": b * 1e3 / sms, "world_steps_per_s_fwd_vjp": b * 1e3 / svjp,
+                        "reference_rtx_pro_6000_ms": REF_RTX6000_MS[b]}
+            if srs:
+                small[b]["rounds"] = srs
     st = synthetic.states(B, config=1)
     sub = {k: v[: a.flop_sample] for k, v in st.items()}
     fl = algorithmic_flops(sub)
@@ -423,6 +441,8 @@ def main():
                                           "6 rounds of n calls (one synchronization each), round 0 dropped")
     if big:
         res["worlds_16384"] = big
+    for b, v in small.items():
+        res[f"worlds_{b}"] = v
     if not a.no_corpus and os.path.exists(CORPUS):
         res["corpus_mf_s0"] = measure_corpus()
     if not a.no_configs:

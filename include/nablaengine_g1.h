@@ -16,7 +16,9 @@ extern "C" {
  * substep, contacts found, constraint rows, flags: 4 contacts beyond 64 dropped, 16 rows beyond 192 dropped);
  * ocon (nw, 64, 8) or NULL: the last substep's contacts (pair, dist, pos[3], normal[3]; pair -1 past the count);
  * tape (nw, nsub * DK_REC_WORDS) or NULL: the adjoint's record (its flags word as the reference's: 4 / 16
- * overflow, 1 << 8 refactored at the final zones, 1 << 9 not converged, 1 << 10 near-singular self contact); work: dk_fwd_work_bytes(nw) bytes or NULL when 0. */
+ * overflow, 1 << 8 refactored at the final zones, 1 << 9 not converged, 1 << 10 near-singular self contact); work:
+ * dk_fwd_work_bytes(nw) bytes or NULL when 0, for the dispatch order (heaviest worlds first), which is skipped, and work
+ * left unwritten, when the GPU holds all nw worlds at once (8 per CU): every world then starts at the launch. */
 int dk_fwd_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
                    int* info, float* ocon, float* tape, void* work);
@@ -115,7 +117,8 @@ int dk_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float*
 
 /* No counterpart in the reference's ABI (its adjoint entries take no work buffer): dk_adjoint with a work buffer of
  * dk_adjoint_work_bytes(nw) bytes, in which the worlds are ordered heaviest first (the tape's contacts) before the
- * launch. Same results as dk_adjoint, which is this entry with work = NULL. */
+ * launch, unless the GPU holds all nw worlds at once (8 per CU: index order, work left unwritten). Same results as
+ * dk_adjoint, which is this entry with work = NULL. */
 int dk_adjoint_work(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,
                     const float* gq_out, const float* gv_out, float* gq_in, float* gv_in, float* gctrl, int* info,
                     const float* ctrl, float clamp_soft, int clamp_kv, int normal, void* work);

@@ -1222,6 +1222,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 }
 
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
+int resident_worlds();
 
 // k_adjoint_sets' sets per workgroup: all of a world's sets in one workgroup (one record phase per substep) once nw
 // alone makes G1_SETS_WAVES waves, else groups small enough that nw x groups does. Of 2048 resident waves (2 per SIMD
@@ -1241,6 +1242,8 @@ int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const fl
   if (nw <= 0) return 0;
   if (reinterpret_cast<uintptr_t>(tape) & 15u) return (int)hipErrorInvalidValue;  // 16-byte copies of the factors
   const int* perm = nullptr;
+  // one set of a batch that fits the resident slots at once: every world starts at the launch, index order
+  if (order == 1 && ncot == 1 && nw <= resident_worlds()) order = 0;
   if (work && order) {  // the dispatch order, heaviest worlds first (order 1: computed here; 2: already in work)
     if (order == 1) {
       const int rc = launch_order_adj(st, nw, nsub, tape, work);

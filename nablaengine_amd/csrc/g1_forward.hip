@@ -1208,13 +1208,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 namespace g1k {
 int launch_order_fwd(hipStream_t st, int nw, const float* qpos, void* work);
-// order: 0 index order (work unused), 1 compute the order into work first, 2 the order already in work; diag: the
+int resident_worlds();
+// order: 0 index order (work unused), 1 compute the order into work first (index order when the batch fits the
+// GPU's resident slots at once: the order cannot change the makespan there), 2 the order already in work; diag: the
 // diagnostic counters added to by each world at its end, or NULL
 int launch_forward(hipStream_t st, int nw, const float* qpos, const float* qvel, const float* warm, const float* ctrl,
                    const float* fric, const float* com, int iterations, int nsub, float* oq, float* ov, float* ow,
                    int* info, float* ocon, float* tape, void* work, int order, unsigned long long* diag) {
   if (nw <= 0) return 0;
   const int* perm = nullptr;
+  if (order == 1 && nw <= resident_worlds()) order = 0;
   if (work && order) {  // the dispatch order, heaviest worlds first
     if (order == 1) {
       const int rc = launch_order_fwd(st, nw, qpos, work);

@@ -14,6 +14,10 @@
 // Then one workgroup buckets the costs (LDS histogram, descending prefix) into the permutation the main kernel reads
 // as blockIdx.x -> world. Results do not depend on the order: every world's computation is the same wherever and
 // whenever it runs, so the permutation only moves work in time (its order inside a bucket is free).
+//
+// A batch that fits the GPU's resident slots at once (8 worlds per CU in both kernels) starts every world at the
+// launch: no world waits for a slot, so the order cannot shorten the makespan, and the order's two launches are
+// skipped (index order).
 #include "g1_device.h"
 #include "g1_collide.h"
 #include "g1_tape.h"
@@ -21,6 +25,21 @@
 namespace g1k {
 
 constexpr int NBKT = COST_BUCKETS;
+
+// worlds resident at once on the current device: 8 per CU (the forward's and the adjoint's LDS and VGPRs), the CU
+// count queried once per device; 0 when the query fails (the order is then always computed)
+constexpr int WORLDS_PER_CU = 8, MAX_DEVICES = 64;
+int resident_worlds() {
+  static int per_dev[MAX_DEVICES];  // 0: not queried yet
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 0;
+  if (per_dev[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+    per_dev[dev] = WORLDS_PER_CU * cus;
+  }
+  return per_dev[dev];
+}
 
 // contacts at the input state: FK of body poses (each body lane walks its chain from the root), geom poses, the main
 // kernel's broadphase and narrowphase (the same code); the cost counts the contacts' constraint rows (4 per pyramid

@@ -370,14 +370,20 @@ def test_capsule_both_free_vjp(ffi):
         assert np.median(e) <= 1e-4 and np.percentile(e, 90) <= 1e-3 and e.max() <= 1e-2
 
 
+def _resident_worlds():
+    """worlds resident at once on device 0 (8 per CU in both kernels): batches up to this size run in index order"""
+    import torch
+    return 8 * torch.cuda.get_device_properties(0).multi_processor_count
+
+
 def test_dispatch_order_does_not_change_results(ffi):
     """The C entries with a work buffer dispatch the worlds heaviest first; without one (NULL) in index order. The
     outputs, the tape and the gradients are bitwise the same both ways (contact-heavy config-4 states, where the
-    order moves the most)."""
+    order moves the most; more worlds than the GPU holds at once, so that the order is computed)."""
     import ctypes
     import torch
     lib = ffi.load_library()
-    B = 1536
+    B = _resident_worlds() + 512
     st = synthetic.states(B, config=4)
     cq, cv = synthetic.cotangents(B)
     args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
@@ -404,3 +410,37 @@ def test_dispatch_order_does_not_change_results(ffi):
         assert torch.equal(x, y)
     perm = work.view(torch.int32)[:B].cpu().numpy()
     assert np.array_equal(np.sort(perm), np.arange(B))  # a permutation of the worlds
+
+
+def test_resident_batch_runs_in_index_order(ffi):
+    """A batch the GPU holds at once starts every world at the launch, so the forward and the one-set adjoint skip the
+    dispatch order: the work buffer is left as it was, and the results are bitwise those of an ordered launch of the
+    same worlds (dk_fwd_order, then dk_fwd_forward_ordered)."""
+    import ctypes
+    import torch
+    lib = ffi.load_library()
+    B = 1000
+    assert B <= _resident_worlds()
+    st = synthetic.states(B, config=4, seed=7)
+    args = [_t(st[k]) for k in ("qpos", "qvel", "warm", "ctrl", "friction", "com")]
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    kw = dict(dtype=torch.float32, device="cuda")
+    outs = []
+    for ordered in (False, True):
+        q1, v1, w1 = torch.empty((B, 36), **kw), torch.empty((B, 35), **kw), torch.empty((B, 35), **kw)
+        info = torch.empty((B, 4), dtype=torch.int32, device="cuda")
+        work = torch.full((int(lib.dk_fwd_work_bytes(B)),), 0xA5, dtype=torch.uint8, device="cuda")
+        if ordered:
+            assert lib.dk_fwd_order(stream, B, p(args[0]), p(work)) == 0
+            assert lib.dk_fwd_forward_ordered(stream, B, *map(p, args), 10, 4, p(q1), p(v1), p(w1), p(info), None,
+                                              None, p(work)) == 0
+        else:
+            assert lib.dk_fwd_forward(stream, B, *map(p, args), 10, 4, p(q1), p(v1), p(w1), p(info), None, None,
+                                      p(work)) == 0
+        torch.cuda.synchronize()
+        if not ordered:
+            assert bool((work == 0xA5).all()), "the forward wrote a dispatch order for a resident batch"
+        outs.append((q1, v1, w1, info))
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)
