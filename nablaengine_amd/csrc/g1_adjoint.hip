@@ -1224,15 +1224,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 int launch_order_adj(hipStream_t st, int nw, int nsub, const float* tape, void* work);
 int resident_worlds();
 
-// k_adjoint_sets' sets per workgroup: all of a world's sets in one workgroup (one record phase per substep) once nw
-// alone makes G1_SETS_WAVES waves, else groups small enough that nw x groups does. Of 2048 resident waves (2 per SIMD
-// on 256 CUs), 16384 makes 8 rounds: the launch's tail is a few sets long, and the record phases repeated per group
-// cost under 2% (measured at 1024, 4096 and 16384 worlds with 4096 to 32768 waves: 16384 within 1% of the best)
+// k_adjoint_sets' sets per workgroup: groups small enough that nw x groups makes G1_SETS_WAVES waves, and at least
+// two groups (a workgroup of all of a world's sets is a long wave, whose tail shows at 16384 worlds: 1.3% there).
+// Of 2048 resident waves (2 per SIMD on 256 CUs), 16384 makes 8 rounds: the launch's tail is a few sets long, and the
+// record phases repeated per group cost under 2% (measured at 1024, 4096 and 16384 worlds with 4096 to 32768 waves:
+// 16384 the best at 4096 worlds and within 0.5% at 1024)
 #ifndef G1_SETS_WAVES
 #define G1_SETS_WAVES 16384
 #endif
 int sets_per_group(int nw, int ncot) {
-  const long long ngrp = std::min<long long>(ncot, std::max<long long>(1, (G1_SETS_WAVES + nw - 1) / nw));
+  const long long ngrp = std::min<long long>(ncot, std::max<long long>(2, (G1_SETS_WAVES + nw - 1) / nw));
   return (int)((ncot + ngrp - 1) / ngrp);
 }
 int launch_adjoint(hipStream_t st, int nw, int nsub, const float* tape, const float* fric, const float* com,

@@ -125,7 +125,7 @@ def test_jacobian_rows_are_the_backward_vjps(ffi, heavy, kv, n, soft):
 
 @pytest.mark.parametrize("B,substeps", [(16384, 4), (4096, 2), (1, 4), (301, 1)])
 def test_jacobian_rows_at_every_grouping(ffi, B, substeps):
-    """The many-cotangent adjoint runs a world's sets in workgroups of a size set by the batch (all 71 in one at 16384
+    """The many-cotangent adjoint runs a world's sets in workgroups of a size set by the batch (36 and 35 at 16384
     worlds, 18 at 4096, 2 at 301 with a last group of one, one each for a single world) and keeps each set's running
     cotangent in its output rows between substeps. At each grouping, and with one substep (the seed and the gradients
     in one pass), every checked row is bitwise backward()'s VJP and info is the forward's."""
@@ -149,7 +149,7 @@ def test_jacobian_rows_at_every_grouping(ffi, B, substeps):
 def test_vjp_sets_are_the_backward_calls(ffi, B, substeps):
     """Nine random cotangent sets in one many-cotangent launch against nine backward() calls, with the counters on:
     the qpos-form, qvel and ctrl gradients and the info words bitwise equal, for a set whose cotangent holds a NaN
-    too (its non-finite bits, NONFINITE_COT among them, the same), at groupings of 9, 3 and 1 sets per workgroup and
+    too (its non-finite bits, NONFINITE_COT among them, the same), at groupings of 5 and 4, 3, and 1 set per workgroup and
     at 1, 3 and 4 substeps; the counters count nine backward calls."""
     import torch
     st = synthetic.states(B, config=4, seed=3 + B)
