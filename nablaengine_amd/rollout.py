@@ -53,9 +53,9 @@ def jacobian(qpos, qvel, warm, ctrl, friction, com, *, iterations=torch_ffi.ITER
 def rollout(qpos, qvel, warm, ctrls, friction, com, *, checkpoint_every=8, **step_kw):
     """T = len(ctrls) differentiable steps from (qpos, qvel, warm) with the controls ctrls (T, B, 29): the states
     [(qpos_t, qvel_t)] for t = 1..T. With checkpoint_every = k > 0 each segment of k steps but the last runs once
-    without keeping its tapes and again in the backward (the forward is deterministic: the recomputed tapes are
-    bitwise the first ones); the last segment keeps its tapes, as torch's checkpoint_sequential does, since the
-    backward would recompute it first thing. k = 0 keeps every tape."""
+    without writing its tapes and again in the backward, which writes them (the forward is deterministic: the
+    recomputed steps are bitwise the first ones); the last segment keeps its tapes, as torch's checkpoint_sequential
+    does, since the backward would recompute it first thing. k = 0 keeps every tape."""
     import torch
     from torch.utils.checkpoint import checkpoint
     T = len(ctrls)
@@ -69,11 +69,24 @@ def rollout(qpos, qvel, warm, ctrls, friction, com, *, checkpoint_every=8, **ste
             states += [q, v]
         return (w,) + tuple(states)
 
+    def first_pass_untaped():
+        """segment for checkpoint(): its first call (the forward pass, whose saved tensors the checkpoint drops) runs
+        the steps without writing tapes; the recomputation in the backward writes them"""
+        calls = [0]
+
+        def run(*xs):
+            calls[0] += 1
+            if calls[0] == 1:
+                with torch_ffi._TapeUnread():
+                    return segment(*xs)
+            return segment(*xs)
+        return run
+
     k = checkpoint_every if checkpoint_every and checkpoint_every > 0 else T
     for t0 in range(0, T, k):
         us = tuple(ctrls[t] for t in range(t0, min(T, t0 + k)))
         if checkpoint_every and t0 + k < T:
-            r = checkpoint(segment, q, v, w, *us, use_reentrant=False)
+            r = checkpoint(first_pass_untaped(), q, v, w, *us, use_reentrant=False)
         else:
             r = segment(q, v, w, *us)
         w = r[0]

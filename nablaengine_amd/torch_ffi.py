@@ -480,6 +480,22 @@ class _StepOptions(NamedTuple):
     kinematics: bool
 
 
+# Set (per thread) while a checkpointed segment's first pass runs (rollout): torch's non-reentrant checkpoint drops
+# what that pass saves and recomputes it, tapes included, when the backward reaches the segment.
+_tape_unread = threading.local()
+
+
+class _TapeUnread:
+    """The steps inside skip writing their tapes: each saves an unwritten tensor of the tape's shape in its place
+    (the checkpoint compares the recomputed saved tensors' shapes with these), which nothing reads."""
+
+    def __enter__(self):
+        _tape_unread.depth = getattr(_tape_unread, "depth", 0) + 1
+
+    def __exit__(self, *exc):
+        _tape_unread.depth -= 1
+
+
 class _StepFunction(torch.autograd.Function):
     """step's autograd node: the forward writes the tape and keeps it with the arrays the adjoint reads; the backward
     runs the adjoint (after the kinematics VJP when cotangents reach the kinematics outputs). Inputs (options, qpos,
@@ -488,8 +504,11 @@ class _StepFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, opts, qpos, qvel, warm, ctrl, friction, com):
+        taped = getattr(_tape_unread, "depth", 0) == 0
         q1, v1, w1, _info, tape, *kin = _ops().forward(qpos, qvel, warm, ctrl, friction, com, opts.iterations,
-                                                    opts.substeps, True, opts.kinematics)
+                                                    opts.substeps, taped, opts.kinematics)
+        if not taped:
+            tape = torch.empty((qpos.shape[0], opts.substeps * rec_words()), dtype=torch.float32, device=qpos.device)
         ctx.opts = opts
         ctx.save_for_backward(tape, friction, com, ctrl, q1, v1)
         ctx.mark_non_differentiable(w1)

@@ -248,11 +248,13 @@ def test_scale_grad_rollout_is_the_manual_chain(ffi):
 
 
 def test_checkpointed_rollout_is_bitwise_the_plain_one(ffi):
-    """A 4-step BPTT rollout on contact-heavy config-4 states: the gradients of a loss on every state with segments
-    of 2 steps recomputed in the backward are bitwise those with every tape kept."""
+    """A 6-step BPTT rollout on contact-heavy config-4 states: the gradients of a loss on every state with segments
+    of 2 steps (the first two recomputed in the backward, their first pass writing no tapes; the last keeping its
+    tapes) are bitwise those with every tape kept, and so are those of a second backward through the same graph
+    (retain_graph: each checkpointed segment recomputed again)."""
     import torch
     from nablaengine_amd import rollout
-    B, T = 256, 4
+    B, T = 256, 6
     st = synthetic.states(B, config=4)
     us = _t(synthetic.ctrl_sequence(T, B))
     grads = []
@@ -262,8 +264,13 @@ def test_checkpointed_rollout_is_bitwise_the_plain_one(ffi):
         u = us.clone().requires_grad_(True)
         states = rollout.rollout(q, v, _t(st["warm"]), u, _t(st["friction"]), _t(st["com"]), checkpoint_every=k)
         loss = sum((qt[:, 2] ** 2).sum() + 0.01 * (vt ** 2).sum() for qt, vt in states)
+        loss.backward(retain_graph=True)
+        first = (q.grad.clone(), v.grad.clone(), u.grad.clone())
+        q.grad = v.grad = u.grad = None
         loss.backward()
+        grads.append(first)
         grads.append((q.grad, v.grad, u.grad))
     torch.cuda.synchronize()
-    for a, b in zip(*grads):
-        assert torch.isfinite(a).all() and torch.equal(a, b)
+    for g in grads[1:]:
+        for a, b in zip(grads[0], g):
+            assert torch.isfinite(a).all() and torch.equal(a, b)
