@@ -6,8 +6,9 @@ torch_ffi.py module docstring for rollouts with torch.utils.checkpoint):
          qvel' 35), columns the inputs (qpos tangent 35, qvel 35, ctrl 29), from one taped forward and 71 one-hot
          VJPs on that tape (the reference's method), the adjoint's dispatch order computed once for the 71;
   rollout(qpos, qvel, warm, ctrls, friction, com, *, checkpoint_every=8, **step_kw) -> [(qpos_t, qvel_t)]: T steps
-      under autograd, each segment of checkpoint_every steps recomputed in the backward (torch.utils.checkpoint):
-      only the segment being differentiated holds its tapes.
+      under autograd, each segment of checkpoint_every steps but the last recomputed in the backward
+      (torch.utils.checkpoint; their first pass writes no tapes): only the segment being differentiated and the last
+      one hold tapes.
 
 qpos tangent: a qpos-form cotangent g (36) of a state with root quaternion q maps to the tangent of
 integrate_pos(q, dq) at dq = 0 (position 3, the local rotation vector 3 as 1/2 vec(q* (x) g_q), hinges 29).
