@@ -173,8 +173,8 @@ def test_taped_factors_vs_oracle(ffi, config):
     for w in range(B):
         warm = st["warm"][w].astype(np.float64)
         for k in range(4):
-            rec = tape[w, k].astype(np.float64)
-            q, v = rec[REC_QPOS:REC_QPOS + 36], rec[REC_QVEL:REC_QVEL + 35]
+            rec = tape[w, k]  # float32 words; the bit-cast integer fields are never converted
+            q, v = rec[REC_QPOS:REC_QPOS + 36].astype(np.float64), rec[REC_QVEL:REC_QVEL + 35].astype(np.float64)
             u, f, c = st["ctrl"][w].astype(np.float64), float(st["friction"][w]), st["com"][w].astype(np.float64)
             M, H = oracle.substep_hessian(q, v, warm, u, f, c)
             LQ, LH = _unpack(rec[REC_LQ:]) * pattern, _unpack(rec[REC_LH:])  # L_Q's other positions: frames
@@ -182,7 +182,7 @@ def test_taped_factors_vs_oracle(ffi, config):
             eq.append(np.abs(LQ - ref).max() / np.abs(ref).max())
             if not flags[w, k] & (4 | 16 | (1 << 9)):
                 eh.append(np.abs(LH.T @ LH - H).max() / np.abs(H).max())
-            warm = rec[REC_ASTAR:REC_ASTAR + 35]
+            warm = rec[REC_ASTAR:REC_ASTAR + 35].astype(np.float64)
     eq, eh = np.array(eq), np.array(eh)
     print(f"config {config}: L_Q vs float64 ({len(eq)} records) median {np.median(eq):.3g} max {eq.max():.3g}; "
           f"L_H'L_H vs float64 H ({len(eh)} records) median {np.median(eh):.3g} p95 {np.percentile(eh, 95):.3g} "
