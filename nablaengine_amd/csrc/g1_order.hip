@@ -18,6 +18,8 @@
 // A batch that fits the GPU's resident slots at once (8 worlds per CU in both kernels) starts every world at the
 // launch: no world waits for a slot, so the order cannot shorten the makespan, and the order's two launches are
 // skipped (index order).
+#include <atomic>
+
 #include "g1_device.h"
 #include "g1_collide.h"
 #include "g1_tape.h"
@@ -27,18 +29,21 @@ namespace g1k {
 constexpr int NBKT = COST_BUCKETS;
 
 // worlds resident at once on the current device: 8 per CU (the forward's and the adjoint's LDS and VGPRs), the CU
-// count queried once per device; 0 when the query fails (the order is then always computed)
+// count queried once per device (host threads may race to store the same value: atomics); 0 when the query fails
+// (the order is then always computed)
 constexpr int WORLDS_PER_CU = 8, MAX_DEVICES = 64;
 int resident_worlds() {
-  static int per_dev[MAX_DEVICES];  // 0: not queried yet
+  static std::atomic<int> per_dev[MAX_DEVICES];  // 0: not queried yet
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 0;
-  if (per_dev[dev] == 0) {
+  int n = per_dev[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
-    per_dev[dev] = WORLDS_PER_CU * cus;
+    n = WORLDS_PER_CU * cus;
+    per_dev[dev].store(n, std::memory_order_relaxed);
   }
-  return per_dev[dev];
+  return n;
 }
 
 // contacts at the input state: FK of body poses (each body lane walks its chain from the root), geom poses, the main
